@@ -1,0 +1,254 @@
+/*
+ * momij_hip.h -- C ABI of the MI355X (gfx950) speculative-decode verify step.
+ *
+ * Plain C: device pointers are `void*` / typed scalars, sizes are ints.  No HIP or torch types
+ * cross this boundary.  Every call is asynchronous on the context's stream unless it says it
+ * synchronises; a context is not re-entrant (the reference engine is single-request too,
+ * README.md:32, Server.swift:677-700); distinct contexts may be driven from distinct threads.
+ * The caller owns every tensor it allocates (weights, activations, outputs); the library owns
+ * only its scratch and, for a model, the KV cache.
+ *
+ * Reference paths below are relative to penta2himajin/momij, swift/Sources/MomijCore/.
+ * Tensor layouts follow MLX (WeightStore.swift:48-92): 2-bit affine weights as uint32 words
+ * packing 16 codes LSB-first, [rows][K/16]; fp16 scales and biases [rows][K/gs]; up||gate
+ * packed with the up rows first.
+ */
+#ifndef MOMIJ_HIP_H
+#define MOMIJ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MJ_ABI_VERSION 1
+#define MJ_MAX_ROWS 64 /* verify rows per pass (draft tree nodes + 1), prefill chunk */
+
+/* Errors -- SeedlessError {noMetal, notReady, unsupportedShape(N,K,gs)}
+ * (SeedlessMetal.swift:3718-3728) plus argument, abort, capacity and runtime failures.
+ * mj_last_error() gives the message (shape errors carry N, K and gs). */
+typedef enum mj_status {
+    MJ_OK = 0,
+    MJ_NO_DEVICE = 1,          /* no gfx950 device (noMetal) */
+    MJ_NOT_READY = 2,          /* library / model not initialised (notReady) */
+    MJ_UNSUPPORTED_SHAPE = 3,  /* unsupportedShape(N:K:gs:) */
+    MJ_INVALID_ARG = 4,        /* null pointer, bad index, bad tree */
+    MJ_ABORTED = 5,            /* abort word set (stopBuf, SeedlessMetal.swift:60, 69-70) */
+    MJ_HIP_ERROR = 6,          /* HIP runtime failure */
+    MJ_CAPACITY = 7            /* KV capacity / prompt too long (SeedlessAttn.swift:279-286) */
+} mj_status;
+
+typedef struct mj_ctx mj_ctx;
+typedef struct mj_model mj_model;
+
+/* ---------------------------------------------------------------- context ---- */
+/* SeedlessMetal.ensureCompiled (SeedlessMetal.swift:63-104): device, queue, stop buffer. */
+mj_status mj_init(int device, mj_ctx** out);
+mj_status mj_destroy(mj_ctx* ctx);
+const char* mj_last_error(const mj_ctx* ctx);
+const char* mj_status_str(mj_status s);
+int mj_abi_version(void);
+/* Use an external hipStream_t (e.g. the caller's current stream); NULL restores the own one. */
+mj_status mj_set_stream(mj_ctx* ctx, void* hip_stream);
+void* mj_get_stream(const mj_ctx* ctx);
+/* Device abort word (stopBuf): non-zero makes every kernel of this context return early and
+ * the next synchronising call report MJ_ABORTED.  Cleared with flag = 0. */
+mj_status mj_set_abort(mj_ctx* ctx, int flag);
+/* One wait for everything queued (cb.commit + waitUntilCompleted,
+ * SeedlessDecodeEngine.swift:324-325).  Reports MJ_ABORTED if the abort word was set. */
+mj_status mj_sync(mj_ctx* ctx);
+
+/* ---------------------------------------------------------------- memory ----- */
+mj_status mj_alloc(mj_ctx* ctx, size_t bytes, void** out);
+mj_status mj_free(mj_ctx* ctx, void* p);
+mj_status mj_h2d(mj_ctx* ctx, void* dst, const void* src, size_t bytes);  /* synchronous */
+mj_status mj_d2h(mj_ctx* ctx, void* dst, const void* src, size_t bytes);  /* synchronous */
+
+/* ------------------------------------------------------------------ ops ------ */
+/* 2-bit affine gather-qmv / verify GEMM -- SeedlessMetal.gqmm2 (SeedlessMetal.swift:312-438),
+ * kernel gqmm2_rows (2168-2221):
+ *   y[mk, n] = half( sum_k (s[e,n,k/gs]*q[e,n,k] + b[e,n,k/gs]) * x[row(mk), k] ),
+ *   e = inds[mk], row(mk) = lhs_per_expert ? mk : mk / ktop, mk < M*ktop.
+ * x fp16 [M or M*ktop][K], w uint32 [E][N][K/16], scales/biases fp16 [E][N][K/gs],
+ * inds int32 [M*ktop] (device), y fp16 [M*ktop][N].
+ * Shapes: K % 512 == 0 (as the reference, SeedlessMetal.swift:336-338), N % 16 == 0,
+ * gs in {64, 128}, M*ktop <= MJ_MAX_ROWS*8.
+ * epilogue MJ_EPI_STORE writes y; MJ_EPI_ADD writes y = half(y + half(acc)) (o-proj residual,
+ * gqmm2_rows_fold_add 3488-3543; requires ktop == 1). */
+#define MJ_EPI_STORE 0
+#define MJ_EPI_ADD 1
+mj_status mj_gather_qmm2(mj_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                         const void* biases, const int32_t* inds, void* y, int M, int ktop,
+                         int K, int N, int gs, int lhs_per_expert, int epilogue);
+
+/* MoE expert weights of one layer (MapleMoE.swift:6-33 / SeedlessAttn.swift:93-99). */
+typedef struct mj_moe_weights {
+    const void* norm_w;        /* fp16 [H] post_attention_layernorm (MJ_MOE_PRENORM) */
+    const void* router_w;      /* fp16 [E][H] mlp.gate */
+    const uint32_t* up_gate_w; /* [E][2I][H/16], rows 0..I-1 up, I..2I-1 gate */
+    const void* up_gate_s;     /* fp16 [E][2I][H/gs] */
+    const void* up_gate_b;
+    const uint32_t* down_w;    /* [E][H][I/16] */
+    const void* down_s;        /* fp16 [E][H][I/gs] */
+    const void* down_b;
+    int E, top_k, H, I, gs;
+    float eps;
+} mj_moe_weights;
+
+/* MoE block -- encodeMoEBlock (SeedlessMetal.swift:576-609), MapleMoE.callAsFunction
+ * (MapleMoE.swift:58-80): [rms(x)] -> router logits -> softmax top-k (lowest index on ties,
+ * renormalised) -> up||gate gather -> clamped SwiGLU -> down gather -> score-weighted combine.
+ * flags: MJ_MOE_PRENORM applies norm_w first; MJ_MOE_RESIDUAL writes y = x + moe.
+ * x, y fp16 [M][H] (may alias); out_inds int32 [M][top_k], out_scores fp32 [M][top_k]
+ * (device, nullable).  Rows are bucketed by expert so each routed expert's weights stream
+ * once per call. */
+#define MJ_MOE_PRENORM 1
+#define MJ_MOE_RESIDUAL 2
+mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y, int M,
+                       int flags, int32_t* out_inds, float* out_scores);
+
+/* Attention weights of one layer (SeedlessAttn.swift:74-92). */
+typedef struct mj_attn_weights {
+    const void* norm_w;      /* fp16 [H] input_layernorm */
+    const uint32_t* qkv_w;   /* [(nQ+2nKV)*D][H/16], q rows then k then v (WeightStore 66-79) */
+    const void* qkv_s;
+    const void* qkv_b;
+    const void* q_norm_w;    /* fp16 [D] */
+    const void* k_norm_w;    /* fp16 [D] */
+    const uint32_t* o_w;     /* [H][nQ*D/16] */
+    const void* o_s;
+    const void* o_b;
+} mj_attn_weights;
+
+typedef struct mj_attn_config {
+    int H, n_heads, n_kv_heads, head_dim; /* head_dim must be 128 */
+    int rope_dim;                         /* rotated leading dims (0 = NoPE) */
+    float rope_base, eps;
+    int window;                           /* sliding window (0 = full attention) */
+    int64_t kv_capacity;                  /* slots C of the cache; >= window + M */
+    int gs;
+} mj_attn_config;
+
+/* Attention block with residual -- encodeAttnBlock (SeedlessMetal.swift:926-1005) with the
+ * input RMSNorm of encodeLayerBlock (1008-1048): h += o_proj(attn(rms(h))).
+ * Verify row r sits at position L + depth(r); parents_host[r] < r gives the draft tree
+ * (NULL = linear chain, parents[0] = -1).  Row r attends the committed positions inside its
+ * window plus its ancestors and itself.  New K/V rows are written at slot (L + r) % C of the
+ * caches kcache/vcache fp16 [n_kv][C][128]; committed position p lives at slot p % C. */
+mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_weights* w,
+                        void* h, void* kcache, void* vcache, int64_t L,
+                        const int32_t* parents_host, int M);
+
+/* lm_head verify -- encodeMetalHead -> maple_lm_head_argmax/reduce
+ * (SeedlessDecodeEngine.swift:481-498, SeedlessMetal.swift:3005-3111) for an fp16 head:
+ * logits[m][v] = sum_k w[v][k] * x[m][k] (fp32), argmax per row with the lowest id winning
+ * ties and banned ids skipped.  x fp16 [M][K], w fp16 [V][K]; out_argmax int32 [M];
+ * out_max fp32 [M] (nullable); out_logits fp32 [M][V] (nullable; written when sampling).
+ * banned int32 [n_banned] device (nullable). */
+mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, int K, int V,
+                            const int32_t* banned, int n_banned, int32_t* out_argmax,
+                            float* out_max, float* out_logits);
+
+/* Greedy acceptance -- verifyDraftChain (SeedlessDecodeEngine.swift:1574-1603) generalised to
+ * a tree: from row 0 step to the lowest-index child whose token equals the current row's
+ * argmax; stop when none does.  tokens/argmax int32 [n_rows] device, parents_host as above.
+ * out int32 device [2 + 2*n_rows]: out[0] = accepted, out[1] = bonus token,
+ * out[2 .. 2+acc] = accepted row path (row 0 first), out[2+n_rows .. 2+n_rows+acc] = emitted
+ * tokens (accepted drafts then the bonus). */
+mj_status mj_accept_greedy(mj_ctx* ctx, const int32_t* tokens, const int32_t* parents_host,
+                           const int32_t* argmax, int n_rows, int32_t* out);
+
+/* Sampled acceptance over the full vocabulary -- SpeculativeSampling.tryAccept / walkDraft
+ * (SpeculativeSampling.swift:27-99) with LogitsProcessor.probabilities / samplePrepared
+ * (LogitsProcessor.swift:116-189), no penalties.  logits fp32 [rows][V] device (row i = target
+ * after feed i), draft int32 [rows-1] device.  q_mode MJ_Q_POINT: q = q_point[i] at the draft
+ * token (q_point device nullable = 1, the reference default); MJ_Q_UNIFORM: q = 1/V.
+ * Uniforms: Philox4x32-10, key = seed, counter = (row, counter lo, counter hi, 0x6d6a6a76),
+ * u0 = accept test, u1 = residual walk (row rows-1: u0 = bonus).  Sums and walks use a fixed
+ * blocked order (16-element chunks, 64-chunk blocks) so results are reproducible bit for bit.
+ * out int32 device [2]: accepted count, emitted token.  temperature must be > 1e-5. */
+#define MJ_Q_POINT 0
+#define MJ_Q_UNIFORM 1
+mj_status mj_accept_sampled(mj_ctx* ctx, const float* logits, int rows, int V,
+                            const int32_t* draft, float temperature, int q_mode,
+                            const float* q_point, uint64_t seed, uint64_t counter, int32_t* out);
+
+/* ---------------------------------------------------------------- model ------ */
+typedef struct mj_model_config {
+    int n_layers;
+    int H, n_heads, n_kv_heads, head_dim, rope_dim;
+    float rope_base, eps;
+    int window;            /* sliding window of every layer (0 = full) */
+    int64_t kv_capacity;   /* ring slots per layer (>= window + MJ_MAX_ROWS when windowed) */
+    int E, top_k, I, gs;
+    int vocab;
+} mj_model_config;
+
+typedef struct mj_layer_weights {
+    mj_attn_weights attn;
+    mj_moe_weights moe;    /* moe.norm_w = post_attention_layernorm */
+} mj_layer_weights;
+
+/* A resident stack (SeedlessLayerStack, SeedlessAttn.swift:369-456): caller-owned weights,
+ * library-owned KV caches and scratch sized for MJ_MAX_ROWS rows.  layers [n_layers] is copied;
+ * the device buffers it points to must outlive the model.  embed fp16 [V][H], final_norm_w
+ * fp16 [H], lm_head fp16 [V][H]. */
+mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_layer_weights* layers,
+                          const void* embed, const void* final_norm_w, const void* lm_head,
+                          mj_model** out);
+mj_status mj_model_destroy(mj_model* model);
+/* Committed tokens (SeedlessLayerBlock.offset) and rewind (rewindOffset, SeedlessAttn.swift
+ * 319-322; the reject rollback of snapshotForChain 540-586 when writes are append-only). */
+int64_t mj_model_offset(const mj_model* model);
+mj_status mj_model_rewind(mj_model* model, int64_t offset);
+/* Device pointers of layer `layer`'s caches, fp16 [n_kv][kv_capacity][head_dim]. */
+mj_status mj_model_kv(mj_model* model, int layer, void** kcache, void** vcache);
+
+/* prefillPrompt (SeedlessDecodeEngine.swift:516-545): feed tokens in chunks of <= chunk rows
+ * (<= MJ_MAX_ROWS), commit them, return the argmax after the last token.  Synchronises. */
+mj_status mj_prefill(mj_model* model, const int32_t* tokens, int n, int chunk,
+                     int32_t* out_next);
+
+/* stepChainFeeds (SeedlessDecodeEngine.swift:194-228): one pass over the chain `feeds`
+ * (M rows), commit all M, return the greedy argmax after each row.  Synchronises. */
+mj_status mj_step_chain_feeds(mj_model* model, const int32_t* feeds, int M, int32_t* out_evals);
+
+/* verifyDraftChain (SeedlessDecodeEngine.swift:1574-1603), tree-capable: one pass over rows
+ * [y] + draft (parents NULL = chain; else parents[0] = -1 and parents[r] < r over the rows),
+ * greedy acceptance on the device, accepted rows compacted into the cache, offset advanced by
+ * accepted + 1.  out_tokens [n_draft + 1]: accepted drafts then the bonus token.
+ * One device wait per call. */
+mj_status mj_verify_greedy(mj_model* model, int32_t y, const int32_t* draft, int n_draft,
+                           const int32_t* parents, int32_t* out_accepted, int32_t* out_tokens);
+
+/* verifyDraftSampled (SeedlessDecodeEngine.swift:1541-1571) over the exact fp16 head and the
+ * full vocabulary (chain drafts): one pass, device-side sampled acceptance (mj_accept_sampled
+ * rules), commit accepted + 1 rows.  out_token = resampled token or bonus. */
+mj_status mj_verify_sampled(mj_model* model, int32_t y, const int32_t* draft, int n_draft,
+                            float temperature, int q_mode, const float* q_point, uint64_t seed,
+                            uint64_t counter, int32_t* out_accepted, int32_t* out_token);
+
+/* Debug capture for layer-by-layer checks: when set, each pass copies h after the embedding
+ * and after every layer into h_capture fp16 [n_layers+1][MJ_MAX_ROWS][H], the routing into
+ * inds_capture int32 [n_layers][MJ_MAX_ROWS][top_k] and the head logits into logits_capture
+ * fp32 [MJ_MAX_ROWS][V] (device pointers, any may be NULL; all NULL disables). */
+mj_status mj_model_set_capture(mj_model* model, void* h_capture, int32_t* inds_capture,
+                               float* logits_capture);
+
+/* Use HIP graphs for verify passes (one graph per row count and mode, replayed with a device
+ * step descriptor).  On by default. */
+mj_status mj_model_set_graphs(mj_model* model, int enable);
+
+/* Per-pass device timing of the last verify call (ms), from HIP events on the model stream. */
+float mj_model_last_pass_ms(const mj_model* model);
+
+/* Hardware self-check of the MFMA operand layout the kernels rely on (16x16x32 f16):
+ * D = A[16x32] * B[32x16] with A, B fp16 row-major device, D fp32 [16][16] device. */
+mj_status mj_selftest_mfma(mj_ctx* ctx, const void* A, const void* B, float* D);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,125 @@
+"""ctypes binding of libmomij_hip.so (the C ABI declared in include/momij_hip.h).
+
+The library is built in-tree by momij_amd.build (or __graft_entry__.build()).  Loading fails
+loudly when it is missing: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmomij_hip.so")
+
+MJ_OK = 0
+STATUS = {0: "MJ_OK", 1: "MJ_NO_DEVICE", 2: "MJ_NOT_READY", 3: "MJ_UNSUPPORTED_SHAPE",
+          4: "MJ_INVALID_ARG", 5: "MJ_ABORTED", 6: "MJ_HIP_ERROR", 7: "MJ_CAPACITY"}
+MJ_MAX_ROWS = 64
+MJ_EPI_STORE, MJ_EPI_ADD = 0, 1
+MJ_MOE_PRENORM, MJ_MOE_RESIDUAL = 1, 2
+MJ_Q_POINT, MJ_Q_UNIFORM = 0, 1
+
+
+class MomijError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+vp = C.c_void_p
+i32 = C.c_int
+f32 = C.c_float
+i64 = C.c_int64
+u64 = C.c_uint64
+
+
+class MoeWeights(C.Structure):
+    _fields_ = [("norm_w", vp), ("router_w", vp), ("up_gate_w", vp), ("up_gate_s", vp),
+                ("up_gate_b", vp), ("down_w", vp), ("down_s", vp), ("down_b", vp),
+                ("E", i32), ("top_k", i32), ("H", i32), ("I", i32), ("gs", i32), ("eps", f32)]
+
+
+class AttnWeights(C.Structure):
+    _fields_ = [("norm_w", vp), ("qkv_w", vp), ("qkv_s", vp), ("qkv_b", vp), ("q_norm_w", vp),
+                ("k_norm_w", vp), ("o_w", vp), ("o_s", vp), ("o_b", vp)]
+
+
+class AttnConfig(C.Structure):
+    _fields_ = [("H", i32), ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
+                ("rope_dim", i32), ("rope_base", f32), ("eps", f32), ("window", i32),
+                ("kv_capacity", i64), ("gs", i32)]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("n_layers", i32), ("H", i32), ("n_heads", i32), ("n_kv_heads", i32),
+                ("head_dim", i32), ("rope_dim", i32), ("rope_base", f32), ("eps", f32),
+                ("window", i32), ("kv_capacity", i64), ("E", i32), ("top_k", i32), ("I", i32),
+                ("gs", i32), ("vocab", i32)]
+
+
+class LayerWeights(C.Structure):
+    _fields_ = [("attn", AttnWeights), ("moe", MoeWeights)]
+
+
+_SIGS = {
+    "mj_abi_version": (i32, []),
+    "mj_status_str": (C.c_char_p, [i32]),
+    "mj_init": (i32, [i32, C.POINTER(vp)]),
+    "mj_destroy": (i32, [vp]),
+    "mj_last_error": (C.c_char_p, [vp]),
+    "mj_set_stream": (i32, [vp, vp]),
+    "mj_get_stream": (vp, [vp]),
+    "mj_set_abort": (i32, [vp, i32]),
+    "mj_sync": (i32, [vp]),
+    "mj_alloc": (i32, [vp, C.c_size_t, C.POINTER(vp)]),
+    "mj_free": (i32, [vp, vp]),
+    "mj_h2d": (i32, [vp, vp, vp, C.c_size_t]),
+    "mj_d2h": (i32, [vp, vp, vp, C.c_size_t]),
+    "mj_gather_qmm2": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32]),
+    "mj_moe_block": (i32, [vp, C.POINTER(MoeWeights), vp, vp, i32, i32, vp, vp]),
+    "mj_attn_block": (i32, [vp, C.POINTER(AttnConfig), C.POINTER(AttnWeights), vp, vp, vp, i64,
+                            vp, i32]),
+    "mj_lm_head_verify": (i32, [vp, vp, vp, i32, i32, i32, vp, i32, vp, vp, vp]),
+    "mj_accept_greedy": (i32, [vp, vp, vp, vp, i32, vp]),
+    "mj_accept_sampled": (i32, [vp, vp, i32, i32, vp, f32, i32, vp, u64, u64, vp]),
+    "mj_model_create": (i32, [vp, C.POINTER(ModelConfig), vp, vp, vp, vp, C.POINTER(vp)]),
+    "mj_model_destroy": (i32, [vp]),
+    "mj_model_offset": (i64, [vp]),
+    "mj_model_rewind": (i32, [vp, i64]),
+    "mj_model_kv": (i32, [vp, i32, C.POINTER(vp), C.POINTER(vp)]),
+    "mj_prefill": (i32, [vp, vp, i32, i32, vp]),
+    "mj_step_chain_feeds": (i32, [vp, vp, i32, vp]),
+    "mj_verify_greedy": (i32, [vp, i32, vp, i32, vp, vp, vp]),
+    "mj_verify_sampled": (i32, [vp, i32, vp, i32, f32, i32, vp, u64, u64, vp, vp]),
+    "mj_model_set_capture": (i32, [vp, vp, vp, vp]),
+    "mj_model_set_graphs": (i32, [vp, i32]),
+    "mj_model_last_pass_ms": (f32, [vp]),
+    "mj_selftest_mfma": (i32, [vp, vp, vp, vp]),
+}
+
+_lib = None
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m momij_amd.build` (or "
+                "__graft_entry__.build()) first -- there is no fallback path")
+        lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/momij_hip.h."""
+    import re
+
+    hdr = os.path.join(os.path.dirname(HERE), "include", "momij_hip.h")
+    text = open(hdr).read()
+    return sorted(set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(mj_\w+)\s*\(", text, flags=re.M)))

@@ -1,0 +1,396 @@
+// abi.cpp -- C ABI: context, device memory, and the op-level entry points.
+//
+// The context mirrors SeedlessMetal's process-global state (device, queue, stop buffer;
+// SeedlessMetal.swift:23-104) as an explicit handle: one HIP stream, a device abort word and a
+// scratch arena for the op-level calls.  Shape guards mirror SeedlessMetal.gqmm2's
+// (SeedlessMetal.swift:336-338), widened to what the gfx950 kernels tile.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/momij_hip.h"
+#include "mj_abi_internal.h"
+#include "mj_internal.h"
+
+mj_status mj_fail(mj_ctx* ctx, mj_status st, const char* fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return st;
+}
+
+mj_status mj_hip(mj_ctx* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return MJ_OK;
+    return mj_fail(ctx, MJ_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+}
+
+mj_status mj_scratch_reserve(mj_ctx* ctx, size_t bytes) {
+    if (bytes <= ctx->scratch_bytes) return MJ_OK;
+    mj_status s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "scratch sync");
+    if (s != MJ_OK) return s;
+    if (ctx->scratch) hipFree(ctx->scratch);
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+    const size_t want = bytes + (bytes >> 2) + 4096;
+    s = mj_hip(ctx, hipMalloc(&ctx->scratch, want), "scratch alloc");
+    if (s != MJ_OK) return s;
+    ctx->scratch_bytes = want;
+    return MJ_OK;
+}
+
+void* Arena::take(size_t bytes) {
+    off = (off + 255) & ~(size_t)255;
+    void* p = base ? (char*)base + off : nullptr;
+    off += bytes;
+    return p;
+}
+
+mj_status mj_check_abort(mj_ctx* ctx) {
+    int v = 0;
+    mj_status s = mj_hip(ctx, hipMemcpyAsync(&v, ctx->abort_dev, sizeof v, hipMemcpyDeviceToHost,
+                                             ctx->stream), "abort read");
+    if (s != MJ_OK) return s;
+    s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "abort sync");
+    if (s != MJ_OK) return s;
+    return v ? mj_fail(ctx, MJ_ABORTED, "aborted by the abort word") : MJ_OK;
+}
+
+extern "C" {
+
+int mj_abi_version(void) { return MJ_ABI_VERSION; }
+
+const char* mj_status_str(mj_status s) {
+    switch (s) {
+        case MJ_OK: return "ok";
+        case MJ_NO_DEVICE: return "no device";
+        case MJ_NOT_READY: return "not ready";
+        case MJ_UNSUPPORTED_SHAPE: return "unsupported shape";
+        case MJ_INVALID_ARG: return "invalid argument";
+        case MJ_ABORTED: return "aborted";
+        case MJ_HIP_ERROR: return "hip error";
+        case MJ_CAPACITY: return "capacity exceeded";
+    }
+    return "unknown";
+}
+
+mj_status mj_init(int device, mj_ctx** out) {
+    if (!out) return MJ_INVALID_ARG;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0 || device < 0 || device >= n)
+        return MJ_NO_DEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return MJ_NO_DEVICE;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return MJ_NO_DEVICE;
+    if (hipSetDevice(device) != hipSuccess) return MJ_NO_DEVICE;
+    mj_ctx* c = new mj_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc(&c->abort_dev, sizeof(int)) != hipSuccess ||
+        hipMemset(c->abort_dev, 0, sizeof(int)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        delete c;
+        return MJ_HIP_ERROR;
+    }
+    c->stream = c->own;
+    *out = c;
+    return MJ_OK;
+}
+
+mj_status mj_destroy(mj_ctx* ctx) {
+    if (!ctx) return MJ_INVALID_ARG;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) hipFree(ctx->scratch);
+    if (ctx->abort_dev) hipFree(ctx->abort_dev);
+    if (ctx->own) hipStreamDestroy(ctx->own);
+    delete ctx;
+    return MJ_OK;
+}
+
+const char* mj_last_error(const mj_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+mj_status mj_set_stream(mj_ctx* ctx, void* s) {
+    if (!ctx) return MJ_INVALID_ARG;
+    ctx->stream = s ? (hipStream_t)s : ctx->own;
+    return MJ_OK;
+}
+
+void* mj_get_stream(const mj_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+mj_status mj_set_abort(mj_ctx* ctx, int flag) {
+    if (!ctx) return MJ_INVALID_ARG;
+    const int v = flag ? 1 : 0;
+    mj_status s = mj_hip(ctx, hipMemcpyAsync(ctx->abort_dev, &v, sizeof v, hipMemcpyHostToDevice,
+                                             ctx->stream), "set abort");
+    if (s != MJ_OK) return s;
+    return mj_hip(ctx, hipStreamSynchronize(ctx->stream), "set abort sync");
+}
+
+mj_status mj_sync(mj_ctx* ctx) {
+    if (!ctx) return MJ_INVALID_ARG;
+    mj_status s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "sync");
+    if (s != MJ_OK) return s;
+    return mj_check_abort(ctx);
+}
+
+mj_status mj_alloc(mj_ctx* ctx, size_t bytes, void** out) {
+    if (!ctx || !out) return MJ_INVALID_ARG;
+    *out = nullptr;
+    return mj_hip(ctx, hipMalloc(out, bytes ? bytes : 1), "alloc");
+}
+
+mj_status mj_free(mj_ctx* ctx, void* p) {
+    if (!ctx) return MJ_INVALID_ARG;
+    if (!p) return MJ_OK;
+    mj_status s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "free sync");
+    if (s != MJ_OK) return s;
+    return mj_hip(ctx, hipFree(p), "free");
+}
+
+mj_status mj_h2d(mj_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return MJ_INVALID_ARG;
+    mj_status s = mj_hip(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream),
+                         "h2d");
+    if (s != MJ_OK) return s;
+    return mj_hip(ctx, hipStreamSynchronize(ctx->stream), "h2d sync");
+}
+
+mj_status mj_d2h(mj_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return MJ_INVALID_ARG;
+    mj_status s = mj_hip(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream),
+                         "d2h");
+    if (s != MJ_OK) return s;
+    return mj_hip(ctx, hipStreamSynchronize(ctx->stream), "d2h sync");
+}
+
+mj_status mj_gather_qmm2(mj_ctx* ctx, const void* x, const uint32_t* w, const void* scales,
+                         const void* biases, const int32_t* inds, void* y, int M, int ktop,
+                         int K, int N, int gs, int lhs_per_expert, int epilogue) {
+    if (!ctx) return MJ_INVALID_ARG;
+    if (!x || !w || !scales || !biases || !inds || !y || M < 1 || ktop < 1)
+        return mj_fail(ctx, MJ_INVALID_ARG, "gather_qmm2: null pointer or M/ktop < 1");
+    if (K % 512 != 0 || N % 16 != 0 || K < 512 || N < 16 || (gs != 64 && gs != 128) ||
+        M * ktop > MJ_MAX_PAIRS)
+        return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
+                       "unsupported shape N=%d K=%d gs=%d (need K%%512==0, N%%16==0, gs 64|128, "
+                       "M*ktop<=%d)", N, K, gs, MJ_MAX_PAIRS);
+    if (epilogue != MJ_EPI_STORE && epilogue != MJ_EPI_ADD)
+        return mj_fail(ctx, MJ_INVALID_ARG, "gather_qmm2: unknown epilogue %d", epilogue);
+    if (epilogue == MJ_EPI_ADD && ktop != 1)
+        return mj_fail(ctx, MJ_INVALID_ARG, "gather_qmm2: MJ_EPI_ADD needs ktop == 1");
+    hipSetDevice(ctx->device);
+    const int P = M * ktop;
+    if (P == 1 && epilogue == MJ_EPI_STORE && (K == 1024 || K == 2048 || K == 4096)) {
+        QmvArgs a{};
+        a.x = (const uint16_t*)x;
+        a.w = w;
+        a.s = (const uint16_t*)scales;
+        a.b = (const uint16_t*)biases;
+        a.inds = inds;
+        a.y = (uint16_t*)y;
+        a.K = K;
+        a.N = N;
+        a.gs = gs;
+        a.pairs = 1;
+        a.lhs_per = 0;
+        a.abort = ctx->abort_dev;
+        return mj_hip(ctx, launch_qmv2(a, EPI_STORE, ctx->stream), "qmv2 launch");
+    }
+    const int rows_x = lhs_per_expert ? P : M;
+    Arena ar;
+    ar.take((size_t)rows_x * K * 2);
+    ar.take((size_t)rows_x * (K / 64) * sizeof(float2));
+    ar.take(sizeof(Buckets));
+    mj_status s = mj_scratch_reserve(ctx, ar.off);
+    if (s != MJ_OK) return s;
+    ar = Arena{ctx->scratch, 0};
+    uint16_t* xperm = (uint16_t*)ar.take((size_t)rows_x * K * 2);
+    float2* xsum = (float2*)ar.take((size_t)rows_x * (K / 64) * sizeof(float2));
+    Buckets* bk = (Buckets*)ar.take(sizeof(Buckets));
+    s = mj_hip(ctx, launch_qx_prep((const uint16_t*)x, xperm, xsum, rows_x, K, ctx->abort_dev,
+                                   ctx->stream), "qx prep");
+    if (s != MJ_OK) return s;
+    s = mj_hip(ctx, launch_bucket_inds(inds, P, bk, ctx->abort_dev, ctx->stream), "bucket");
+    if (s != MJ_OK) return s;
+    GatherArgs g{};
+    g.xperm = xperm;
+    g.xsum = xsum;
+    g.w = w;
+    g.s = (const uint16_t*)scales;
+    g.b = (const uint16_t*)biases;
+    g.bk = bk;
+    g.y = (uint16_t*)y;
+    g.K = K;
+    g.N = N;
+    g.gs = gs;
+    g.x_div = lhs_per_expert ? 1 : ktop;
+    g.abort = ctx->abort_dev;
+    const int nb = P < MJ_MAX_EXPERTS ? P : MJ_MAX_EXPERTS;
+    return mj_hip(ctx, launch_gather(g, epilogue == MJ_EPI_ADD ? EPI_ADD : EPI_STORE, P, nb,
+                                     ctx->stream), "gather launch");
+}
+
+mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y, int M,
+                       int flags, int32_t* out_inds, float* out_scores) {
+    if (!ctx) return MJ_INVALID_ARG;
+    if (!w || !x || !y || M < 1 || M > MJ_MAX_ROWS)
+        return mj_fail(ctx, MJ_INVALID_ARG, "moe_block: null pointer or M outside 1..%d",
+                       MJ_MAX_ROWS);
+    if (!w->router_w || !w->up_gate_w || !w->up_gate_s || !w->up_gate_b || !w->down_w ||
+        !w->down_s || !w->down_b || ((flags & MJ_MOE_PRENORM) && !w->norm_w))
+        return mj_fail(ctx, MJ_INVALID_ARG, "moe_block: null weight pointer");
+    const int H = w->H, I = w->I, E = w->E, k = w->top_k, gs = w->gs;
+    if (H % 2048 != 0 || H > 4096 || I % 1024 != 0 || I > 4096 || E < k || E > MJ_MAX_EXPERTS ||
+        k < 1 || k > 8 || (gs != 64 && gs != 128))
+        return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
+                       "moe_block: unsupported shape H=%d I=%d E=%d top_k=%d gs=%d", H, I, E, k,
+                       gs);
+    hipSetDevice(ctx->device);
+    MoeScratch ms;
+    mj_status s = moe_scratch(ctx, H, I, E, k, M, ms);
+    if (s != MJ_OK) return s;
+    return run_moe(ctx, w, (const uint16_t*)x, (uint16_t*)y, M, flags, ms,
+                   out_inds ? out_inds : ms.inds, out_scores ? out_scores : ms.scores,
+                   ctx->stream);
+}
+
+mj_status mj_selftest_mfma(mj_ctx* ctx, const void* A, const void* B, float* D) {
+    if (!ctx || !A || !B || !D) return MJ_INVALID_ARG;
+    hipSetDevice(ctx->device);
+    return mj_hip(ctx, launch_selftest_mfma((const uint16_t*)A, (const uint16_t*)B, D,
+                                            ctx->stream), "selftest launch");
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------------------------------------
+// MoE block orchestration (shared with the model pass).
+// ----------------------------------------------------------------------------------------
+mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms) {
+    Arena ar;
+    auto layout = [&](Arena& a) {
+        ms.xn = (uint16_t*)a.take((size_t)M * H * 2);
+        ms.xperm = (uint16_t*)a.take((size_t)M * H * 2);
+        ms.xsum = (float2*)a.take((size_t)M * (H / 64) * sizeof(float2));
+        ms.logits = (float*)a.take((size_t)M * E * 4);
+        ms.inds = (int32_t*)a.take((size_t)M * k * 4);
+        ms.scores = (float*)a.take((size_t)M * k * 4);
+        ms.bk = (Buckets*)a.take(sizeof(Buckets));
+        ms.act = (uint16_t*)a.take((size_t)M * k * I * 2);
+        ms.act_sum = (float2*)a.take((size_t)M * k * (I / 64) * sizeof(float2));
+        ms.down = (uint16_t*)a.take((size_t)M * k * H * 2);
+    };
+    layout(ar);
+    mj_status s = mj_scratch_reserve(ctx, ar.off);
+    if (s != MJ_OK) return s;
+    Arena real{ctx->scratch, 0};
+    layout(real);
+    return MJ_OK;
+}
+
+mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
+                  int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st) {
+    const int H = w->H, I = w->I, E = w->E, k = w->top_k;
+    const int* ab = ctx->abort_dev;
+    const uint16_t* xn = x;
+    mj_status s;
+    if (M == 1) {
+        if (flags & MJ_MOE_PRENORM) {
+            s = mj_hip(ctx, launch_rmsnorm_qx(x, (const uint16_t*)w->norm_w, w->eps, ms.xn,
+                                              nullptr, nullptr, 1, H, ab, st), "rmsnorm");
+            if (s != MJ_OK) return s;
+            xn = ms.xn;
+        }
+        s = mj_hip(ctx, launch_router((const uint16_t*)w->router_w, xn, ms.logits, 1, E, H, ab,
+                                      st), "router");
+        if (s != MJ_OK) return s;
+        s = mj_hip(ctx, launch_topk_bucket(ms.logits, 1, E, k, inds, scores, nullptr, ab, st),
+                   "topk");
+        if (s != MJ_OK) return s;
+        QmvArgs up{};
+        up.x = xn;
+        up.w = w->up_gate_w;
+        up.s = (const uint16_t*)w->up_gate_s;
+        up.b = (const uint16_t*)w->up_gate_b;
+        up.inds = inds;
+        up.y = ms.act;
+        up.K = H;
+        up.N = 2 * I;
+        up.gs = w->gs;
+        up.pairs = k;
+        up.lhs_per = 0;
+        up.abort = ab;
+        s = mj_hip(ctx, launch_qmv2(up, EPI_SWIGLU, st), "up qmv");
+        if (s != MJ_OK) return s;
+        QmvArgs dn = up;
+        dn.x = ms.act;
+        dn.w = w->down_w;
+        dn.s = (const uint16_t*)w->down_s;
+        dn.b = (const uint16_t*)w->down_b;
+        dn.y = ms.down;
+        dn.K = I;
+        dn.N = H;
+        dn.lhs_per = 1;
+        s = mj_hip(ctx, launch_qmv2(dn, EPI_STORE, st), "down qmv");
+        if (s != MJ_OK) return s;
+    } else {
+        if (flags & MJ_MOE_PRENORM) {
+            s = mj_hip(ctx, launch_rmsnorm_qx(x, (const uint16_t*)w->norm_w, w->eps, ms.xn,
+                                              ms.xperm, ms.xsum, M, H, ab, st), "rmsnorm");
+            xn = ms.xn;
+        } else {
+            s = mj_hip(ctx, launch_qx_prep(x, ms.xperm, ms.xsum, M, H, ab, st), "qx prep");
+        }
+        if (s != MJ_OK) return s;
+        s = mj_hip(ctx, launch_router((const uint16_t*)w->router_w, xn, ms.logits, M, E, H, ab,
+                                      st), "router");
+        if (s != MJ_OK) return s;
+        s = mj_hip(ctx, launch_topk_bucket(ms.logits, M, E, k, inds, scores, ms.bk, ab, st),
+                   "topk");
+        if (s != MJ_OK) return s;
+        const int nb = M * k < E ? M * k : E;
+        GatherArgs up{};
+        up.xperm = ms.xperm;
+        up.xsum = ms.xsum;
+        up.w = w->up_gate_w;
+        up.s = (const uint16_t*)w->up_gate_s;
+        up.b = (const uint16_t*)w->up_gate_b;
+        up.bk = ms.bk;
+        up.y = ms.act;
+        up.ysum = ms.act_sum;
+        up.K = H;
+        up.N = 2 * I;
+        up.gs = w->gs;
+        up.x_div = k;
+        up.abort = ab;
+        s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, nb, st), "up gather");
+        if (s != MJ_OK) return s;
+        GatherArgs dn{};
+        dn.xperm = ms.act;
+        dn.xsum = ms.act_sum;
+        dn.w = w->down_w;
+        dn.s = (const uint16_t*)w->down_s;
+        dn.b = (const uint16_t*)w->down_b;
+        dn.bk = ms.bk;
+        dn.y = ms.down;
+        dn.K = I;
+        dn.N = H;
+        dn.gs = w->gs;
+        dn.x_div = 1;
+        dn.abort = ab;
+        s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, nb, st), "down gather");
+        if (s != MJ_OK) return s;
+    }
+    return mj_hip(ctx, launch_score_combine(ms.down, scores,
+                                            (flags & MJ_MOE_RESIDUAL) ? x : nullptr, y, M, k, H,
+                                            ab, st), "combine");
+}

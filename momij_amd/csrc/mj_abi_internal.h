@@ -1,0 +1,46 @@
+// mj_abi_internal.h -- host-side state behind the C ABI handles.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/momij_hip.h"
+#include "mj_internal.h"
+
+struct mj_ctx {
+    int device = 0;
+    hipStream_t own = nullptr;     // the context's own stream (default priority)
+    hipStream_t stream = nullptr;  // stream in use (own, or a caller's)
+    int* abort_dev = nullptr;      // device abort word (stopBuf)
+    void* scratch = nullptr;       // op-level scratch arena
+    size_t scratch_bytes = 0;
+    std::string err;
+};
+
+// Bump allocator over a buffer (base == nullptr: size counting only).
+struct Arena {
+    void* base = nullptr;
+    size_t off = 0;
+    void* take(size_t bytes);
+};
+
+struct MoeScratch {
+    uint16_t* xn;        // normed rows, plain [M][H]
+    uint16_t* xperm;     // qx rows [M][H]
+    float2* xsum;        // [M][H/64]
+    float* logits;       // [M][E]
+    int32_t* inds;       // [M][k]
+    float* scores;       // [M][k]
+    Buckets* bk;
+    uint16_t* act;       // [M*k][I] (qx for M > 1, plain for M == 1)
+    float2* act_sum;     // [M*k][I/64]
+    uint16_t* down;      // [M*k][H]
+};
+
+mj_status mj_fail(mj_ctx* ctx, mj_status st, const char* fmt, ...);
+mj_status mj_hip(mj_ctx* ctx, hipError_t e, const char* what);
+mj_status mj_scratch_reserve(mj_ctx* ctx, size_t bytes);
+mj_status mj_check_abort(mj_ctx* ctx);
+mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms);
+mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
+                  int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st);

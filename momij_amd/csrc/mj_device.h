@@ -1,0 +1,143 @@
+// mj_device.h -- device helpers shared by the gfx950 kernels.
+//
+// 2-bit code expansion.  A uint32 word of the MLX layout holds codes c0..c15 (code i in bits
+// [2i, 2i+1]).  unpack16() turns it into eight fp16 pairs without a per-code shift:
+//     v[i] = (base_i + c_i, base_i + c_{i+8}),  base_i = 16 (i even) or 4 (i odd),
+// by masking two code positions straight into the fp16 mantissa of a constant whose ulp is
+// 1: 0x4C00 = 16.0 (mantissa bits 6-7 carry c) and 0x4400 = 4.0 (bits 8-9).  Four shifted
+// copies of the word cover all 16 codes: 12 VALU ops per 16 weights.  The constant part is
+// removed exactly after the dot product: sum_k (base_k + c_k) x_k - sum_k base_k x_k, with
+// Bx = sum_k base_k x_k precomputed once per 64-element block of x.  Small bases keep the
+// fp32 partial sums within ~100x of the result, so the subtraction costs < 1e-5 relative.
+//
+// Activations feeding a 2-bit product are stored "permuted": inside each 16-element block
+// the order is x0 x8 x1 x9 x2 x10 x3 x11 x4 x12 x5 x13 x6 x14 x7 x15, i.e. fp16 pair i is
+// (x_i, x_{i+8}) and lines up with v[i].  Each 64-block also carries float2 {X, Bx} =
+// {sum x, sum base*x}.  Together this is the "qx" activation format.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+#define MJ_WAVE 64
+
+__device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ float hround(float f) { return (float)(_Float16)f; }
+
+__device__ __forceinline__ void unpack16(uint32_t w, uint32_t v[8]) {
+    const uint32_t s1 = w << 6, s2 = w << 2, s3 = w >> 2, s4 = w >> 6;
+    v[0] = (s1 & 0x00C000C0u) | 0x4C004C00u;
+    v[1] = (s1 & 0x03000300u) | 0x44004400u;
+    v[2] = (s2 & 0x00C000C0u) | 0x4C004C00u;
+    v[3] = (s2 & 0x03000300u) | 0x44004400u;
+    v[4] = (s3 & 0x00C000C0u) | 0x4C004C00u;
+    v[5] = (s3 & 0x03000300u) | 0x44004400u;
+    v[6] = (s4 & 0x00C000C0u) | 0x4C004C00u;
+    v[7] = (s4 & 0x03000300u) | 0x44004400u;
+}
+
+// base of permuted pair i (16 for even code index, 4 for odd)
+__device__ __forceinline__ float code_base(int i) { return (i & 1) ? 4.0f : 16.0f; }
+
+// fp16 pair (lo, hi) from two raw fp16 bit patterns
+__device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) {
+    return (lo16 & 0xFFFFu) | (hi16 << 16);
+}
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, a), __builtin_bit_cast(h2v, b), c,
+                                  false);
+}
+
+// Permute one 16-element block held as 8 plain pairs u[j] = (x_{2j}, x_{2j+1}) into the qx
+// order p[i] = (x_i, x_{i+8}).
+__device__ __forceinline__ void perm16(const uint32_t u[8], uint32_t p[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        p[2 * j] = (u[j] & 0xFFFFu) | (u[j + 4] << 16);
+        p[2 * j + 1] = (u[j] >> 16) | (u[j + 4] & 0xFFFF0000u);
+    }
+}
+
+// Position of plain element i (0..15) inside a permuted 16-block.
+__device__ __forceinline__ int perm_pos(int i) { return i < 8 ? 2 * i : 2 * (i - 8) + 1; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, MJ_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MJ_WAVE));
+    return v;
+}
+
+// (value, index) argmax across the wave: larger value wins, lower index on ties.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, MJ_WAVE);
+        const int oi = __shfl_xor(i, o, MJ_WAVE);
+        if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+}
+
+__device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h8 as_h8(u4v v) { return __builtin_bit_cast(h8, v); }
+
+__device__ __forceinline__ bool aborted(const int* flag) { return flag != nullptr && *flag != 0; }
+
+// ------------------------------------------------------------------------------------------
+// Canonical arithmetic for sampled acceptance.  The CPU oracle evaluates the identical IEEE
+// operation sequence, so both produce the same bits: exp by Cody-Waite reduction and a
+// degree-7 Taylor polynomial in fused multiply-adds, scaled by 2^n from exponent bits.
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ float canon_expf(float x) {
+#pragma clang fp contract(off)
+    if (!(x >= -87.0f)) return 0.0f;
+    const float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e400p-1f, x);
+    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0x1.000000p-1f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float two_n = __builtin_bit_cast(float, (uint32_t)((int)n + 127) << 23);
+    return p * two_n;
+}
+
+// Philox4x32-10 (Salmon et al., SC'11).
+__device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+        c[1] = (uint32_t)p1;
+        c[3] = (uint32_t)p0;
+        c[0] = n0;
+        c[2] = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+__device__ __forceinline__ float u01(uint32_t x) { return (float)(x >> 8) * 0x1p-24f; }

@@ -1,0 +1,167 @@
+"""GPU parity: 2-bit gather-qmm (GEMV and bucketed MFMA GEMM) and the MoE block vs the oracle.
+
+Float outputs: relative-to-norm 2e-2 and absolute 1e-2 (the verify-step bar).  Expert indices
+are compared bit for bit.
+"""
+import numpy as np
+import pytest
+
+from momij_amd import synth
+from tests.gpu_util import assert_close, dev, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import torch
+
+    from momij_amd.ops import Context
+
+    assert torch.cuda.is_available()
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def _run(ctx, fn):
+    import torch
+
+    torch.cuda.synchronize()
+    fn()
+    ctx.sync()
+
+
+def test_mfma_operand_layout(ctx):
+    import torch
+
+    rng = np.random.default_rng(0)
+    A = rng.integers(-4, 5, (16, 32)).astype(np.float16)
+    B = rng.integers(-4, 5, (32, 16)).astype(np.float16)
+    D = torch.zeros((16, 16), dtype=torch.float32, device="cuda")
+    dA, dB = dev(A), dev(B)
+    _run(ctx, lambda: ctx.selftest_mfma(dA, dB, D))
+    ref = A.astype(np.float64) @ B.astype(np.float64)
+    assert (host(D) == ref).all()
+
+
+def test_qmv2_gemv_config0(ctx, orc):
+    """Single-token 2-bit GEMV: W [5632 x 2048], gs 64, x ~ N(0,1)."""
+    import torch
+
+    print("case: qmv2 cfg0 N=5632 K=2048 gs=64", flush=True)
+    rng = np.random.default_rng(100)
+    N, K, gs = 5632, 2048, 64
+    w, s, b = synth.qweight(rng, (1,), N, K, gs)
+    x = synth.normal_f16(rng, (1, K))
+    inds = np.zeros(1, np.int32)
+    ref = orc.qmm2(x, w, s, b, inds, 1, 1, K, N, gs)
+    y = torch.empty((1, N), dtype=torch.float16, device="cuda")
+    dx, dw, ds, db, di = dev(x), dev(w), dev(s), dev(b), dev(inds)
+    _run(ctx, lambda: ctx.gather_qmm2(dx, dw, ds, db, di, y, 1, 1, K, N, gs))
+    rel, mx = assert_close(host(y), ref, what="cfg0")
+    assert rel < 2e-3  # fp16 output rounding level
+    # float64 closed form as a second restatement
+    dense = synth.dequant(w[0], s[0], b[0], gs)
+    ref64 = dense @ x[0].astype(np.float64)
+    assert_close(host(y)[0], ref64, what="cfg0 vs f64")
+
+
+@pytest.mark.parametrize("case", ["up_gs64", "down_lhs", "gs128", "dense_add", "prefill_rows"])
+def test_gather_rows(ctx, orc, case):
+    import torch
+
+    print(f"case: gather {case}", flush=True)
+    rng = np.random.default_rng(hash(case) % 1000)
+    E, M, ktop, K, N, gs, lhs, epi = 16, 9, 8, 2048, 256, 64, False, 0
+    if case == "down_lhs":
+        K, lhs = 1024, True
+    elif case == "gs128":
+        gs = 128
+    elif case == "dense_add":
+        E, ktop, N, epi = 1, 1, 512, 1
+    elif case == "prefill_rows":
+        M, ktop, E = 40, 2, 4  # more rows per expert than one MFMA row group holds
+    w, s, b = synth.qweight(rng, (E,), N, K, gs)
+    x = synth.normal_f16(rng, (M * ktop if lhs else M, K))
+    inds = np.stack([rng.permutation(E)[:ktop] for _ in range(M)]).reshape(-1).astype(np.int32)
+    y0 = synth.normal_f16(rng, (M * ktop, N))
+    ref = orc.qmm2(x, w, s, b, inds, M, ktop, K, N, gs, lhs)
+    if epi == 1:
+        ref = (y0.astype(np.float32) + ref.astype(np.float32)).astype(np.float16)
+    y = dev(y0)
+    dx, dw, ds, db, di = dev(x), dev(w), dev(s), dev(b), dev(inds)
+    _run(ctx, lambda: ctx.gather_qmm2(dx, dw, ds, db, di, y, M, ktop, K, N, gs, lhs, epi))
+    rel, _ = assert_close(host(y), ref, what=case)
+    assert rel < 3e-3
+
+
+def _moe_data(rng, E, H, I, gs):
+    return synth.moe_weights(rng, E, H, I, gs)
+
+
+def _moe_dev(mw):
+    d = {k: (dev(v) if isinstance(v, np.ndarray) else v) for k, v in mw.items()}
+    return d
+
+
+@pytest.mark.parametrize("M,flags", [(1, 0), (8, 0), (8, 3), (1, 3), (17, 3)])
+def test_moe_block(ctx, orc, M, flags):
+    """Config 1 (M=1) and the K=8 verify rows of config 2 (M=8), and the pre-norm+residual form
+    used inside a layer: routing bit-exact, outputs within tolerance."""
+    import torch
+
+    print(f"case: moe M={M} flags={flags}", flush=True)
+    rng = np.random.default_rng(200 + M + flags)
+    E, H, I, gs, k = 64, 2048, 1024, 64, 8
+    mw = _moe_data(rng, E, H, I, gs)
+    x = synth.normal_f16(rng, (M, H))
+    ref_y, ref_i, ref_s = orc.moe_block(mw, x, prenorm=bool(flags & 1), residual=bool(flags & 2))
+    dmw = _moe_dev(mw)
+    dx = dev(x)
+    y = torch.empty_like(dx)
+    inds = torch.empty((M, k), dtype=torch.int32, device="cuda")
+    scores = torch.empty((M, k), dtype=torch.float32, device="cuda")
+    _run(ctx, lambda: ctx.moe_block(dmw, dx, y, M, flags, inds, scores))
+    gi = host(inds)
+    assert (gi == ref_i).all(), (gi, ref_i)
+    assert np.allclose(host(scores), ref_s, rtol=1e-4, atol=1e-5)
+    rel, _ = assert_close(host(y), ref_y, what=f"moe M={M}")
+    assert rel < 5e-3
+
+
+def test_abort_word_skips_work(ctx):
+    import torch
+
+    from momij_amd._lib import MomijError
+
+    rng = np.random.default_rng(5)
+    N, K, gs = 512, 2048, 64
+    w, s, b = synth.qweight(rng, (1,), N, K, gs)
+    x = synth.normal_f16(rng, (1, K))
+    y = torch.full((1, N), 7.0, dtype=torch.float16, device="cuda")
+    dx, dw, ds, db = dev(x), dev(w), dev(s), dev(b)
+    di = dev(np.zeros(1, np.int32))
+    torch.cuda.synchronize()
+    ctx.set_abort(True)
+    ctx.gather_qmm2(dx, dw, ds, db, di, y, 1, 1, K, N, gs)
+    with pytest.raises(MomijError) as e:
+        ctx.sync()
+    assert e.value.status == 5
+    ctx.set_abort(False)
+    ctx.sync()
+    assert (host(y) == 7.0).all()
+
+
+def test_shape_guards(ctx):
+    import torch
+
+    from momij_amd._lib import MomijError
+
+    t = torch.zeros(16, dtype=torch.int32, device="cuda")
+    with pytest.raises(MomijError) as e:
+        ctx.gather_qmm2(t, t, t, t, t, t, 1, 1, 1000, 64, 64)
+    assert e.value.status == 3
+    with pytest.raises(MomijError) as e:
+        ctx.gather_qmm2(t, t, t, t, t, t, 1, 1, 1024, 64, 96)
+    assert e.value.status == 3
