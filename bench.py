@@ -1,0 +1,285 @@
+#!/usr/bin/env python3
+"""Verify-step benchmark on one MI355X.
+
+Workload (the verify step of a 24-layer Maple-like 2-bit MoE): hidden 2048, 16 query / 4 KV
+heads of 128, sliding window 1024, RoPE base 1e6 on 64 dims, 64 experts top-8 with
+intermediate 1024, 2-bit affine experts and projections (group 64), fp16 lm_head [151936 x
+2048], RMSNorm eps 1e-6; random-init weights, a 2048-token seeded prompt prefilled into the KV
+cache.  One step = one verify pass over [y] + K=8 chain draft rows (the first 5 draft tokens
+are the target's greedy continuation, the other 3 random), device-side greedy acceptance and KV
+commit, one host wait.  Reported value = accepted tokens (accepted + bonus) per second.
+The 16-node depth-6 draft tree is measured the same way and reported under "tree".
+
+roofline: the dominant kernel is the bucketed up||gate expert gather; algorithmic bytes per
+launch = routed unique experts x 1,310,720 B (2-bit codes + fp16 scales/biases of 2048 x 2048)
++ activations, divided by its launch time from HIP events on the model stream.
+cpu_baseline: the CPU oracle (C restatement, OpenMP) on a bounded sample of the same step --
+2 of the 24 layers plus the full lm_head for the 9 verify rows, scaled to 24 layers.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+TREE16 = [-1, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 10, 11, 12, 13, 14]
+METRIC = "verify-step tokens/s (K=8, 1 GPU) + 2-bit gather-qmm HBM GB/s vs peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def greedy_continuation(eng, y, n):
+    L0 = eng.offset
+    out, t = [], y
+    for _ in range(n):
+        t = eng.step_chain_feeds([t])[0]
+        out.append(t)
+    eng.rewind(L0)
+    return out
+
+
+def tree_draft(cont, vocab, rng, depth_hit=4):
+    toks = [int(t) for t in rng.integers(0, vocab, len(TREE16) - 1)]
+    depth = [0] * len(TREE16)
+    for r in range(1, len(TREE16)):
+        depth[r] = depth[TREE16[r]] + 1
+    path = [0]
+    while True:
+        kids = [c for c in range(1, len(TREE16)) if TREE16[c] == path[-1]]
+        if not kids:
+            break
+        path.append(kids[0])
+    for d, r in enumerate(path[1:1 + depth_hit]):
+        toks[r - 1] = cont[d]
+    for r in range(1, len(TREE16)):
+        if r not in path[1:1 + depth_hit] and toks[r - 1] == cont[depth[r] - 1]:
+            toks[r - 1] = (toks[r - 1] + 1) % vocab
+    return toks
+
+
+def timed_steps(eng, y, draft, parents, L0, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        eng.rewind(L0)
+        eng.verify_greedy(y, draft, parents)
+    torch.cuda.synchronize()
+    toks, dev_ms = 0, 0.0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.rewind(L0)
+        acc, _ = eng.verify_greedy(y, draft, parents)
+        toks += acc + 1
+        dev_ms += eng.last_pass_ms()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return toks, dt, dev_ms / steps, acc
+
+
+def expert_bytes(cfg, inds_layers, M):
+    """Algorithmic bytes of one up||gate and one down launch per layer (unique experts once)."""
+    H, I, gs, k = cfg.H, cfg.I, cfg.gs, cfg.top_k
+    up_w = 2 * I * (H // 16 * 4 + 2 * (H // gs) * 2)
+    dn_w = H * (I // 16 * 4 + 2 * (I // gs) * 2)
+    up, dn, uniq = [], [], []
+    for l in range(cfg.n_layers):
+        eu = len(np.unique(inds_layers[l, :M]))
+        uniq.append(eu)
+        act = M * k * I * 2 + M * k * (I // 64) * 8
+        xin = M * H * 2 + M * (H // 64) * 8
+        up.append(eu * up_w + xin + act)
+        dn.append(eu * dn_w + act + M * k * H * 2)
+    return np.array(up), np.array(dn), np.array(uniq)
+
+
+def cpu_baseline(eng, cfg, weights, y, draft, L0):
+    """Oracle restatement timed on the host: layers 0-1 of the verify pass (from the GPU's own
+    layer inputs and KV cache) + the full fp16 lm_head for the 9 rows; scaled to 24 layers."""
+    import torch
+
+    from oracle import oracle as orc
+
+    orc.build()
+    layers, embed, fnorm, head = weights
+    M = len(draft) + 1
+    hcap = torch.empty((cfg.n_layers + 1, 64, cfg.H), dtype=torch.float16, device="cuda")
+    eng.rewind(L0)
+    kv0 = []
+    for l in range(2):
+        k, _ = eng.kv(l)
+        n = 2 * cfg.n_kv_heads * cfg.kv_capacity * 128
+        buf = np.empty(n, np.float16)
+        eng.ctx.check(eng.lib.mj_d2h(eng.ctx.h, buf.ctypes.data, k, n * 2))
+        kv0.append(buf.reshape(2, cfg.n_kv_heads, cfg.kv_capacity, 128))
+    eng.set_capture(h=hcap)
+    acc, _ = eng.verify_greedy(y, draft)
+    eng.set_capture()
+    hc = hcap.cpu().numpy()
+
+    def hw(d):
+        return {kk: (v.detach().cpu().numpy().view(np.uint32) if v.dtype == torch.int32 else
+                     v.detach().cpu().numpy()) if hasattr(v, "detach") else v
+                for kk, v in d.items()}
+
+    lw = [dict(attn=hw(layers[l]["attn"]), moe=hw(layers[l]["moe"])) for l in range(2)]
+    head_h = head.cpu().numpy()
+    fn = fnorm.cpu().numpy()
+    par = np.array(list(range(-1, M - 1)), np.int32)
+    t0 = time.perf_counter()
+    for l in range(2):
+        orc.layer_forward(cfg.attn_cfg(), lw[l], hc[l, :M], kv0[l][0], kv0[l][1], L0, par)
+    t_layers = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    xf = orc.rms_norm(hc[cfg.n_layers, :M], fn, cfg.eps)
+    logits = orc.lm_head_logits(xf, head_h)
+    orc.argmax_rows(logits)
+    t_head = time.perf_counter() - t0
+    step_s = t_layers / 2 * cfg.n_layers + t_head
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return dict(value=round((acc + 1) / step_s, 4), unit="tokens/s", cores=threads, kind="port",
+                sample=(f"oracle verify pass, layers 0-1 of 24 ({t_layers:.2f} s, teacher-forced "
+                        f"from the GPU layer inputs) + fp16 lm_head over 9 rows ({t_head:.2f} s), "
+                        f"scaled to 24 layers: {step_s:.2f} s/step, {acc + 1} tokens/step"))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--seed", type=int, default=2024)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X only (asked for --gpus {args.gpus}); the verify "
+              "step runs on a single GPU in this build", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from momij_amd.engine import MapleLikeConfig, VerifyEngine, random_model
+    from momij_amd.ops import Context
+
+    ctx = Context(0)
+    cfg = MapleLikeConfig()
+    t0 = time.perf_counter()
+    weights = random_model(cfg, seed=args.seed)
+    torch.cuda.synchronize()
+    eng = VerifyEngine(ctx, cfg, *weights)
+    log(f"model ready in {time.perf_counter() - t0:.1f}s")
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, cfg.vocab, 2048).tolist()
+    t0 = time.perf_counter()
+    y = eng.prefill(prompt, chunk=64)
+    log(f"prefill 2048 tokens in {time.perf_counter() - t0:.2f}s, offset {eng.offset}")
+    cont = greedy_continuation(eng, y, 8)
+    draft = cont[:5] + [int(t) for t in rng.integers(0, cfg.vocab, 3)]
+    for i in range(5, 8):
+        if draft[i] == cont[i]:
+            draft[i] = (draft[i] + 1) % cfg.vocab
+    L0 = eng.offset
+
+    # headline: chain K=8, graphs on
+    toks, dt, dev_ms, acc = timed_steps(eng, y, draft, None, L0, args.steps, args.warmup)
+    value = toks / dt
+    log(f"chain K=8: {value:.1f} tok/s, {dt / args.steps * 1e3:.3f} ms/step wall, "
+        f"{dev_ms:.3f} ms/step device, accepted {acc}")
+    # tree
+    tdraft = tree_draft(cont, cfg.vocab, rng)
+    ttoks, tdt, tdev, tacc = timed_steps(eng, y, tdraft, TREE16, L0, args.steps, args.warmup)
+    log(f"tree16: {ttoks / tdt:.1f} tok/s, {tdt / args.steps * 1e3:.3f} ms/step, accepted {tacc}")
+
+    # per-kernel times from HIP events (eager passes) and the routing of the pass
+    icap = torch.empty((cfg.n_layers, 64, cfg.top_k), dtype=torch.int32, device="cuda")
+    eng.rewind(L0)
+    eng.set_capture(inds=icap)
+    eng.verify_greedy(y, draft)
+    eng.set_capture()
+    inds = icap.cpu().numpy()
+    M = len(draft) + 1
+    up_b, dn_b, uniq = expert_bytes(cfg, inds, M)
+    prof_steps = max(5, min(args.steps, 20))
+    eng.profile(True)
+    for _ in range(prof_steps):
+        eng.rewind(L0)
+        eng.verify_greedy(y, draft)
+    km = eng.kernel_ms()
+    eng.profile(False)
+    up_ms, up_n = km["expert_up"]
+    dn_ms, dn_n = km["expert_down"]
+    hd_ms, hd_n = km["lm_head"]
+    up_gbs = up_b.sum() * prof_steps / (up_ms * 1e-3) / 1e9
+    dn_gbs = dn_b.sum() * prof_steps / (dn_ms * 1e-3) / 1e9
+    head_bytes = cfg.vocab * cfg.H * 2 + M * cfg.H * 2
+    hd_gbs = head_bytes * hd_n / (hd_ms * 1e-3) / 1e9
+    kernels = {name: dict(ms_per_launch=round(ms / max(n, 1), 5), launches=n)
+               for name, (ms, n) in km.items()}
+    kernels["expert_up"]["GBps"] = round(up_gbs, 1)
+    kernels["expert_down"]["GBps"] = round(dn_gbs, 1)
+    kernels["lm_head"]["GBps"] = round(hd_gbs, 1)
+    log(f"expert up {up_gbs:.0f} GB/s, down {dn_gbs:.0f} GB/s, head {hd_gbs:.0f} GB/s, "
+        f"unique experts/layer {uniq.mean():.1f}")
+
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(eng, cfg, weights, y, draft, L0)
+            log(f"cpu baseline {cpu}")
+        except Exception as e:  # the CPU leg is reported, never required
+            log(f"cpu baseline skipped: {e!r}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random-init weights, 2048-token random prompt)",
+        "config": {
+            "workload": "24-layer Maple-like 2-bit MoE verify step, K=8 chain draft "
+                        "(5 accepted + bonus), 2048-token prompt, window 1024",
+            "layers": cfg.n_layers, "hidden": cfg.H, "experts": cfg.E, "top_k": cfg.top_k,
+            "moe_intermediate": cfg.I, "group_size": cfg.gs, "vocab": cfg.vocab,
+            "verify_rows": M, "accepted": acc, "device_ms_per_step": round(dev_ms, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "expert up||gate bucketed gather (k_gather SWIGLU)",
+            "achieved": round(up_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(up_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": int(up_b.mean()),
+            "ms_per_launch": round(up_ms / max(up_n, 1), 5),
+        },
+        "cpu_baseline": cpu,
+        "tree": {"tokens_per_s": round(ttoks / tdt, 3), "ms_per_step": round(tdt / args.steps * 1e3, 4),
+                 "accepted": tacc, "rows": len(TREE16), "device_ms_per_step": round(tdev, 4)},
+        "kernels": kernels,
+        "unique_experts_per_layer": round(float(uniq.mean()), 2),
+    }
+    print(json.dumps(line), flush=True)
+    eng.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

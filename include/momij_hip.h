@@ -244,6 +244,17 @@ mj_status mj_model_set_graphs(mj_model* model, int enable);
 /* Per-pass device timing of the last verify call (ms), from HIP events on the model stream. */
 float mj_model_last_pass_ms(const mj_model* model);
 
+/* Per-kernel timing for measurement: when enabled, verify passes run without graphs and record
+ * HIP events around each launch of the classes below on the model stream (counters reset on
+ * every call).  mj_model_kernel_ms returns the summed milliseconds and the launch count. */
+#define MJ_KERNEL_EXPERT_UP 0   /* bucketed up||gate gather + SwiGLU */
+#define MJ_KERNEL_EXPERT_DOWN 1 /* bucketed down gather */
+#define MJ_KERNEL_LM_HEAD 2     /* fp16 lm_head + argmax partials */
+#define MJ_KERNEL_ATTENTION 3   /* split-K attention + combine */
+#define MJ_KERNEL_DENSE 4       /* qkv and o projections */
+mj_status mj_model_profile(mj_model* model, int enable);
+float mj_model_kernel_ms(const mj_model* model, int kernel_class, int64_t* launches);
+
 /* Hardware self-check of the MFMA operand layout the kernels rely on (16x16x32 f16):
  * D = A[16x32] * B[32x16] with A, B fp16 row-major device, D fp32 [16][16] device. */
 mj_status mj_selftest_mfma(mj_ctx* ctx, const void* A, const void* B, float* D);

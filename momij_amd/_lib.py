@@ -95,6 +95,8 @@ _SIGS = {
     "mj_model_set_graphs": (i32, [vp, i32]),
     "mj_model_last_pass_ms": (f32, [vp]),
     "mj_selftest_mfma": (i32, [vp, vp, vp, vp]),
+    "mj_model_profile": (i32, [vp, i32]),
+    "mj_model_kernel_ms": (f32, [vp, i32, C.POINTER(i64)]),
 }
 
 _lib = None

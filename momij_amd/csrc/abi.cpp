@@ -298,7 +298,8 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
 }
 
 mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
-                  int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st) {
+                  int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st,
+                  Prof* prof) {
     const int H = w->H, I = w->I, E = w->E, k = w->top_k;
     const int* ab = ctx->abort_dev;
     const uint16_t* xn = x;
@@ -372,7 +373,9 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         up.gs = w->gs;
         up.x_div = k;
         up.abort = ab;
+        if (prof) prof->begin(PROF_UP, st);
         s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, nb, st), "up gather");
+        if (prof) prof->end(st);
         if (s != MJ_OK) return s;
         GatherArgs dn{};
         dn.xperm = ms.act;
@@ -387,7 +390,9 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         dn.gs = w->gs;
         dn.x_div = 1;
         dn.abort = ab;
+        if (prof) prof->begin(PROF_DOWN, st);
         s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, nb, st), "down gather");
+        if (prof) prof->end(st);
         if (s != MJ_OK) return s;
     }
     return mj_hip(ctx, launch_score_combine(ms.down, scores,

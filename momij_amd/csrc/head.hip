@@ -1,0 +1,313 @@
+// head.hip -- exact fp16 lm_head verify, greedy acceptance, KV commit and token embedding.
+//
+// k_lm_head      maple_lm_head_argmax semantics (SeedlessMetal.swift:3005-3090) for an fp16
+//                head: logits[m][v] = sum_k w[v][k] x[m][k] (fp32), banned ids skipped, lowest
+//                id wins ties.  One 512-thread block per CU streams 16-row vocab strips through
+//                v_mfma_f32_16x16x32_f16 (A = 16 vocab rows x 32 k straight from HBM, B = the
+//                M <= 32 hidden rows staged once in LDS); per-lane running argmax, optional
+//                fp32 logits, one partial per (block, row).
+// k_head_final   maple_lm_head_reduce (3093-3111): folds the block partials per row.
+// k_accept_greedy verifyDraftChain's longest-prefix rule (SeedlessDecodeEngine.swift:1574-1603)
+//                walked over a draft tree: lowest-index child whose token equals the argmax.
+// k_kv_commit    keeps the accepted rows: the KV written at slot L + path[i] moves to L + i
+//                (SeedlessAttn.swift:219-270 rewinds the offset for append-only writes; a tree
+//                also needs the accepted path compacted into consecutive positions).
+#include "mj_device.h"
+#include "mj_internal.h"
+
+struct HeadArgs {
+    const uint16_t* x;   // [M][K] fp16
+    const uint16_t* w;   // [V][K] fp16
+    int M, K, V;
+    const int32_t* banned;
+    int n_banned;
+    float* logits;       // [M][V] or nullptr
+    float* pval;         // [blocks][32]
+    int* pidx;           // [blocks][32]
+    const int* abort;
+};
+
+template <int NT>
+__global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
+    if (aborted(a.abort)) return;
+    extern __shared__ uint16_t xs[];  // [NT*16][K + 8]
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int K = a.K, XS = K + 8;
+    for (int idx = t; idx < NT * 16 * (K / 8); idx += 512) {
+        const int m = idx / (K / 8), part = idx % (K / 8);
+        u4v v = {0u, 0u, 0u, 0u};
+        if (m < a.M) v = *(const u4v*)(a.x + (size_t)m * K + 8 * part);
+        *(u4v*)(xs + m * XS + 8 * part) = v;
+    }
+    __syncthreads();
+    const int ln = lane & 15, lq = lane >> 4;
+    const int nstrips = (a.V + 15) / 16;
+    const int TW = gridDim.x * 8;
+    float bv[NT];
+    int bi[NT];
+#pragma unroll
+    for (int tl = 0; tl < NT; ++tl) {
+        bv[tl] = -INFINITY;
+        bi[tl] = 0x7fffffff;
+    }
+    for (int strip = blockIdx.x * 8 + wv; strip < nstrips; strip += TW) {
+        const int v0 = strip * 16;
+        const int vr = v0 + ln;
+        const u4v* wr = (const u4v*)(a.w + (size_t)(vr < a.V ? vr : a.V - 1) * K) + lq;
+        f4 acc[NT];
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < K / 32; s0 += 8) {
+            u4v av[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) av[u] = wr[4 * (s0 + u)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                for (int tl = 0; tl < NT; ++tl) {
+                    const u4v xb =
+                        *(const u4v*)(xs + (tl * 16 + ln) * XS + 32 * (s0 + u) + 8 * lq);
+                    acc[tl] = mfma16x16x32(as_h8(av[u]), as_h8(xb), acc[tl]);
+                }
+            }
+        }
+        // lane holds logits for vocab v0 + 4*lq + r, row tl*16 + ln
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl) {
+            const int m = tl * 16 + ln;
+            if (m >= a.M) continue;
+            float vals[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int v = v0 + 4 * lq + r;
+                float s = acc[tl][r];
+                bool keep = v < a.V;
+                for (int b = 0; b < a.n_banned; ++b)
+                    if (a.banned[b] == v) keep = false;
+                vals[r] = s;
+                if (keep && (s > bv[tl] || (s == bv[tl] && v < bi[tl]))) {
+                    bv[tl] = s;
+                    bi[tl] = v;
+                }
+            }
+            if (a.logits) {
+                float* lp = a.logits + (size_t)m * a.V + v0 + 4 * lq;
+                if (v0 + 4 * lq + 3 < a.V) {
+                    *(float4*)lp = make_float4(vals[0], vals[1], vals[2], vals[3]);
+                } else {
+                    for (int r = 0; r < 4; ++r)
+                        if (v0 + 4 * lq + r < a.V) lp[r] = vals[r];
+                }
+            }
+        }
+    }
+    // reduce across lanes of the same row (lane, lane^16, lane^32, lane^48)
+#pragma unroll
+    for (int tl = 0; tl < NT; ++tl) {
+#pragma unroll
+        for (int o = 16; o < 64; o <<= 1) {
+            const float ov = __shfl_xor(bv[tl], o, MJ_WAVE);
+            const int oi = __shfl_xor(bi[tl], o, MJ_WAVE);
+            if (ov > bv[tl] || (ov == bv[tl] && oi < bi[tl])) {
+                bv[tl] = ov;
+                bi[tl] = oi;
+            }
+        }
+    }
+    __shared__ float sv[8][32];
+    __shared__ int si[8][32];
+    if (lane < 16) {
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl) {
+            sv[wv][tl * 16 + lane] = bv[tl];
+            si[wv][tl * 16 + lane] = bi[tl];
+        }
+    }
+    __syncthreads();
+    if (t < NT * 16 && t < a.M) {
+        float b = sv[0][t];
+        int i = si[0][t];
+        for (int w = 1; w < 8; ++w)
+            if (sv[w][t] > b || (sv[w][t] == b && si[w][t] < i)) {
+                b = sv[w][t];
+                i = si[w][t];
+            }
+        a.pval[(size_t)blockIdx.x * 32 + t] = b;
+        a.pidx[(size_t)blockIdx.x * 32 + t] = i;
+    }
+}
+
+// One wave per row: fold the block partials (value, lowest id on ties).
+__global__ __launch_bounds__(64) void k_head_final(const float* pval, const int* pidx, int nblk,
+                                                   int M, int32_t* out_idx, float* out_max,
+                                                   const int* abort) {
+    if (aborted(abort)) return;
+    const int m = blockIdx.x, lane = threadIdx.x;
+    if (m >= M) return;
+    float b = -INFINITY;
+    int i = 0x7fffffff;
+    for (int k = lane; k < nblk; k += 64) {
+        const float v = pval[(size_t)k * 32 + m];
+        const int j = pidx[(size_t)k * 32 + m];
+        if (v > b || (v == b && j < i)) {
+            b = v;
+            i = j;
+        }
+    }
+    wave_argmax(b, i);
+    if (lane == 0) {
+        out_idx[m] = i;
+        if (out_max) out_max[m] = b;
+    }
+}
+
+int head_blocks() { return 256; }
+
+// Rows go through in groups of <= 32 (two 16-row MFMA tiles staged in LDS per group).
+hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, int V,
+                          const int32_t* banned, int n_banned, float* logits, float* pval,
+                          int* pidx, int32_t* out_idx, float* out_max, const int* abort,
+                          hipStream_t st) {
+    const int nb = head_blocks();
+    for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mg = M - m0 < 32 ? M - m0 : 32;
+        HeadArgs a{x + (size_t)m0 * K, w, mg, K, V, banned, n_banned,
+                   logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
+        if (mg <= 16) {
+            const size_t lds = (size_t)16 * (K + 8) * 2;
+            hipLaunchKernelGGL(k_lm_head<1>, dim3(nb), dim3(512), lds, st, a);
+        } else {
+            const size_t lds = (size_t)32 * (K + 8) * 2;
+            hipLaunchKernelGGL(k_lm_head<2>, dim3(nb), dim3(512), lds, st, a);
+        }
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg,
+                           out_idx + m0, out_max ? out_max + m0 : nullptr, abort);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// ---------------------------------------------------------------------------------------
+// Greedy acceptance over rows 0..n-1 (row 0 = the fed token y).  tokens/parents from the
+// step descriptor (or explicit arrays), argmax per row.  Single thread: n <= 64.
+// ---------------------------------------------------------------------------------------
+__global__ void k_accept_greedy(const int32_t* tokens, const int32_t* parents,
+                                const int32_t* argmax, int n, StepResult* res,
+                                int32_t* out_flat, const int* abort) {
+    if (aborted(abort)) return;
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    int cur = 0, acc = 0;
+    int path[MJ_ROWS], emit[MJ_ROWS];
+    path[0] = 0;
+    for (;;) {
+        int next = -1;
+        for (int c = cur + 1; c < n; ++c)
+            if (parents[c] == cur && tokens[c] == argmax[cur]) {
+                next = c;
+                break;
+            }
+        if (next < 0) break;
+        emit[acc] = tokens[next];
+        ++acc;
+        path[acc] = next;
+        cur = next;
+    }
+    emit[acc] = argmax[cur];
+    if (res) {
+        res->accepted = acc;
+        res->token = argmax[cur];
+        for (int i = 0; i <= acc; ++i) {
+            res->path[i] = path[i];
+            res->emit[i] = emit[i];
+        }
+        for (int i = 0; i < n; ++i) res->argmax[i] = argmax[i];
+    }
+    if (out_flat) {
+        out_flat[0] = acc;
+        out_flat[1] = argmax[cur];
+        for (int i = 0; i <= acc; ++i) {
+            out_flat[2 + i] = path[i];
+            out_flat[2 + n + i] = emit[i];
+        }
+    }
+}
+
+hipError_t launch_accept_greedy(const int32_t* tokens, const int32_t* parents,
+                                const int32_t* argmax, int n, StepResult* res, int32_t* out_flat,
+                                const int* abort, hipStream_t st) {
+    hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64), 0, st, tokens, parents, argmax, n, res,
+                       out_flat, abort);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------
+// KV commit: block per (layer, kv head).  Reads every accepted row first, then writes.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_kv_commit(uint16_t* kv, int64_t layer_stride,
+                                                   int64_t C, int nKV, const StepDesc* sd,
+                                                   const StepResult* res, const int* abort) {
+    if (aborted(abort)) return;
+    const int acc = res->accepted;
+    const int layer = blockIdx.x / (2 * nKV), rest = blockIdx.x % (2 * nKV);
+    uint16_t* base = kv + layer * layer_stride + (int64_t)rest * C * 128;  // K heads then V heads
+    const int64_t L = sd->L;
+    __shared__ u4v rows[MJ_ROWS][16];
+    const int t = threadIdx.x;
+    bool moved = false;
+    for (int i = 1; i <= acc; ++i) moved |= res->path[i] != i;
+    if (!moved) return;
+    for (int idx = t; idx < (acc + 1) * 16; idx += 256) {
+        const int i = idx >> 4, part = idx & 15;
+        const int64_t src = (L + res->path[i]) % C;
+        rows[i][part] = *(const u4v*)(base + src * 128 + 8 * part);
+    }
+    __syncthreads();
+    for (int idx = t; idx < (acc + 1) * 16; idx += 256) {
+        const int i = idx >> 4, part = idx & 15;
+        const int64_t dst = (L + i) % C;
+        *(u4v*)(base + dst * 128 + 8 * part) = rows[i][part];
+    }
+}
+
+hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, int64_t C, int nKV,
+                            const StepDesc* sd, const StepResult* res, const int* abort,
+                            hipStream_t st) {
+    hipLaunchKernelGGL(k_kv_commit, dim3(n_layers * 2 * nKV), dim3(256), 0, st, kv, layer_stride,
+                       C, nKV, sd, res, abort);
+    return hipGetLastError();
+}
+
+// Token embedding: h[r] = table[tokens[r]] (maple_embed_token, SeedlessMetal.swift:3114-3126).
+__global__ __launch_bounds__(256) void k_embed(const uint16_t* table, const StepDesc* sd, int M,
+                                               int H, uint16_t* h, const int* abort) {
+    if (aborted(abort)) return;
+    const int r = blockIdx.x;
+    if (r >= M) return;
+    const int tok = sd->tokens[r];
+    for (int i = threadIdx.x; i < H / 8; i += 256)
+        *(u4v*)(h + (size_t)r * H + 8 * i) = *(const u4v*)(table + (size_t)tok * H + 8 * i);
+}
+
+hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
+                        const int* abort, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed, dim3(M), dim3(256), 0, st, table, sd, M, H, h, abort);
+    return hipGetLastError();
+}
+
+hipError_t set_attn_attributes();
+
+hipError_t set_kernel_attributes() {
+    static bool done = false;
+    if (done) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute((const void*)k_lm_head<1>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)k_lm_head<2>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
+    if (e == hipSuccess) e = set_attn_attributes();
+    if (e == hipSuccess) done = true;
+    return e;
+}

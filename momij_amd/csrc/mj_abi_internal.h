@@ -37,10 +37,29 @@ struct MoeScratch {
     uint16_t* down;      // [M*k][H]
 };
 
+// Optional per-kernel-class event timing of eager passes (classes of mj_model_kernel_ms).
+enum { PROF_UP = 0, PROF_DOWN = 1, PROF_HEAD = 2, PROF_ATTN = 3, PROF_DENSE = 4, PROF_CLASSES = 5 };
+struct Prof {
+    hipEvent_t* pool = nullptr;
+    int cap = 0, used = 0;
+    int cls[1024];
+    void begin(int c, hipStream_t st) {
+        if (!pool || used + 2 > cap) return;
+        cls[used / 2] = c;
+        hipEventRecord(pool[used], st);
+    }
+    void end(hipStream_t st) {
+        if (!pool || used + 2 > cap) return;
+        hipEventRecord(pool[used + 1], st);
+        used += 2;
+    }
+};
+
 mj_status mj_fail(mj_ctx* ctx, mj_status st, const char* fmt, ...);
 mj_status mj_hip(mj_ctx* ctx, hipError_t e, const char* what);
 mj_status mj_scratch_reserve(mj_ctx* ctx, size_t bytes);
 mj_status mj_check_abort(mj_ctx* ctx);
 mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms);
 mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
-                  int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st);
+                  int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st,
+                  Prof* prof = nullptr);

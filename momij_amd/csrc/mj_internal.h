@@ -18,6 +18,36 @@ struct Buckets {
 
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
 
+#define MJ_ROWS 64  // == MJ_MAX_ROWS of the C ABI
+
+// Per-pass parameters read by the kernels from device memory, so one captured graph serves
+// every step with the same row count.  Row r of a pass sits at position L + depth[r]; anc[r]
+// has bit a set iff row a is row r or one of its ancestors; tokens[r] is the token fed there.
+struct StepDesc {
+    int64_t L;
+    int32_t M;
+    int32_t pad0;
+    int32_t tokens[MJ_ROWS];
+    int32_t parents[MJ_ROWS];
+    int32_t depth[MJ_ROWS];
+    uint64_t anc[MJ_ROWS];
+    uint64_t seed, counter;  // sampled acceptance
+    float temperature;
+    float q_uniform;         // 1/V (q_mode uniform)
+    int32_t q_mode;
+    int32_t has_qpoint;
+    float q_point[MJ_ROWS];
+};
+
+// Result of a verify pass (device, copied back once per step).
+struct StepResult {
+    int32_t accepted;
+    int32_t token;           // bonus (greedy) / resampled or bonus (sampled)
+    int32_t path[MJ_ROWS];   // accepted rows, row 0 first
+    int32_t emit[MJ_ROWS];   // accepted drafts then the final token
+    int32_t argmax[MJ_ROWS];
+};
+
 struct GatherArgs {
     const uint16_t* xperm;  // qx activations [rows_x][K]
     const float2* xsum;     // [rows_x][K/64] {sum x, sum base*x}
@@ -51,6 +81,56 @@ hipError_t launch_qmv2(const QmvArgs& a, int epi, hipStream_t st);
 hipError_t launch_gather(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets_max,
                          hipStream_t st);
 hipError_t launch_selftest_mfma(const uint16_t* A, const uint16_t* B, float* D, hipStream_t st);
+
+struct AttnArgs {
+    const uint16_t* qkv;     // [M][(nQ+2nKV)*128] projection output (plain)
+    const uint16_t* q_norm_w;
+    const uint16_t* k_norm_w;
+    const float* inv_freq;   // [rope_dim/2]
+    const StepDesc* sd;
+    uint16_t* qbuf;          // [M][nQ][128] normed + rotated queries
+    uint16_t* kc;            // [nKV][C][128]
+    uint16_t* vc;
+    float* opart;            // [nKV][max_chunks][nqt*16][128] partial outputs
+    float2* mlpart;          // [nKV][max_chunks][nqt*16] {max, sum}
+    uint16_t* out_perm;      // attention output, qx [M][nQ*128]
+    float2* out_sum;         // [M][nQ*2]
+    int M, nQ, nKV, rope_dim, window, max_chunks;
+    int64_t C;
+    float eps, scale;
+    const int* abort;
+};
+
+// attn.hip
+hipError_t launch_qknorm_rope_kv(const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn(const AttnArgs& a, hipStream_t st);
+int attn_max_chunks(int window, int64_t L_max, int M);
+
+// head.hip
+hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, int V,
+                          const int32_t* banned, int n_banned, float* logits, float* pval,
+                          int* pidx, int32_t* out_idx, float* out_max, const int* abort,
+                          hipStream_t st);
+int head_blocks();
+hipError_t launch_accept_greedy(const int32_t* tokens, const int32_t* parents,
+                                const int32_t* argmax, int n, StepResult* res, int32_t* out_flat,
+                                const int* abort, hipStream_t st);
+hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, int64_t C, int nKV,
+                            const StepDesc* sd, const StepResult* res, const int* abort,
+                            hipStream_t st);
+hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
+                        const int* abort, hipStream_t st);
+
+// sample.hip
+hipError_t launch_accept_sampled(const float* logits, int rows, int V, const int32_t* draft,
+                                 float temperature, int q_mode, const float* q_point,
+                                 uint64_t seed, uint64_t counter, float* rowmax, float* bsum,
+                                 int32_t* out, StepResult* res, const StepDesc* sd,
+                                 const int* abort, hipStream_t st);
+int sample_nblocks(int V);
+
+// large-LDS kernels need their limit raised once per process
+hipError_t set_kernel_attributes();
 
 // moe.hip
 hipError_t launch_rmsnorm_qx(const uint16_t* x, const uint16_t* w, float eps, uint16_t* out_plain,

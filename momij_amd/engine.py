@@ -1,0 +1,176 @@
+"""VerifyEngine: the resident verify stack through the C ABI (mirrors SeedlessDecodeEngine's
+decode/verify surface: prefillPrompt, stepChainFeeds, verifyDraftChain, verifyDraftSampled --
+SeedlessDecodeEngine.swift:194-228, 516-545, 1541-1603).
+
+Weights are caller-owned torch device tensors in the MLX layout; the engine keeps them alive.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+from . import _lib
+from ._lib import LayerWeights, ModelConfig, MomijError
+from .ops import Context, ptr
+
+
+@dataclass
+class MapleLikeConfig:
+    n_layers: int = 24
+    H: int = 2048
+    n_heads: int = 16
+    n_kv_heads: int = 4
+    head_dim: int = 128
+    rope_dim: int = 64
+    rope_base: float = 1e6
+    eps: float = 1e-6
+    window: int = 1024
+    kv_capacity: int = 1024 + 64
+    E: int = 64
+    top_k: int = 8
+    I: int = 1024
+    gs: int = 64
+    vocab: int = 151936
+
+    def to_c(self) -> ModelConfig:
+        return ModelConfig(self.n_layers, self.H, self.n_heads, self.n_kv_heads, self.head_dim,
+                           self.rope_dim, self.rope_base, self.eps, self.window, self.kv_capacity,
+                           self.E, self.top_k, self.I, self.gs, self.vocab)
+
+    def attn_cfg(self) -> dict:
+        return dict(H=self.H, nQ=self.n_heads, nKV=self.n_kv_heads, D=self.head_dim,
+                    rope_dim=self.rope_dim, rope_base=self.rope_base, eps=self.eps,
+                    window=self.window, C=self.kv_capacity, gs=self.gs)
+
+
+class VerifyEngine:
+    def __init__(self, ctx: Context, cfg: MapleLikeConfig, layers: list, embed, final_norm_w,
+                 lm_head):
+        self.ctx = ctx
+        self.cfg = cfg
+        self.lib = ctx.lib
+        self._keep = (layers, embed, final_norm_w, lm_head)
+        arr = (LayerWeights * cfg.n_layers)()
+        for i, lw in enumerate(layers):
+            arr[i].attn = Context.attn_struct(lw["attn"])
+            arr[i].moe = Context.moe_struct(lw["moe"])
+        self._arr = arr
+        h = C.c_void_p()
+        c = cfg.to_c()
+        ctx.check(self.lib.mj_model_create(ctx.h, C.byref(c), C.cast(arr, C.c_void_p), ptr(embed),
+                                           ptr(final_norm_w), ptr(lm_head), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.mj_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------ state
+    @property
+    def offset(self) -> int:
+        return int(self.lib.mj_model_offset(self.h))
+
+    def rewind(self, offset: int):
+        self.ctx.check(self.lib.mj_model_rewind(self.h, offset))
+
+    def kv(self, layer: int):
+        k, v = C.c_void_p(), C.c_void_p()
+        self.ctx.check(self.lib.mj_model_kv(self.h, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def set_graphs(self, enable: bool):
+        self.ctx.check(self.lib.mj_model_set_graphs(self.h, int(enable)))
+
+    def set_capture(self, h=None, inds=None, logits=None):
+        self.ctx.check(self.lib.mj_model_set_capture(self.h, ptr(h), ptr(inds), ptr(logits)))
+
+    def last_pass_ms(self) -> float:
+        return float(self.lib.mj_model_last_pass_ms(self.h))
+
+    KERNEL_CLASSES = ("expert_up", "expert_down", "lm_head", "attention", "dense")
+
+    def profile(self, enable: bool):
+        self.ctx.check(self.lib.mj_model_profile(self.h, int(enable)))
+
+    def kernel_ms(self) -> dict:
+        out = {}
+        for i, name in enumerate(self.KERNEL_CLASSES):
+            n = C.c_int64()
+            ms = self.lib.mj_model_kernel_ms(self.h, i, C.byref(n))
+            out[name] = (float(ms), int(n.value))
+        return out
+
+    # ------------------------------------------------------------------ passes
+    def prefill(self, tokens, chunk: int = 64) -> int:
+        toks = (C.c_int32 * len(tokens))(*[int(t) for t in tokens])
+        nxt = C.c_int32()
+        self.ctx.check(self.lib.mj_prefill(self.h, toks, len(tokens), chunk, C.byref(nxt)))
+        return nxt.value
+
+    def step_chain_feeds(self, feeds) -> list[int]:
+        M = len(feeds)
+        f = (C.c_int32 * M)(*[int(t) for t in feeds])
+        ev = (C.c_int32 * M)()
+        self.ctx.check(self.lib.mj_step_chain_feeds(self.h, f, M, ev))
+        return list(ev)
+
+    def verify_greedy(self, y: int, draft, parents=None) -> tuple[int, list[int]]:
+        n = len(draft)
+        d = (C.c_int32 * max(n, 1))(*[int(t) for t in draft])
+        par = None
+        if parents is not None:
+            assert len(parents) == n + 1
+            par = (C.c_int32 * (n + 1))(*[int(p) for p in parents])
+        acc = C.c_int32()
+        out = (C.c_int32 * (n + 1))()
+        self.ctx.check(self.lib.mj_verify_greedy(self.h, int(y), d, n, par, C.byref(acc), out))
+        return acc.value, list(out[: acc.value + 1])
+
+    def verify_sampled(self, y: int, draft, temperature: float, q_mode: int, seed: int,
+                       counter: int, q_point=None) -> tuple[int, int]:
+        n = len(draft)
+        d = (C.c_int32 * max(n, 1))(*[int(t) for t in draft])
+        qp = None if q_point is None else (C.c_float * max(n, 1))(*[float(q) for q in q_point])
+        acc, tok = C.c_int32(), C.c_int32()
+        self.ctx.check(self.lib.mj_verify_sampled(self.h, int(y), d, n, temperature, q_mode, qp,
+                                                  seed, counter, C.byref(acc), C.byref(tok)))
+        return acc.value, tok.value
+
+
+def random_model(cfg: MapleLikeConfig, seed: int = 0, device: str = "cuda"):
+    """Random-init weights of the configuration on the device (same distributions as the
+    2-bit workloads); returns (layers, embed, final_norm_w, lm_head)."""
+    import torch
+
+    from . import synth
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    H, D, nQ, nKV = cfg.H, cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    layers = []
+    for _ in range(cfg.n_layers):
+        qw, qs, qb = synth.torch_qweight(gen, (), (nQ + 2 * nKV) * D, H, cfg.gs, device)
+        ow, os_, ob = synth.torch_qweight(gen, (), H, nQ * D, cfg.gs, device)
+        ugw, ugs, ugb = synth.torch_qweight(gen, (cfg.E,), 2 * cfg.I, H, cfg.gs, device)
+        dw, ds, db = synth.torch_qweight(gen, (cfg.E,), H, cfg.I, cfg.gs, device)
+
+        def norm_w(n):
+            return (1.0 + 0.1 * torch.randn(n, generator=gen, device=device)).half()
+
+        attn = dict(norm_w=norm_w(H), qkv_w=qw, qkv_s=qs, qkv_b=qb, q_norm_w=norm_w(D),
+                    k_norm_w=norm_w(D), o_w=ow, o_s=os_, o_b=ob)
+        moe = dict(norm_w=norm_w(H), router_w=synth.torch_normal(gen, (cfg.E, H), 0.02, device),
+                   up_gate_w=ugw, up_gate_s=ugs, up_gate_b=ugb, down_w=dw, down_s=ds, down_b=db,
+                   E=cfg.E, top_k=cfg.top_k, H=H, I=cfg.I, gs=cfg.gs, eps=cfg.eps)
+        layers.append(dict(attn=attn, moe=moe))
+    embed = synth.torch_normal(gen, (cfg.vocab, H), 0.02, device)
+    final_norm = (1.0 + 0.1 * torch.randn(H, generator=gen, device=device)).half()
+    lm_head = synth.torch_normal(gen, (cfg.vocab, H), 0.02, device)
+    return layers, embed, final_norm, lm_head

@@ -71,6 +71,7 @@ def lib():
         L.or_route_topk.argtypes = [vp, vp, vp, i, i, i]
         L.or_moe_block.argtypes = [vp, vp, vp, i, i, vp, vp]
         L.or_layer_forward.argtypes = [vp, vp, vp, vp, vp, vp, C.c_int64, vp, i, vp, vp]
+        L.or_attn_block.argtypes = [vp, vp, vp, vp, vp, vp, C.c_int64, vp, i]
         L.or_lm_head_logits.argtypes = [vp, vp, vp, i, i, i]
         L.or_argmax_rows.argtypes = [vp, i, i, vp, i, vp, vp, vp]
         L.or_accept_greedy.argtypes = [vp, vp, vp, i, vp, vp]
@@ -264,6 +265,21 @@ def attention(q, kcache, vcache, C_slots, L, parents, window):
 def make_cfg(cfg: dict) -> _Cfg:
     return _Cfg(cfg["H"], cfg["nQ"], cfg["nKV"], cfg["D"], cfg["rope_dim"], cfg["window"],
                 cfg["gs"], cfg["rope_base"], cfg["eps"], cfg["C"])
+
+
+def attn_block(cfg: dict, aw: dict, h, kcache, vcache, L, parents):
+    """Attention block with residual on copies; returns (h_out, kcache, vcache)."""
+    keep = []
+    st = _attn_struct(aw, keep)
+    c = make_cfg(cfg)
+    inv = rope_inv_freq(cfg["rope_dim"], cfg["rope_base"])
+    h = np.array(h, dtype=np.float16, copy=True, order="C")
+    kc = np.array(kcache, dtype=np.float16, copy=True, order="C")
+    vc = np.array(vcache, dtype=np.float16, copy=True, order="C")
+    par = _c(parents, np.int32)
+    lib().or_attn_block(C.byref(c), C.byref(st), inv.ctypes.data, h.ctypes.data, kc.ctypes.data,
+                        vc.ctypes.data, C.c_int64(L), par.ctypes.data, h.shape[0])
+    return h, kc, vc
 
 
 def layer_forward(cfg: dict, lw: dict, h, kcache, vcache, L, parents):

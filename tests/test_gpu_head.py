@@ -1,0 +1,176 @@
+"""GPU parity: exact fp16 lm_head verify (argmax, logits) and greedy / sampled acceptance.
+
+Config 3: lm_head fp16 [151936 x 2048] ~ N(0, 0.02), hidden fp16 [8 x 2048] ~ N(0, 1); drafts:
+the first 5 equal the target argmax, the rest random; sampled acceptance at T = 0.7 with
+Philox uniforms and a uniform (or point-mass) draft q.  Argmax ids, accepted lengths and
+emitted tokens are compared bit for bit; for the argmax the oracle's top-1/top-2 margin is
+checked to exceed the fp32 accumulation error bound, so the match is not luck.
+"""
+import numpy as np
+import pytest
+
+from tests.gpu_util import assert_close, dev, host
+
+pytestmark = pytest.mark.gpu
+
+V, K, M = 151936, 2048, 8
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from momij_amd.ops import Context
+
+    c = Context(0)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def head_case(ctx, orc):
+    import torch
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    w = (torch.randn((V, K), generator=gen, device="cuda") * 0.02).half()
+    x = torch.randn((M, K), generator=gen, device="cuda").half()
+    logits = torch.empty((M, V), dtype=torch.float32, device="cuda")
+    am = torch.empty(M, dtype=torch.int32, device="cuda")
+    mx = torch.empty(M, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.lm_head_verify(x, w, M, K, V, am, mx, logits)
+    ctx.sync()
+    wh, xh = host(w), host(x)
+    ref = orc.lm_head_logits(xh, wh)
+    return dict(w=w, x=x, logits=logits, am=host(am), mx=host(mx), ref=ref, wh=wh, xh=xh)
+
+
+def test_lm_head_config3(head_case, orc):
+    c = head_case
+    ref = c["ref"]
+    idx, best, second = orc.argmax_rows(ref)
+    # rounding bound of an fp32 sum of 2048 products (8 sqrt(K) eps sum|w x|) at the top-2
+    top2 = np.argsort(-ref, axis=1)[:, :2]
+    absdot = np.array([[np.abs(c["wh"][v].astype(np.float64) * c["xh"][m]).sum()
+                        for v in top2[m]] for m in range(M)])
+    bound = 8 * np.sqrt(K) * 2.0 ** -24 * absdot.max(1)
+    print("margins", (best - second).tolist(), "bound", bound.tolist(), flush=True)
+    assert ((best - second) > bound).all()
+    assert (c["am"] == idx).all(), (c["am"], idx)
+    got = host(c["logits"])
+    assert_close(got, ref, rel_tol=1e-5, abs_tol=1e-4, what="cfg3 logits")
+    assert (c["mx"] == got.max(1)).all()
+
+
+def test_lm_head_banned_and_ties(ctx):
+    import torch
+
+    Vs, Ks, Ms = 4096, 256, 3
+    w = torch.zeros((Vs, Ks), dtype=torch.float16, device="cuda")
+    x = torch.ones((Ms, Ks), dtype=torch.float16, device="cuda")
+    w[[17, 900, 901, 4000], 0] = 1.0  # four tied maxima
+    am = torch.empty(Ms, dtype=torch.int32, device="cuda")
+    banned = torch.tensor([17, 901], dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.lm_head_verify(x, w, Ms, Ks, Vs, am)
+    ctx.sync()
+    assert host(am).tolist() == [17, 17, 17]
+    ctx.lm_head_verify(x, w, Ms, Ks, Vs, am, banned=banned, n_banned=2)
+    ctx.sync()
+    assert host(am).tolist() == [900, 900, 900]
+
+
+@pytest.mark.parametrize("Ms", [17, 36, 64])
+def test_lm_head_many_rows(ctx, orc, Ms):
+    """17 verify rows (a 16-node tree + root) use the two-tile path; 36 and 64 rows (prefill
+    chunks) go through in groups of 32."""
+    import torch
+
+    rng = np.random.default_rng(9 + Ms)
+    Vs = 20000
+    w = (rng.standard_normal((Vs, K)) * 0.02).astype(np.float16)
+    x = rng.standard_normal((Ms, K)).astype(np.float16)
+    am = torch.empty(Ms, dtype=torch.int32, device="cuda")
+    lg = torch.empty((Ms, Vs), dtype=torch.float32, device="cuda")
+    dw, dx = dev(w), dev(x)
+    torch.cuda.synchronize()
+    ctx.lm_head_verify(dx, dw, Ms, K, Vs, am, None, lg)
+    ctx.sync()
+    ref = orc.lm_head_logits(x, w)
+    idx, _, _ = orc.argmax_rows(ref)
+    assert (host(am) == idx).all()
+    assert_close(host(lg), ref, rel_tol=1e-5, abs_tol=1e-4, what=f"{Ms} rows")
+
+
+def test_accept_greedy_config3(ctx, head_case, orc):
+    import torch
+
+    am = head_case["am"]
+    rng = np.random.default_rng(11)
+    draft = am[:M - 1].copy()
+    for i in range(5, M - 1):
+        while draft[i] == am[i]:
+            draft[i] = rng.integers(0, V)
+    tokens = np.concatenate([[123], draft]).astype(np.int32)
+    out = torch.empty(2 + 2 * M, dtype=torch.int32, device="cuda")
+    dt, da = dev(tokens), dev(am.astype(np.int32))
+    torch.cuda.synchronize()
+    ctx.accept_greedy(dt, None, da, M, out)
+    ctx.sync()
+    o = host(out)
+    acc, path, emit = orc.accept_greedy(tokens, None, am)
+    assert acc == 5 and o[0] == acc and o[1] == am[acc]
+    assert list(o[2:3 + acc]) == list(path) and list(o[2 + M:3 + M + acc]) == list(emit)
+
+
+def test_accept_greedy_trees(ctx, orc):
+    import torch
+
+    rng = np.random.default_rng(12)
+    for trial in range(30):
+        n = int(rng.integers(1, 20))
+        parents = [-1] + [int(rng.integers(0, r)) for r in range(1, n)]
+        argmax = rng.integers(0, 5, n).astype(np.int32)
+        tokens = rng.integers(0, 5, n).astype(np.int32)
+        out = torch.empty(2 + 2 * n, dtype=torch.int32, device="cuda")
+        dt, da = dev(tokens), dev(argmax)
+        torch.cuda.synchronize()
+        ctx.accept_greedy(dt, parents, da, n, out)
+        ctx.sync()
+        o = host(out)
+        acc, path, emit = orc.accept_greedy(tokens, parents, argmax)
+        assert o[0] == acc and list(o[2:3 + acc]) == list(path), trial
+        assert list(o[2 + n:3 + n + acc]) == list(emit), trial
+
+
+@pytest.mark.parametrize("q_mode,temp", [(1, 0.7), (0, 0.7), (0, 0.1)])
+def test_accept_sampled_bit_exact(ctx, head_case, orc, q_mode, temp):
+    """Device rejection sampling == the oracle's canonical rule on the same logits and Philox
+    uniforms: accepted count and emitted token, for many counters.  Uniform q at T = 0.7 is the
+    config-3 case; a point-mass q (the reference default) accepts only where p is large, so it
+    also runs at T = 0.1."""
+    import torch
+
+    am = head_case["am"]
+    logits = head_case["logits"]
+    lh = host(logits)
+    rng = np.random.default_rng(13 + q_mode)
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    seen = {}
+    for trial in range(24):
+        draft = am[:M - 1].copy()
+        for i in range(5, M - 1):
+            draft[i] = rng.integers(0, V)
+        if trial % 3 == 0:
+            draft[int(rng.integers(0, 5))] = rng.integers(0, V)  # early reject
+        dd = dev(draft.astype(np.int32))
+        torch.cuda.synchronize()
+        ctx.accept_sampled(logits, M, V, dd, temp, q_mode, 2024, trial, out)
+        ctx.sync()
+        got = tuple(int(v) for v in host(out))
+        u = orc.verify_uniforms(2024, trial, M)
+        ref = orc.accept_sampled(lh, draft, temp, q_mode, u)
+        assert got == ref, (trial, got, ref)
+        seen[ref[0]] = seen.get(ref[0], 0) + 1
+    print("accepted-count histogram", seen, flush=True)
+    if temp < 0.5 or q_mode == 1:
+        assert len(seen) >= 2  # both early rejects and long accepts were exercised
