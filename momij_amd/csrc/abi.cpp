@@ -188,6 +188,10 @@ mj_status mj_gather_qmm2(mj_ctx* ctx, const void* x, const uint32_t* w, const vo
     if (epilogue == MJ_EPI_ADD && ktop != 1)
         return mj_fail(ctx, MJ_INVALID_ARG, "gather_qmm2: MJ_EPI_ADD needs ktop == 1");
     hipSetDevice(ctx->device);
+    {
+        mj_status sa = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
+        if (sa != MJ_OK) return sa;
+    }
     const int P = M * ktop;
     if (P == 1 && epilogue == MJ_EPI_STORE && (K == 1024 || K == 2048 || K == 4096)) {
         QmvArgs a{};
@@ -255,6 +259,10 @@ mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void
                        "moe_block: unsupported shape H=%d I=%d E=%d top_k=%d gs=%d", H, I, E, k,
                        gs);
     hipSetDevice(ctx->device);
+    {
+        mj_status sa = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
+        if (sa != MJ_OK) return sa;
+    }
     MoeScratch ms;
     mj_status s = moe_scratch(ctx, H, I, E, k, M, ms);
     if (s != MJ_OK) return s;

@@ -298,6 +298,7 @@ hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H,
 }
 
 hipError_t set_attn_attributes();
+hipError_t set_gather_attributes();
 
 hipError_t set_kernel_attributes() {
     static bool done = false;
@@ -308,6 +309,7 @@ hipError_t set_kernel_attributes() {
         e = hipFuncSetAttribute((const void*)k_lm_head<2>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
+    if (e == hipSuccess) e = set_gather_attributes();
     if (e == hipSuccess) done = true;
     return e;
 }

@@ -41,6 +41,13 @@ __device__ __forceinline__ void unpack16(uint32_t w, uint32_t v[8]) {
     v[7] = (s4 & 0x03000300u) | 0x44004400u;
 }
 
+// Value the optimiser cannot see through: keeps loop-invariant code expansion from being
+// hoisted out of a loop (and held live across it) when registers are the scarce resource.
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // base of permuted pair i (16 for even code index, 4 for odd)
 __device__ __forceinline__ float code_base(int i) { return (i & 1) ? 4.0f : 16.0f; }
 
