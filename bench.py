@@ -160,6 +160,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--copy-calib-mb", type=int, default=0,
+                    help="end with one plain device copy of this many MiB (a known-size "
+                         "reference for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only (asked for --gpus {args.gpus}); the verify "
@@ -277,6 +280,14 @@ def main():
         "unique_experts_per_layer": round(float(uniq.mean()), 2),
     }
     print(json.dumps(line), flush=True)
+    if args.copy_calib_mb > 0:
+        n = args.copy_calib_mb << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {n} bytes")
     eng.close()
     ctx.close()
 

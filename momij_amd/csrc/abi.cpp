@@ -42,6 +42,8 @@ mj_status mj_scratch_reserve(mj_ctx* ctx, size_t bytes) {
     const size_t want = bytes + (bytes >> 2) + 4096;
     s = mj_hip(ctx, hipMalloc(&ctx->scratch, want), "scratch alloc");
     if (s != MJ_OK) return s;
+    s = mj_hip(ctx, hipMemset(ctx->scratch, 0, want), "scratch clear");
+    if (s != MJ_OK) return s;
     ctx->scratch_bytes = want;
     return MJ_OK;
 }
@@ -312,19 +314,43 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
     const int* ab = ctx->abort_dev;
     const uint16_t* xn = x;
     mj_status s;
+    const bool fused = route_supported(H, E, k);
+    if (fused) {
+        RouteArgs ra{};
+        ra.x = x;
+        ra.norm_w = (flags & MJ_MOE_PRENORM) ? (const uint16_t*)w->norm_w : nullptr;
+        ra.W = (const uint16_t*)w->router_w;
+        ra.xn = (M == 1 && (flags & MJ_MOE_PRENORM)) ? ms.xn : nullptr;
+        ra.xperm = M > 1 ? ms.xperm : nullptr;
+        ra.xsum = M > 1 ? ms.xsum : nullptr;
+        ra.inds = inds;
+        ra.scores = scores;
+        ra.bk = M > 1 ? ms.bk : nullptr;
+        ra.M = M;
+        ra.E = E;
+        ra.k = k;
+        ra.eps = w->eps;
+        ra.abort = ab;
+        s = mj_hip(ctx, launch_route(ra, H, st), "route");
+        if (s != MJ_OK) return s;
+        if (M == 1 && (flags & MJ_MOE_PRENORM)) xn = ms.xn;
+    }
     if (M == 1) {
-        if (flags & MJ_MOE_PRENORM) {
+        if (fused) {
+        } else if (flags & MJ_MOE_PRENORM) {
             s = mj_hip(ctx, launch_rmsnorm_qx(x, (const uint16_t*)w->norm_w, w->eps, ms.xn,
                                               nullptr, nullptr, 1, H, ab, st), "rmsnorm");
             if (s != MJ_OK) return s;
             xn = ms.xn;
         }
-        s = mj_hip(ctx, launch_router((const uint16_t*)w->router_w, xn, ms.logits, 1, E, H, ab,
-                                      st), "router");
-        if (s != MJ_OK) return s;
-        s = mj_hip(ctx, launch_topk_bucket(ms.logits, 1, E, k, inds, scores, nullptr, ab, st),
-                   "topk");
-        if (s != MJ_OK) return s;
+        if (!fused) {
+            s = mj_hip(ctx, launch_router((const uint16_t*)w->router_w, xn, ms.logits, 1, E, H,
+                                          ab, st), "router");
+            if (s != MJ_OK) return s;
+            s = mj_hip(ctx, launch_topk_bucket(ms.logits, 1, E, k, inds, scores, nullptr, ab, st),
+                       "topk");
+            if (s != MJ_OK) return s;
+        }
         QmvArgs up{};
         up.x = xn;
         up.w = w->up_gate_w;
@@ -352,20 +378,22 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         s = mj_hip(ctx, launch_qmv2(dn, EPI_STORE, st), "down qmv");
         if (s != MJ_OK) return s;
     } else {
-        if (flags & MJ_MOE_PRENORM) {
-            s = mj_hip(ctx, launch_rmsnorm_qx(x, (const uint16_t*)w->norm_w, w->eps, ms.xn,
-                                              ms.xperm, ms.xsum, M, H, ab, st), "rmsnorm");
-            xn = ms.xn;
-        } else {
-            s = mj_hip(ctx, launch_qx_prep(x, ms.xperm, ms.xsum, M, H, ab, st), "qx prep");
+        if (!fused) {
+            if (flags & MJ_MOE_PRENORM) {
+                s = mj_hip(ctx, launch_rmsnorm_qx(x, (const uint16_t*)w->norm_w, w->eps, ms.xn,
+                                                  ms.xperm, ms.xsum, M, H, ab, st), "rmsnorm");
+                xn = ms.xn;
+            } else {
+                s = mj_hip(ctx, launch_qx_prep(x, ms.xperm, ms.xsum, M, H, ab, st), "qx prep");
+            }
+            if (s != MJ_OK) return s;
+            s = mj_hip(ctx, launch_router((const uint16_t*)w->router_w, xn, ms.logits, M, E, H,
+                                          ab, st), "router");
+            if (s != MJ_OK) return s;
+            s = mj_hip(ctx, launch_topk_bucket(ms.logits, M, E, k, inds, scores, ms.bk, ab, st),
+                       "topk");
+            if (s != MJ_OK) return s;
         }
-        if (s != MJ_OK) return s;
-        s = mj_hip(ctx, launch_router((const uint16_t*)w->router_w, xn, ms.logits, M, E, H, ab,
-                                      st), "router");
-        if (s != MJ_OK) return s;
-        s = mj_hip(ctx, launch_topk_bucket(ms.logits, M, E, k, inds, scores, ms.bk, ab, st),
-                   "topk");
-        if (s != MJ_OK) return s;
         const int nb = M * k < E ? M * k : E;
         GatherArgs up{};
         up.xperm = ms.xperm;

@@ -82,7 +82,6 @@ hipError_t launch_qknorm_rope_kv(const AttnArgs& a, hipStream_t st) {
 }
 
 __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
-    if (aborted(a.abort)) return;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int g = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
     const StepDesc* sd = a.sd;
@@ -101,62 +100,78 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     uint16_t* Ps = Vt + HD * VSTR;               // [4 waves][16][VSTR]
     int64_t* kpos = (int64_t*)(Ps + 4 * 16 * VSTR);
     int* ktree = (int*)(kpos + AK);
-    int* kslot = ktree + AK;
+    int* s_abort = ktree + AK;
 
-    // keys of this chunk
+    // Every load of the block is issued before the first wait: this thread's K/V quarter row
+    // (key kk = t / 4, dims 32 (t % 4) ..), its share of the Q rows, and the key metadata.
+    const int kk = t >> 2, dq = t & 3;
+    const int64_t ki = (int64_t)c * AK + kk;
+    const bool kvalid = ki < nk;
+    int64_t kslot_v = 0;
+    if (kvalid) kslot_v = (ki < ncm ? lo_min + ki : L + (ki - ncm)) % a.C;
+    u4v kv[4], vv[4];
+    {
+        const size_t base = ((size_t)g * a.C + kslot_v) * HD + 32 * dq;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            kv[q] = (u4v){0u, 0u, 0u, 0u};
+            vv[q] = (u4v){0u, 0u, 0u, 0u};
+            if (kvalid) {
+                kv[q] = *(const u4v*)(a.kc + base + 8 * q);
+                vv[q] = *(const u4v*)(a.vc + base + 8 * q);
+            }
+        }
+    }
     if (t < AK) {
         const int64_t i = (int64_t)c * AK + t;
-        int64_t pos = INT64_MIN / 2, slot = 0;
+        int64_t pos = INT64_MIN / 2;
         int tree = -2;  // -2 invalid, -1 committed, >=0 tree row
         if (i < nk) {
             if (i < ncm) {
                 pos = lo_min + i;
-                slot = pos % a.C;
                 tree = -1;
             } else {
                 const int ar = (int)(i - ncm);
-                slot = (L + ar) % a.C;
                 pos = L + sd->depth[ar];
                 tree = ar;
             }
         }
         kpos[t] = pos;
         ktree[t] = tree;
-        kslot[t] = (int)slot;
     }
-    // Q rows of this kv group: qv = r * gqa + j  <-  head g*gqa + j of row r
-    for (int idx = t; idx < nqt * 16 * 16; idx += 256) {
-        const int qv = idx >> 4, part = idx & 15;
-        u4v v = {0u, 0u, 0u, 0u};
-        if (qv < nqv) {
-            const int r = qv / gqa, j = qv % gqa;
-            v = *(const u4v*)(a.qbuf + ((size_t)r * a.nQ + g * gqa + j) * HD + 8 * part);
-        }
-        *(u4v*)(Qs + qv * QSTR + 8 * part) = v;
-    }
-    __syncthreads();
-    // K rows and V transposed
-    {
-        const int kk = t >> 2, dq = t & 3;
-        const bool valid = ktree[kk] != -2;
-        const size_t base = ((size_t)g * a.C + (valid ? kslot[kk] : 0)) * HD + 32 * dq;
+    // Q rows of this kv group: qv = r * gqa + j  <-  head g*gqa + j of row r; four 16-byte
+    // parts per thread per round
+    for (int base = 0; base < nqt * 256; base += 1024) {
+        u4v qv4[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            u4v kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-            if (valid) {
-                kv = *(const u4v*)(a.kc + base + 8 * q);
-                vv = *(const u4v*)(a.vc + base + 8 * q);
-            }
-            *(u4v*)(Ks + kk * QSTR + 32 * dq + 8 * q) = kv;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int d = 32 * dq + 8 * q + 2 * j;
-                Vt[d * VSTR + kk] = (uint16_t)(vv[j] & 0xFFFFu);
-                Vt[(d + 1) * VSTR + kk] = (uint16_t)(vv[j] >> 16);
+        for (int j = 0; j < 4; ++j) {
+            const int idx = base + t + 256 * j;
+            const int qv = idx >> 4, part = idx & 15;
+            qv4[j] = (u4v){0u, 0u, 0u, 0u};
+            if (idx < nqt * 256 && qv < nqv) {
+                const int r = qv / gqa, jj = qv % gqa;
+                qv4[j] = *(const u4v*)(a.qbuf + ((size_t)r * a.nQ + g * gqa + jj) * HD + 8 * part);
             }
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int idx = base + t + 256 * j;
+            if (idx < nqt * 256) *(u4v*)(Qs + (idx >> 4) * QSTR + 8 * (idx & 15)) = qv4[j];
+        }
     }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        *(u4v*)(Ks + kk * QSTR + 32 * dq + 8 * q) = kv[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = 32 * dq + 8 * q + 2 * j;
+            Vt[d * VSTR + kk] = (uint16_t)(vv[q][j] & 0xFFFFu);
+            Vt[(d + 1) * VSTR + kk] = (uint16_t)(vv[q][j] >> 16);
+        }
+    }
+    if (t == 0) *s_abort = a.abort ? *a.abort : 0;
     __syncthreads();
+    if (*s_abort) return;  // block-uniform
 
     const int ln = lane & 15, lq = lane >> 4;
     uint16_t* Pw = Ps + wv * 16 * VSTR;
@@ -246,93 +261,81 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     }
 }
 
-// One wave per (row, group of 4 query heads): lane = head (lane/16) x 8 dims (lane%16).
+// One 256-thread block per (row, query head): wave w merges chunks w, w + 4, ... (lane = two
+// dims), then the four wave sums are added in wave order and the row is written in qx order.
+// Every chunk below the row's count holds a partial (a fully masked one has max -inf, sum 0).
 __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
-    if (aborted(a.abort)) return;
-    const int lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int hgroups = a.nQ / 4;
-    const int r = gw / hgroups, hg = gw % hgroups;
-    if (r >= a.M) return;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int r = blockIdx.x / a.nQ, hq = blockIdx.x % a.nQ;
     const int gqa = a.nQ / a.nKV;
-    const int hq = hg * 4 + (lane >> 4), d0 = 8 * (lane & 15);
     const int g = hq / gqa, qv = r * gqa + (hq % gqa);
-    const int nqt = (a.M * gqa + 15) / 16;
+    const size_t nq16 = (size_t)((a.M * gqa + 15) / 16) * 16;
     const int64_t L = a.sd->L;
     const int64_t lo_min = a.window > 0 ? (L - a.window + 1 > 0 ? L - a.window + 1 : 0) : 0;
     const int64_t nk = (L - lo_min) + a.M;
     const int nch = (int)((nk + AK - 1) / AK);
+    const float2* ml = a.mlpart + (size_t)g * a.max_chunks * nq16 + qv;
+    const float* op = a.opart + ((size_t)g * a.max_chunks * nq16 + qv) * HD + 2 * lane;
     float mx = -INFINITY;
-    for (int c = 0; c < nch; ++c) {
-        const float2 ml = a.mlpart[((size_t)g * a.max_chunks + c) * (nqt * 16) + qv];
-        mx = fmaxf(mx, ml.x);
-    }
-    float lsum = 0.0f, o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int c = 0; c < nch; ++c) {
-        const size_t idx = ((size_t)g * a.max_chunks + c) * (nqt * 16) + qv;
-        const float2 ml = a.mlpart[idx];
-        if (ml.x == -INFINITY) continue;
-        const float w = expf(ml.x - mx);
-        lsum += ml.y * w;
-        const float4* op = (const float4*)(a.opart + idx * HD + d0);
-        const float4 p0 = op[0], p1 = op[1];
-        o[0] += w * p0.x;
-        o[1] += w * p0.y;
-        o[2] += w * p0.z;
-        o[3] += w * p0.w;
-        o[4] += w * p1.x;
-        o[5] += w * p1.y;
-        o[6] += w * p1.z;
-        o[7] += w * p1.w;
-    }
-    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    u4v ov;
+    for (int c = lane; c < nch; c += 64) mx = fmaxf(mx, ml[(size_t)c * nq16].x);
+    mx = wave_max(mx);
+    float o0 = 0.0f, o1 = 0.0f, ls = 0.0f;
+    for (int c0 = wv; c0 < nch; c0 += 16) {
+        float2 m4[4], p4[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        ov[j] = (uint32_t)f2h(o[2 * j] * inv) | ((uint32_t)f2h(o[2 * j + 1] * inv) << 16);
-    // qx emit: lanes in aligned groups of 8 hold one 64-block
-    u4v ox;
-    ox.x = __shfl_xor(ov.x, 1, MJ_WAVE);
-    ox.y = __shfl_xor(ov.y, 1, MJ_WAVE);
-    ox.z = __shfl_xor(ov.z, 1, MJ_WAVE);
-    ox.w = __shfl_xor(ov.w, 1, MJ_WAVE);
-    const bool odd = lane & 1;
-    const uint32_t u[8] = {odd ? ox.x : ov.x, odd ? ox.y : ov.y, odd ? ox.z : ov.z, odd ? ox.w : ov.w,
-                           odd ? ov.x : ox.x, odd ? ov.y : ox.y, odd ? ov.z : ox.z, odd ? ov.w : ox.w};
-    uint32_t p[8];
-    perm16(u, p);
-    u4v pv;
-    pv.x = odd ? p[4] : p[0];
-    pv.y = odd ? p[5] : p[1];
-    pv.z = odd ? p[6] : p[2];
-    pv.w = odd ? p[7] : p[3];
-    const int K = a.nQ * HD;
-    const int k0 = hq * HD + d0;
-    *(u4v*)(a.out_perm + (size_t)r * K + k0) = pv;
-    float X = 0.0f, Bx = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+            const int c = c0 + 4 * j;
+            m4[j] = make_float2(-INFINITY, 0.0f);
+            p4[j] = make_float2(0.0f, 0.0f);
+            if (c < nch) {
+                m4[j] = ml[(size_t)c * nq16];
+                p4[j] = *(const float2*)(op + (size_t)c * nq16 * HD);
+            }
+        }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        X = dot2(ov[j], 0x3C003C00u, X);
-        Bx = dot2(ov[j], 0x44004C00u, Bx);
+        for (int j = 0; j < 4; ++j) {
+            const float w = m4[j].x == -INFINITY ? 0.0f : expf(m4[j].x - mx);
+            ls += m4[j].y * w;
+            o0 += w * p4[j].x;
+            o1 += w * p4[j].y;
+        }
     }
+    __shared__ float s_o[4][HD];
+    __shared__ float s_l[4];
+    __shared__ int s_abort;
+    s_o[wv][2 * lane] = o0;
+    s_o[wv][2 * lane + 1] = o1;
+    if (lane == 0) s_l[wv] = ls;
+    if (tid == 0) s_abort = a.abort ? *a.abort : 0;
+    __syncthreads();
+    if (s_abort) return;
+    if (tid < 16) {
+        const float lsum = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        u4v ov;
 #pragma unroll
-    for (int m = 1; m < 8; m <<= 1) {
-        X += __shfl_xor(X, m, MJ_WAVE);
-        Bx += __shfl_xor(Bx, m, MJ_WAVE);
+        for (int j = 0; j < 4; ++j) {
+            const int d = 8 * tid + 2 * j;
+            const float v0 = (((s_o[0][d] + s_o[1][d]) + s_o[2][d]) + s_o[3][d]) * inv;
+            const float v1 =
+                (((s_o[0][d + 1] + s_o[1][d + 1]) + s_o[2][d + 1]) + s_o[3][d + 1]) * inv;
+            ov[j] = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
+        }
+        const int K = a.nQ * HD;
+        emit_qx(ov, tid, a.out_perm + (size_t)r * K, a.out_sum + (size_t)r * (K / 64),
+                hq * HD + 8 * tid);
     }
-    if ((lane & 7) == 0) a.out_sum[(size_t)r * (K / 64) + (k0 >> 6)] = make_float2(X, Bx);
 }
 
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
     const int gqa = a.nQ / a.nKV;
     const int nqt = (a.M * gqa + 15) / 16;
     const size_t lds = (size_t)(nqt * 16 * QSTR + AK * QSTR + HD * VSTR + 4 * 16 * VSTR) * 2 +
-                       AK * (8 + 4 + 4);
+                       AK * (8 + 4) + 16;
     hipLaunchKernelGGL(k_attn_chunk, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int waves = a.M * (a.nQ / 4);
-    hipLaunchKernelGGL(k_attn_combine, dim3((waves + 3) / 4), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.M * a.nQ), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -299,6 +299,7 @@ hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H,
 
 hipError_t set_attn_attributes();
 hipError_t set_gather_attributes();
+hipError_t set_moe_attributes();
 
 hipError_t set_kernel_attributes() {
     static bool done = false;
@@ -310,6 +311,7 @@ hipError_t set_kernel_attributes() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
     if (e == hipSuccess) e = set_gather_attributes();
+    if (e == hipSuccess) e = set_moe_attributes();
     if (e == hipSuccess) done = true;
     return e;
 }

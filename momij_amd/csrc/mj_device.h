@@ -74,6 +74,44 @@ __device__ __forceinline__ void perm16(const uint32_t u[8], uint32_t p[8]) {
 // Position of plain element i (0..15) inside a permuted 16-block.
 __device__ __forceinline__ int perm_pos(int i) { return i < 8 ? 2 * i : 2 * (i - 8) + 1; }
 
+// Writes 8 consecutive plain values (4 fp16 pairs in v, elements k0..k0+7 of a row, k0 a
+// multiple of 8) in qx order, and the block sums from lanes with (lane & 7) == 0.  Lanes must
+// come in aligned groups of 8 covering one 64-block.
+__device__ __forceinline__ void emit_qx(const u4v v, int lane, uint16_t* xperm_row,
+                                        float2* xsum_row, int k0) {
+    u4v o;
+    o.x = __shfl_xor(v.x, 1, MJ_WAVE);
+    o.y = __shfl_xor(v.y, 1, MJ_WAVE);
+    o.z = __shfl_xor(v.z, 1, MJ_WAVE);
+    o.w = __shfl_xor(v.w, 1, MJ_WAVE);
+    const bool odd = lane & 1;
+    const uint32_t u[8] = {odd ? o.x : v.x, odd ? o.y : v.y, odd ? o.z : v.z, odd ? o.w : v.w,
+                           odd ? v.x : o.x, odd ? v.y : o.y, odd ? v.z : o.z, odd ? v.w : o.w};
+    uint32_t p[8];
+    perm16(u, p);
+    u4v out;
+    out.x = odd ? p[4] : p[0];
+    out.y = odd ? p[5] : p[1];
+    out.z = odd ? p[6] : p[2];
+    out.w = odd ? p[7] : p[3];
+    *(u4v*)(xperm_row + k0) = out;
+    float X = 0.0f, Bx = 0.0f;
+    X = dot2(v.x, 0x3C003C00u, X);
+    X = dot2(v.y, 0x3C003C00u, X);
+    X = dot2(v.z, 0x3C003C00u, X);
+    X = dot2(v.w, 0x3C003C00u, X);
+    Bx = dot2(v.x, 0x44004C00u, Bx);
+    Bx = dot2(v.y, 0x44004C00u, Bx);
+    Bx = dot2(v.z, 0x44004C00u, Bx);
+    Bx = dot2(v.w, 0x44004C00u, Bx);
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+        X += __shfl_xor(X, m, MJ_WAVE);
+        Bx += __shfl_xor(Bx, m, MJ_WAVE);
+    }
+    if ((lane & 7) == 0) xsum_row[k0 >> 6] = make_float2(X, Bx);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, MJ_WAVE);

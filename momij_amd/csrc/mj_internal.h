@@ -142,6 +142,22 @@ hipError_t launch_topk_bucket(const float* logits, int M, int E, int k, int32_t*
                               float* scores, Buckets* bk, const int* abort, hipStream_t st);
 hipError_t launch_bucket_inds(const int32_t* inds, int P, Buckets* bk, const int* abort,
                               hipStream_t st);
+struct RouteArgs {
+    const uint16_t* x;       // [M][H] rows
+    const uint16_t* norm_w;  // [H] RMSNorm weight, nullptr: rows are already normed
+    const uint16_t* W;       // router [E][H]
+    uint16_t* xn;            // normed rows, plain [M][H] (optional)
+    uint16_t* xperm;         // normed rows, qx [M][H] (optional)
+    float2* xsum;            // [M][H/64]
+    int32_t* inds;           // [M][k]
+    float* scores;           // [M][k]
+    Buckets* bk;             // optional
+    int M, E, k;
+    float eps;
+    const int* abort;
+};
+bool route_supported(int H, int E, int k);
+hipError_t launch_route(const RouteArgs& a, int H, hipStream_t st);
 hipError_t launch_score_combine(const uint16_t* down, const float* scores, const uint16_t* x_resid,
                                 uint16_t* y, int M, int k, int H, const int* abort,
                                 hipStream_t st);

@@ -382,6 +382,8 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
                "inv_freq upload");
     if (s == MJ_OK)
         s = mj_hip(ctx, hipMemset(m->kv, 0, (size_t)c.n_layers * m->layer_stride * 2), "kv clear");
+    // pass scratch starts zeroed: an aborted pass leaves empty expert buckets behind
+    if (s == MJ_OK) s = mj_hip(ctx, hipMemset(m->arena, 0, count.off), "scratch clear");
     if (s == MJ_OK) s = mj_hip(ctx, hipDeviceSynchronize(), "create sync");
     if (s != MJ_OK) {
         mj_model_destroy(m);

@@ -13,44 +13,6 @@
 #include "mj_device.h"
 #include "mj_internal.h"
 
-// Writes 8 consecutive plain values (4 fp16 pairs in v, elements k0..k0+7 of a row, k0 a
-// multiple of 8) in qx order, and the block sums from lanes with (lane & 7) == 0.  Lanes must
-// come in aligned groups of 8 covering one 64-block.
-__device__ __forceinline__ void emit_qx(const u4v v, int lane, uint16_t* xperm_row,
-                                        float2* xsum_row, int k0) {
-    u4v o;
-    o.x = __shfl_xor(v.x, 1, MJ_WAVE);
-    o.y = __shfl_xor(v.y, 1, MJ_WAVE);
-    o.z = __shfl_xor(v.z, 1, MJ_WAVE);
-    o.w = __shfl_xor(v.w, 1, MJ_WAVE);
-    const bool odd = lane & 1;
-    const uint32_t u[8] = {odd ? o.x : v.x, odd ? o.y : v.y, odd ? o.z : v.z, odd ? o.w : v.w,
-                           odd ? v.x : o.x, odd ? v.y : o.y, odd ? v.z : o.z, odd ? v.w : o.w};
-    uint32_t p[8];
-    perm16(u, p);
-    u4v out;
-    out.x = odd ? p[4] : p[0];
-    out.y = odd ? p[5] : p[1];
-    out.z = odd ? p[6] : p[2];
-    out.w = odd ? p[7] : p[3];
-    *(u4v*)(xperm_row + k0) = out;
-    float X = 0.0f, Bx = 0.0f;
-    X = dot2(v.x, 0x3C003C00u, X);
-    X = dot2(v.y, 0x3C003C00u, X);
-    X = dot2(v.z, 0x3C003C00u, X);
-    X = dot2(v.w, 0x3C003C00u, X);
-    Bx = dot2(v.x, 0x44004C00u, Bx);
-    Bx = dot2(v.y, 0x44004C00u, Bx);
-    Bx = dot2(v.z, 0x44004C00u, Bx);
-    Bx = dot2(v.w, 0x44004C00u, Bx);
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) {
-        X += __shfl_xor(X, m, MJ_WAVE);
-        Bx += __shfl_xor(Bx, m, MJ_WAVE);
-    }
-    if ((lane & 7) == 0) xsum_row[k0 >> 6] = make_float2(X, Bx);
-}
-
 // One 256-thread block per row; H % 2048 == 0, H <= 8192.
 __global__ __launch_bounds__(256) void k_rmsnorm_qx(const uint16_t* __restrict__ x,
                                                     const uint16_t* __restrict__ w, float eps,
@@ -285,4 +247,251 @@ hipError_t launch_score_combine(const uint16_t* down, const float* scores, const
     hipLaunchKernelGGL(k_score_combine, dim3((M * H + 255) / 256), dim3(256), 0, st, down, scores,
                        x_resid, y, M, k, H, abort);
     return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------
+// Fused MoE front: RMSNorm of the pass rows, router logits on MFMA, softmax / top-k per row
+// and the expert buckets, in one 512-thread block (the whole step is a few hundred KB, so
+// one launch with every load issued up front beats four dependent launches).
+// Arithmetic as above except the order of the logit sum (MFMA over 32-element k slices,
+// then the two K-halves in order).  H = 2048: rows go in chunks of 16 (wave w normalises
+// rows w and w + 8 of the chunk); for the router the 8 waves are 4 expert tiles x 2 K-halves
+// of 1024 and each keeps its slice of the router rows of one 64-expert chunk in registers.
+// ---------------------------------------------------------------------------------------
+#define RT_H 2048
+#define RT_XS (RT_H + 8)  // LDS row stride (halves)
+#define RT_NS 32          // MFMA k-steps per wave (1024 / 32)
+
+static constexpr size_t route_lds_bytes() {
+    return (size_t)16 * RT_XS * 2 + 2 * 16 * 64 * 4 + 16 * MJ_MAX_EXPERTS * 4 +
+           MJ_MAX_EXPERTS * 8 + MJ_MAX_PAIRS * 4 + MJ_MAX_EXPERTS * 4 + 16;
+}
+
+__global__ __launch_bounds__(512) void k_route(RouteArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int M = a.M, E = a.E, k = a.k;
+    extern __shared__ __align__(16) char rt_lds[];
+    uint16_t* xs = (uint16_t*)rt_lds;                                  // [16][RT_XS]
+    float* red = (float*)(xs + 16 * RT_XS);                            // [2][16][64]
+    float* lg = red + 2 * 16 * 64;                                     // [16][E]
+    unsigned long long* s_mask = (unsigned long long*)(lg + 16 * MJ_MAX_EXPERTS);  // [E]
+    int* s_inds = (int*)(s_mask + MJ_MAX_EXPERTS);                     // [M*k]
+    int* s_start = s_inds + MJ_MAX_PAIRS;                              // [E]
+    int* s_abort = s_start + MJ_MAX_EXPERTS;
+
+    const int et = wv & 3, kh = wv >> 2;
+    const int ecol = et * 16 + (lane & 15);
+    const int kl = kh * 1024 + 8 * (lane >> 4);
+    u4v wr[RT_NS];
+#pragma unroll
+    for (int s = 0; s < RT_NS; ++s)
+        wr[s] = *(const u4v*)(a.W + (size_t)ecol * RT_H + kl + 32 * s);
+    for (int e = tid; e < MJ_MAX_EXPERTS; e += 512) s_mask[e] = 0ull;
+
+    for (int c0 = 0; c0 < M; c0 += 16) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int rl = wv + 8 * half, r = c0 + rl;
+            u4v o[4];
+            if (r < M) {
+                const uint16_t* xr = a.x + (size_t)r * RT_H;
+                u4v nw[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    o[c] = *(const u4v*)(xr + 512 * c + 8 * lane);
+                    nw[c] = a.norm_w ? *(const u4v*)(a.norm_w + 512 * c + 8 * lane)
+                                     : (u4v){0u, 0u, 0u, 0u};
+                }
+                if (a.norm_w) {
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float x0 = h2f(o[c][j] & 0xFFFFu), x1 = h2f(o[c][j] >> 16);
+                            ss += x0 * x0;
+                            ss += x1 * x1;
+                        }
+                    ss = wave_sum(ss);
+                    const float inv = 1.0f / sqrtf(ss / (float)RT_H + a.eps);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const float x0 = h2f(o[c][j] & 0xFFFFu) * inv * h2f(nw[c][j] & 0xFFFFu);
+                            const float x1 = h2f(o[c][j] >> 16) * inv * h2f(nw[c][j] >> 16);
+                            o[c][j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+                        }
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) o[c] = (u4v){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) *(u4v*)(xs + rl * RT_XS + 512 * c + 8 * lane) = o[c];
+        }
+        if (c0 == 0 && tid == 0) *s_abort = a.abort ? *a.abort : 0;
+        __syncthreads();
+        if (*s_abort) {
+            if (tid == 0 && a.bk) a.bk->count = 0;
+            return;  // block-uniform
+        }
+        // normed rows out (plain and / or qx)
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int rl = wv + 8 * half, r = c0 + rl;
+            if (r < M && (a.xn || a.xperm)) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int k0 = 512 * c + 8 * lane;
+                    const u4v o = *(const u4v*)(xs + rl * RT_XS + k0);
+                    if (a.xn) *(u4v*)(a.xn + (size_t)r * RT_H + k0) = o;
+                    if (a.xperm)
+                        emit_qx(o, lane, a.xperm + (size_t)r * RT_H,
+                                a.xsum + (size_t)r * (RT_H / 64), k0);
+                }
+            }
+        }
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            if (e0 > 0 || c0 > 0) {
+#pragma unroll
+                for (int s = 0; s < RT_NS; ++s)
+                    wr[s] = *(const u4v*)(a.W + (size_t)(e0 + ecol) * RT_H + kl + 32 * s);
+            }
+            f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < RT_NS; ++s) {
+                const u4v av = *(const u4v*)(xs + (lane & 15) * RT_XS + kl + 32 * s);
+                d = mfma16x16x32(as_h8(av), as_h8(wr[s]), d);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) red[(kh * 16 + 4 * (lane >> 4) + q) * 64 + ecol] = d[q];
+            __syncthreads();
+#pragma unroll
+            for (int rep = 0; rep < 2; ++rep) {
+                const int idx = tid + 512 * rep, row = idx >> 6, col = idx & 63;
+                lg[row * E + e0 + col] =
+                    red[(0 * 16 + row) * 64 + col] + red[(1 * 16 + row) * 64 + col];
+            }
+            __syncthreads();
+        }
+        // softmax + top-k, wave wv <-> rows wv and wv + 8 of the chunk
+        for (int half = 0; half < 2; ++half) {
+            const int rl = wv + 8 * half, r = c0 + rl;
+            if (r >= M) continue;
+            const float* lr = lg + rl * E;
+            float lv[4], work[4], g[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = lane + 64 * i;
+                lv[i] = e < E ? lr[e] : -INFINITY;
+                mx = fmaxf(mx, lv[i]);
+            }
+            mx = wave_max(mx);
+            float z = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = lane + 64 * i;
+                g[i] = e < E ? expf(lv[i] - mx) : 0.0f;
+                z += g[i];
+                work[i] = lv[i];
+            }
+            z = wave_sum(z);
+            // lane j keeps the j-th pick
+            float mysel = 0.0f, ssum = 0.0f;
+            int myidx = 0;
+            for (int j = 0; j < k; ++j) {
+                float bv = work[0];
+                int bi = lane;
+#pragma unroll
+                for (int i = 1; i < 4; ++i)
+                    if (work[i] > bv) {
+                        bv = work[i];
+                        bi = lane + 64 * i;
+                    }
+                wave_argmax(bv, bi);
+                float gsel = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (lane + 64 * i == bi) {
+                        work[i] = -INFINITY;
+                        gsel = g[i] / z;
+                    }
+                gsel = __shfl(gsel, bi & 63, MJ_WAVE);
+                ssum += gsel;
+                if (lane == j) {
+                    mysel = gsel;
+                    myidx = bi;
+                }
+            }
+            if (lane < k) {
+                a.inds[r * k + lane] = myidx;
+                a.scores[r * k + lane] = mysel / ssum;
+                s_inds[r * k + lane] = myidx;
+                atomicOr(&s_mask[myidx], 1ull << r);
+            }
+        }
+        __syncthreads();  // xs / lg reuse, masks complete
+    }
+    if (a.bk == nullptr) return;
+    Buckets* bk = a.bk;
+    // experts in increasing id; each bucket lists its pairs in increasing (row, slot) order
+    if (wv == 0) {
+        int cnt[4], tot = 0, nz = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + i;
+            cnt[i] = e < E ? __popcll(s_mask[e]) : 0;
+            tot += cnt[i];
+            nz += cnt[i] > 0;
+        }
+        int ptot = tot, pnz = nz;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t1 = __shfl_up(ptot, o, MJ_WAVE), t2 = __shfl_up(pnz, o, MJ_WAVE);
+            if (lane >= o) {
+                ptot += t1;
+                pnz += t2;
+            }
+        }
+        int pos = ptot - tot, u = pnz - nz;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + i;
+            if (e < E) s_start[e] = pos;
+            if (cnt[i] > 0) {
+                bk->expert[u] = e;
+                bk->start[u] = pos;
+                ++u;
+            }
+            pos += cnt[i];
+        }
+        if (lane == 63) {
+            bk->count = pnz;
+            bk->start[pnz] = ptot;
+        }
+    }
+    __syncthreads();
+    for (int p = tid; p < M * k; p += 512) {
+        const int e = s_inds[p], r = p / k;
+        const int rank = __popcll(s_mask[e] & ((1ull << r) - 1ull));
+        bk->pair[s_start[e] + rank] = p;
+    }
+}
+
+bool route_supported(int H, int E, int k) {
+    return H == RT_H && E % 64 == 0 && E <= MJ_MAX_EXPERTS && k >= 1 && k <= 8;
+}
+
+hipError_t launch_route(const RouteArgs& a, int H, hipStream_t st) {
+    if (!route_supported(H, a.E, a.k) || a.M < 1 || a.M > MJ_ROWS || a.M * a.k > MJ_MAX_PAIRS)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route, dim3(1), dim3(512), route_lds_bytes(), st, a);
+    return hipGetLastError();
+}
+
+hipError_t set_moe_attributes() {
+    return hipFuncSetAttribute((const void*)k_route, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)route_lds_bytes());
 }

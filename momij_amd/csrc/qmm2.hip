@@ -382,9 +382,9 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 256) void k_gather(Gather
 
 template <int RG, int T, int EPI>
 __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
-    if (aborted(a.abort)) return;
     constexpr int BT = 2 * T;
     constexpr int R = RG * 4;
+    static_assert(EPI != EPI_ADD || BT * R * 16 <= 512, "one residual element per thread");
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x;
     const int tg = wv >> 2, ks = wv & 3;
     const int nq = lane >> 4, nn = lane & 15;
@@ -410,6 +410,8 @@ __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
     float2* xsum = (float2*)(xs + R * XS);                   // [R][K/64]
     float* red = (float*)(xsum + R * kb_n);                  // [4][BT][R][16]
     float* actl = red + 4 * BT * R * 16;                     // [R][65] (SWIGLU)
+    __shared__ int s_pair[R];
+    __shared__ int s_abort;
 
     u4v cw[T][G2_SMAX];
     uint32_t sb[T][G2_SMAX];  // scale | bias << 16
@@ -437,27 +439,45 @@ __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
         }
     }
 
+    // staging: thread -> activation row sr = tid / 32, 16-byte parts (tid % 32) + 32 i
+    const int sr = tid >> 5, sl = tid & 31;
     for (int pb = 0; pb < np; pb += R) {
         const int npass = min(R, np - pb);
-        for (int idx = tid; idx < R * (K / 8); idx += 512) {
-            const int r = idx / (K / 8), part = idx % (K / 8);
-            u4v v = {0u, 0u, 0u, 0u};
-            if (r < npass) {
-                const int pr = bk ? bk->pair[p0 + pb + r] : pb + r;
-                v = *(const u4v*)(a.xperm + (size_t)(pr / a.x_div) * K + 8 * part);
+        {
+            const bool ok = sr < npass;
+            int pr = 0;
+            if (ok) pr = bk ? bk->pair[p0 + pb + sr] : pb + sr;
+            const int src = pr / a.x_div;
+            u4v xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int part = sl + 32 * i;
+                xv[i] = (u4v){0u, 0u, 0u, 0u};
+                if (ok && part < (K >> 3)) xv[i] = *(const u4v*)(a.xperm + (size_t)src * K + 8 * part);
             }
-            *(u4v*)(xs + r * XS + 8 * part) = v;
-        }
-        for (int idx = tid; idx < R * kb_n; idx += 512) {
-            const int r = idx / kb_n, kb = idx % kb_n;
-            float2 v = make_float2(0.0f, 0.0f);
-            if (r < npass) {
-                const int pr = bk ? bk->pair[p0 + pb + r] : pb + r;
-                v = a.xsum[(size_t)(pr / a.x_div) * kb_n + kb];
+            float2 xsv = make_float2(0.0f, 0.0f);
+            if (ok && sl < kb_n) xsv = a.xsum[(size_t)src * kb_n + sl];
+            if (pb == 0 && tid == 0) s_abort = a.abort ? *a.abort : 0;
+            if (sr < R) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int part = sl + 32 * i;
+                    if (part < (K >> 3)) *(u4v*)(xs + sr * XS + 8 * part) = xv[i];
+                }
+                if (sl < kb_n) xsum[sr * kb_n + sl] = xsv;
+                if (sl == 0) s_pair[sr] = pr;
             }
-            xsum[r * kb_n + kb] = v;
         }
         __syncthreads();
+        if (s_abort) return;  // block-uniform
+
+        // residual of this thread's output element (EPI_ADD), fetched before the math
+        uint16_t yold = 0;
+        if constexpr (EPI == EPI_ADD) {
+            const int i = tid / (R * 16), rem = tid % (R * 16), r = rem / 16, n = rem % 16;
+            if (i < BT && r < npass)
+                yold = a.y[(size_t)s_pair[r] * a.N + (tb * BT + i) * 16 + n];
+        }
 
         float acc[T][RG][4];
 #pragma unroll
@@ -472,27 +492,31 @@ __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
             const int t = t0 + s;
             if (t >= t1) break;
             const int kb = 4 * t + nq;
-            // activation operands of this 64-block: the same for every tile
-            u4v av[RG][8];
             float2 xv[RG][4];
 #pragma unroll
-            for (int rg = 0; rg < RG; ++rg) {
-#pragma unroll
-                for (int st = 0; st < 8; ++st) {
-                    av[rg][st] = (u4v){0u, 0u, 0u, 0u};
-                    if (arow) av[rg][st] = *(const u4v*)(xs + (rg * 4 + xm) * XS + 64 * kb + 8 * st);
-                }
+            for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) xv[rg][r] = xsum[(rg * 4 + r) * kb_n + kb];
-            }
+            f4 d[T][RG];
 #pragma unroll
-            for (int i = 0; i < T; ++i) {
-                const float sc = h2f(sb[i][s] & 0xFFFFu), bi = h2f(sb[i][s] >> 16);
-                f4 d[RG];
+            for (int i = 0; i < T; ++i)
 #pragma unroll
-                for (int rg = 0; rg < RG; ++rg) d[rg] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+                for (int rg = 0; rg < RG; ++rg) d[i][rg] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int wd = 0; wd < 4; ++wd) {
+            for (int wd = 0; wd < 4; ++wd) {
+                // activation operands of 32 k of this 64-block: shared by the T tiles
+                u4v av[RG][2];
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        av[rg][h] = (u4v){0u, 0u, 0u, 0u};
+                        if (arow)
+                            av[rg][h] = *(const u4v*)(xs + (rg * 4 + xm) * XS + 64 * kb +
+                                                      8 * (2 * wd + h));
+                    }
+#pragma unroll
+                for (int i = 0; i < T; ++i) {
                     uint32_t v[8];
                     unpack16(opaque(cw[i][s][wd]), v);
 #pragma unroll
@@ -504,14 +528,18 @@ __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
                         bv.w = v[4 * h + 3];
 #pragma unroll
                         for (int rg = 0; rg < RG; ++rg)
-                            d[rg] = mfma16x16x32(as_h8(av[rg][2 * wd + h]), as_h8(bv), d[rg]);
+                            d[i][rg] = mfma16x16x32(as_h8(av[rg][h]), as_h8(bv), d[i][rg]);
                     }
                 }
+            }
+#pragma unroll
+            for (int i = 0; i < T; ++i) {
+                const float sc = h2f(sb[i][s] & 0xFFFFu), bi = h2f(sb[i][s] >> 16);
 #pragma unroll
                 for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        acc[i][rg][r] += sc * (d[rg][r] - xv[rg][r].y) + bi * xv[rg][r].x;
+                        acc[i][rg][r] += sc * (d[i][rg][r] - xv[rg][r].y) + bi * xv[rg][r].x;
             }
         }
         // quarters -> lanes 0..15, then the K-slices through LDS
@@ -534,7 +562,7 @@ __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
                                 red[((1 * BT + i) * R + r) * 16 + n]) +
                                red[((2 * BT + i) * R + r) * 16 + n]) +
                               red[((3 * BT + i) * R + r) * 16 + n];
-            const int pr = bk ? bk->pair[p0 + pb + r] : pb + r;
+            const int pr = s_pair[r];
             if constexpr (EPI == EPI_SWIGLU) {
                 if (n < 8) {
                     const float gate_raw = ((red[((0 * BT + i) * R + r) * 16 + n + 8] +
@@ -554,7 +582,7 @@ __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
                 const int col = (tb * BT + i) * 16 + n;
                 uint16_t* yp = a.y + (size_t)pr * a.N + col;
                 if constexpr (EPI == EPI_ADD)
-                    *yp = f2h(h2f(*yp) + hround(tot));
+                    *yp = f2h(h2f(yold) + hround(tot));
                 else
                     *yp = f2h(tot);
             }
@@ -568,8 +596,7 @@ __global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
                     X += v;
                     Bx += ((c & 1) ? 4.0f : 16.0f) * v;
                 }
-                const int pr = bk ? bk->pair[p0 + pb + tid] : pb + tid;
-                a.ysum[(size_t)pr * (I / 64) + tb] = make_float2(X, Bx);
+                a.ysum[(size_t)s_pair[tid] * (I / 64) + tb] = make_float2(X, Bx);
             }
         }
         __syncthreads();  // LDS reuse by the next pass
@@ -614,7 +641,8 @@ hipError_t launch_gather(const GatherArgs& a, int epi, int max_rows_per_bucket, 
         if (epi == EPI_SWIGLU) {
             if (rows <= 4) return launch_gather2_t<1, 4, EPI_SWIGLU>(a, n_buckets_max, st);
             if (rows <= 8) return launch_gather2_t<2, 4, EPI_SWIGLU>(a, n_buckets_max, st);
-            return launch_gather2_t<4, 4, EPI_SWIGLU>(a, n_buckets_max, st);
+            // larger buckets: passes of 12 rows (16-row passes would spill registers)
+            return launch_gather2_t<3, 4, EPI_SWIGLU>(a, n_buckets_max, st);
         }
         if (a.N % 128 == 0) {
 #define MJ_G2(E)                                                                 \
@@ -642,8 +670,9 @@ hipError_t set_gather_attributes() {
 #define MJ_A(R, T, E)                                                                       \
     if (e == hipSuccess)                                                                    \
         e = hipFuncSetAttribute((const void*)k_gather2<R, T, E>,                            \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    MJ_A(1, 4, EPI_SWIGLU) MJ_A(2, 4, EPI_SWIGLU) MJ_A(4, 4, EPI_SWIGLU)
+                                hipFuncAttributeMaxDynamicSharedMemorySize,                 \
+                                (int)g2_lds<R, T, E>(2048));
+    MJ_A(1, 4, EPI_SWIGLU) MJ_A(2, 4, EPI_SWIGLU) MJ_A(3, 4, EPI_SWIGLU)
     MJ_A(1, 4, EPI_STORE) MJ_A(2, 2, EPI_STORE) MJ_A(3, 1, EPI_STORE) MJ_A(4, 1, EPI_STORE)
     MJ_A(1, 4, EPI_ADD) MJ_A(2, 2, EPI_ADD) MJ_A(3, 1, EPI_ADD) MJ_A(4, 1, EPI_ADD)
 #undef MJ_A
