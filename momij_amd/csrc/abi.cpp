@@ -413,9 +413,17 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, nb, st), "up gather");
         if (prof) prof->end(st);
         if (s != MJ_OK) return s;
+        // the tile kernel's SwiGLU epilogue writes act without block sums: the tile down
+        // kernel forms them from its staged rows, any other down kernel gets them here
+        const bool up_tile = gather3_supported(EPI_SWIGLU, H, 2 * I, w->gs);
+        const bool dn_tile = gather3_supported(EPI_STORE, I, H, w->gs);
+        if (up_tile && !dn_tile) {
+            s = mj_hip(ctx, launch_qx_sums(ms.act, ms.act_sum, M * k, I, ab, st), "act sums");
+            if (s != MJ_OK) return s;
+        }
         GatherArgs dn{};
         dn.xperm = ms.act;
-        dn.xsum = ms.act_sum;
+        dn.xsum = dn_tile ? nullptr : ms.act_sum;
         dn.w = w->down_w;
         dn.s = (const uint16_t*)w->down_s;
         dn.b = (const uint16_t*)w->down_b;

@@ -1,0 +1,466 @@
+// gather.hip -- 2-bit affine gather GEMM for verify passes on v_mfma_f32_16x16x32_f16.
+//
+// Semantics as k_qmv2 / k_gather (gqmm2_rows, SeedlessMetal.swift:2168-2221): per 64-input
+// block, y += s * (sum q*x) + b * (sum x), fp32.
+//
+// Layout of the work: one wave owns a tile of 16 weight rows over the whole K, so it issues
+// every load of its weights (codes, scales, biases) before its first wait and needs no
+// cross-wave reduction.  Lane (n = lane % 16, q = lane / 16) streams the contiguous quarter
+// q of row n: K/256 64-blocks = K/16 bytes of codes, one vector of scales and one of biases.
+// A block is WPB such waves over one expert bucket (or the dense projection): it stages the
+// bucket's activation rows (qx order, <= 4*RG per pass) in LDS once for all its waves.
+// The MFMA A operand carries activation row m only on the A rows 4q+m of k-quarter q, so one
+// MFMA yields a separate sum per quarter (= per lane 64-block) and every 64-block keeps its
+// own scale and bias; the quarters are added after the K loop.
+//
+// Epilogues: STORE y = half(acc); ADD y = half(y + half(acc)) (o-proj residual,
+// gqmm2_rows_fold_add 3488-3543); SWIGLU clamped SwiGLU of the up || gate row pair
+// (maple_clamped_swiglu 2435-2450) written in qx order with its block sums; QKV one head of
+// the dense qkv projection per block, finished with per-head RMSNorm + RoPE of q and k and
+// the K/V append (maple_qk_norm_rope + maple_write_kv_pair, 2794-2901).
+#include "mj_device.h"
+#include "mj_internal.h"
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (wave-uniform lds)
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
+}
+
+// Launch shape: R = 16 activation rows per pass (the MFMA M dimension), RA <= R rows staged in
+// LDS (the rows a bucket can hold), K = 256 * KPL.  A block has WPB waves = TPB tiles of 16
+// weight rows x KS K-slices: wave w owns tile w % TPB and K-slice w / TPB.
+template <int KPL, int GS, int EPI, int WPB, int KS>
+struct G5Shape {
+    static constexpr int R = 16;
+    static constexpr int K = KPL * 256;
+    static constexpr int KB = K / 64;          // 64-blocks per row (= 16-byte code chunks per row)
+    static constexpr int KBW = KB / KS;        // 64-blocks of one wave's K-slice
+    static constexpr int TPB = WPB / KS;       // weight tiles per block
+    static constexpr int XS = K + 8;           // LDS row stride of activations (halves)
+    static constexpr int SCH = K / GS / 8;     // 16-byte scale chunks per weight row
+    static constexpr int SCW = SCH / KS;       // ... per K-slice
+    static constexpr int ES = 129;             // QKV epilogue staging stride (floats)
+    static constexpr int WCODE = 16 * KBW * 16;  // bytes of one wave's code tile
+    static constexpr int WSB = 16 * SCW * 16;    // bytes of one wave's scales (and of its biases)
+    static constexpr int WAVE_BYTES = WCODE + 2 * WSB;
+    static constexpr int SS = KB + 2;          // LDS row stride of block sums (float2)
+    static_assert(WAVE_BYTES >= 64 * 16, "a K-slice partial fits in its wave's tile area");
+    // K-slice partials: in a wave's own tile area when a bucket is one pass (RA < R), else in
+    // their own region (later passes reuse the tiles)
+    static constexpr int RED = (KS - 1) * TPB * 64 * 16;
+    static size_t lds(int RA) {
+        return (size_t)WPB * WAVE_BYTES + (size_t)RA * XS * 2 + (size_t)RA * SS * 8 +
+               (EPI == EPI_QKV ? (size_t)R * ES * 4 : 0) + (RA == R ? RED : 0);
+    }
+};
+
+// Weight tile of one wave: 16 rows x K codes with their scales and biases, fetched straight
+// into LDS.  Scales and biases go first, then the codes in column groups: load j brings
+// 64-blocks 4j .. 4j+3 of all 16 rows (16 runs of 64 bytes), so the MFMAs of group j start as
+// soon as that load has landed while later groups are still streaming.  The code chunk
+// (row r, block B) sits at slot 64 * (B / 4) + 4r + ((B % 4) ^ (r / 4)): lane (n, q) then reads
+// word q of block B of row n from bank 16 (n % 4) + 4 ((B % 4) ^ (n / 4)) + q -- one 64-lane
+// read touches every bank once.
+//
+// MFMA: A = 16 activation rows x 32 k (qx order, from LDS), B = word q of one 64-block of the
+// 16 weight rows (lane (n, q)), so every MFMA stays inside one group of the scale and the
+// block's partial sums D[4q+r][n] are scaled once, in fp32.  The affine remainder
+// sum_B (b_B X_B - s_B Bx_B) is an fp32 MFMA chain over (block, term) pairs.
+
+// s_waitcnt that waits for the vector-memory counter only (gfx9 encoding: expcnt and lgkmcnt
+// left at their maximum)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for LDS data only: this wave's LDS writes done (lgkmcnt 0) and at most N
+// vector-memory loads still in flight (its LDS-DMA staging is older than those N), then
+// s_barrier.  __syncthreads() would also drain every outstanding global load (its fence waits
+// for vmcnt 0), i.e. the whole weight stream.  The "memory" clobber keeps LDS accesses on
+// their side of it.
+// 8-byte LDS store issued as inline assembly: the compiler would otherwise wait for every
+// in-flight LDS-DMA load (it cannot prove the store misses their destinations) before it.  The
+// ranges are disjoint by construction here; lds_barrier's lgkmcnt(0) orders the store.
+__device__ __forceinline__ void lds_store_f2(float2* p, float2 v) {
+    const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)p;
+    const uint64_t bits = __builtin_bit_cast(uint64_t, v);
+    asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(bits) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void lds_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int KPL, int GS, int EPI, int WPB, int KS>
+__global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
+    using S = G5Shape<KPL, GS, EPI, WPB, KS>;
+    constexpr int R = S::R, K = S::K, KB = S::KB, KBW = S::KBW, TPB = S::TPB, XS = S::XS;
+    constexpr int ES = S::ES, SCW = S::SCW;
+    constexpr int NT = WPB * 64;
+    constexpr int PPR = K / 8;                 // 16-byte parts per activation row
+    static_assert(EPI != EPI_QKV || TPB == 8, "one 128-row head per block");
+    static_assert(PPR % 64 == 0 && R % WPB == 0 && SCW >= 1 && SCW <= 4 && KBW % 4 == 0, "shape");
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int q = lane >> 4, n = lane & 15;
+    const int tt = wv % TPB, kh = wv / TPB;   // weight tile and K-slice of this wave
+    const int ncb = a.N / (16 * TPB);
+    const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
+    const Buckets* bk = a.bk;
+    const bool own_sums = a.xsum == nullptr;  // block sums formed here from the staged rows
+
+    // bucket header and abort word together
+    int e = 0, p0 = 0, np = a.dense_rows;
+    {
+        const int ab = a.abort ? *a.abort : 0;
+        if (bk != nullptr) {
+            const int cnt = bk->count, ee = bk->expert[u], s0 = bk->start[u], s1 = bk->start[u + 1];
+            if (u >= cnt) return;  // whole block
+            e = ee;
+            p0 = s0;
+            np = s1 - s0;
+        }
+        if (ab) return;  // whole block
+    }
+
+    extern __shared__ __align__(16) char g5lds[];
+    char* wreg = g5lds + (size_t)wv * S::WAVE_BYTES;      // this wave's weight tile
+    char* wcode = wreg;
+    uint16_t* wsc = (uint16_t*)(wreg + S::WCODE);          // [16][K/GS/KS] this K-slice
+    uint16_t* wbi = (uint16_t*)(wreg + S::WCODE + S::WSB);
+    uint16_t* xs = (uint16_t*)(g5lds + (size_t)WPB * S::WAVE_BYTES);  // [RA][XS] qx rows
+    float2* xsl = (float2*)(xs + RA * XS);                 // [RA][SS] {sum x, sum base*x}
+    float* el = (float*)(xsl + RA * S::SS);                // [R][ES] QKV epilogue staging
+    char* red = (char*)el + (EPI == EPI_QKV ? R * ES * 4 : 0);  // [KS-1][TPB][64] f4 (RA == R)
+    __shared__ int s_pair[R];
+
+    // ---- activation rows of a pass, straight into LDS: rows < npass only (the rest feed
+    // MFMA output rows that are discarded).  Wave w stages rows w, w + WPB, ...
+    auto stage_load = [&](int pb, int npass) {
+        const int myr = min(pb + (lane < R ? lane : 0), np - 1);
+        const int prl = bk ? bk->pair[p0 + myr] : myr;
+#pragma unroll
+        for (int j = 0; j < R / WPB; ++j) {
+            const int r = wv + WPB * j;
+            const int pr = __builtin_amdgcn_readlane(prl, r);
+            if (lane == 0) s_pair[r] = pr;
+            if (r < npass) {
+                const char* src = (const char*)(a.xperm + (size_t)(pr / a.x_div) * K);
+#pragma unroll
+                for (int i = 0; i < PPR / 64; ++i)
+                    load_lds16(src + 1024 * i + 16 * lane, (char*)(xs + r * XS) + 1024 * i);
+                if (!own_sums && lane < KB / 2)
+                    load_lds16((const char*)(a.xsum + (size_t)(pr / a.x_div) * KB) + 16 * lane,
+                               xsl + r * S::SS);
+            }
+        }
+    };
+    // {sum x, sum base*x} of each (row, 64-block) from the staged rows (fixed order)
+    auto own_block_sums = [&](int npass) {
+        for (int idx = tid; idx < npass * KB; idx += NT) {
+            const int r = idx % npass, b = idx / npass;
+            const uint16_t* xr = xs + r * XS + 64 * b;
+            float X = 0.0f, Bx = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const u4v v = *(const u4v*)(xr + 8 * c);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // qx pair (x_i, x_{i+8}) of a 16-block, i = (4c + j) % 8: base of code i
+                    const float base = ((4 * c + j) & 1) ? 4.0f : 16.0f;
+                    const float lo = h2f((uint16_t)v[j]), hi = h2f((uint16_t)(v[j] >> 16));
+                    X += lo + hi;
+                    Bx += base * (lo + hi);
+                }
+            }
+            lds_store_f2(xsl + r * S::SS + b, make_float2(X, Bx));
+        }
+    };
+
+    const int npass0 = min(R, np);
+    stage_load(0, npass0);  // in flight ahead of the weight stream (loads return in issue order)
+
+    // ---- this wave's weight tile, coalesced into LDS
+    const int I = a.N / 2;
+    auto tile_row = [&](int r) -> size_t {  // global row of tile row r
+        if constexpr (EPI == EPI_SWIGLU) {
+            const int j0 = (cb * TPB + tt) * 8;
+            return (size_t)e * a.N + (r < 8 ? j0 + r : I + j0 + r - 8);
+        } else {
+            return (size_t)e * a.N + (cb * TPB + tt) * 16 + r;
+        }
+    };
+    {
+        __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead in the vmcnt queue
+        const char* sg = (const char*)a.s;
+        const char* bg = (const char*)a.b;
+        if (lane < 16 * SCW) {
+            const int r = lane / SCW, c = kh * SCW + lane % SCW;
+            load_lds16(sg + tile_row(r) * (K / GS) * 2 + 16 * c, wsc);
+            load_lds16(bg + tile_row(r) * (K / GS) * 2 + 16 * c, wbi);
+        }
+        const char* wg = (const char*)a.w;
+        const int r = lane >> 2, B4 = (lane & 3) ^ (r >> 2);
+#pragma unroll
+        for (int j = 0; j < KBW / 4; ++j)  // column group j: blocks kh*KBW + 4j .. +3
+            load_lds16(wg + tile_row(r) * (K / 4) + 16 * (kh * KBW + 4 * j + B4),
+                       wcode + 1024 * j);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const UnpackK uk = {opaque(0x00C000C0u), opaque(0x03000300u), opaque(0x4C004C00u),
+                        opaque(0x44004400u)};
+    const int xrow = min(n, RA - 1);
+    const uint16_t* xa = xs + xrow * XS + 16 * q;                 // A: activation row, quarter q
+    const uint32_t* wq = (const uint32_t*)wcode + 16 * n + q;  // B: word q of row n's chunks
+
+    auto run_pass = [&](int pb, int npass) {
+        constexpr int G = KBW / 4;  // code column groups, issued after the two scale loads
+        // every wave's staged rows visible (this wave's were issued before its weights)
+        if (pb == 0)
+            lds_barrier<G + 2>();
+        else
+            lds_barrier<0>();
+        if (own_sums) {
+            own_block_sums(npass);
+            lds_barrier<G + 2>();
+        }
+        wait_vmcnt<G>();           // scales and biases have landed
+        u4v sv[SCW], bv[SCW];
+#pragma unroll
+        for (int c = 0; c < SCW; ++c) {
+            sv[c] = *(const u4v*)(wsc + (n * SCW + c) * 8);
+            bv[c] = *(const u4v*)(wbi + (n * SCW + c) * 8);
+        }
+        const uint16_t* xak = xa + 64 * kh * KBW;  // this K-slice's activations
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // sum_B s_B * (sum q x)_B: per 64-block f16 MFMA sums, scaled in fp32, one column group
+        // at a time as its codes arrive
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            if (j == 0) wait_vmcnt<G - 1>();
+            if (j == 1) wait_vmcnt<(G >= 2 ? G - 2 : 0)>();
+            if (j == 2) wait_vmcnt<(G >= 3 ? G - 3 : 0)>();
+            if (j == 3) wait_vmcnt<(G >= 4 ? G - 4 : 0)>();
+            if (j == 4) wait_vmcnt<(G >= 5 ? G - 5 : 0)>();
+            if (j == 5) wait_vmcnt<(G >= 6 ? G - 6 : 0)>();
+            if (j == 6) wait_vmcnt<(G >= 7 ? G - 7 : 0)>();
+            if (j == 7) wait_vmcnt<0>();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int B = 4 * j; B < 4 * j + 4; ++B) {  // block kh * KBW + B
+                // word q of chunk slot 64 (B / 4) + 4n + ((B % 4) ^ (n / 4))
+                const uint32_t word = wq[256 * (B / 4) + 4 * ((B & 3) ^ (n >> 2))];
+                uint32_t v[8];
+                unpack16k(word, v, uk);
+                f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const u4v av = *(const u4v*)(xak + 64 * B + 8 * h);
+                    const u4v bq = {v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                    d = mfma16x16x32(as_h8(av), as_h8(bq), d);
+                }
+                const int g = B * 64 / GS;
+                const uint32_t sw = opaque(sv[g / 8][(g % 8) / 2]);
+                const float sc = h2f((uint16_t)(sw >> (16 * (g & 1))));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] += sc * d[r];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pin(acc[r]);
+        }
+        // + sum_B (b_B X_B - s_B Bx_B): fp32 MFMA chains over k = (block, term) pairs;
+        // A = activation sums of block 2i + q/2 (term q & 1), B = bias / -scale of row n
+        f4 corr[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) corr[c] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+        const bool hiq = q >= 2, bterm = (q & 1) == 0;
+        const float* xcs = (const float*)(xsl + xrow * S::SS + kh * KBW + (q >> 1)) + (q & 1);
+#pragma unroll
+        for (int i = 0; i < KBW / 2; ++i) {
+            const float xa_k = xcs[4 * i];  // block 2i + q/2
+            const int g0 = (2 * i) * 64 / GS, g1 = (2 * i + 1) * 64 / GS;
+            const uint32_t s0 = (sv[g0 / 8][(g0 % 8) / 2] >> (16 * (g0 & 1))) & 0xFFFFu;
+            const uint32_t s1 = (sv[g1 / 8][(g1 % 8) / 2] >> (16 * (g1 & 1))) & 0xFFFFu;
+            const uint32_t b0 = (bv[g0 / 8][(g0 % 8) / 2] >> (16 * (g0 & 1))) & 0xFFFFu;
+            const uint32_t b1 = (bv[g1 / 8][(g1 % 8) / 2] >> (16 * (g1 & 1))) & 0xFFFFu;
+            const uint32_t sb = hiq ? s1 : s0, bb = hiq ? b1 : b0;
+            const float wk = bterm ? h2f((uint16_t)bb) : -h2f((uint16_t)sb);
+            corr[i & 3] = mfma16x16x4f32(xa_k, wk, corr[i & 3]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] += (corr[0][r] + corr[1][r]) + (corr[2][r] + corr[3][r]);
+        if constexpr (KS > 1) {
+            // K-slices of a tile meet in LDS (a slice's partial goes into its own wave's tile
+            // area, free once its MFMAs are done); slice 0 adds them in slice order
+            auto slot = [&](int k2) -> f4* {
+                return (f4*)(RA == R ? red + ((k2 - 1) * TPB + tt) * 1024
+                                     : g5lds + (size_t)(k2 * TPB + tt) * S::WAVE_BYTES) + lane;
+            };
+            if (kh > 0) *slot(kh) = (f4){acc[0], acc[1], acc[2], acc[3]};
+            lds_barrier<0>();
+            if (kh == 0) {
+#pragma unroll
+                for (int k2 = 1; k2 < KS; ++k2) {
+                    const f4 o = *slot(k2);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[r] += o[r];
+                }
+            }
+        }
+        // lane (n, q) now holds the outputs of activation rows 4q .. 4q+3 for weight row n
+        if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float gate_raw = __shfl_xor(acc[r], 8, MJ_WAVE);
+                const int i = 4 * q + r;
+                if (kh == 0 && n < 8 && i < npass) {
+                    float up = hround(acc[r]);
+                    float g = hround(gate_raw);
+                    g = fminf(g, 7.0f);
+                    up = fminf(fmaxf(up, -7.0f), 7.0f);
+                    const float act = hround(g / (1.0f + expf(-g)) * up);
+                    const int j = (cb * TPB + tt) * 8 + n;
+                    a.y[(size_t)s_pair[i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
+                }
+            }
+        } else if constexpr (EPI == EPI_QKV) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 4 * q + r;
+                if (kh == 0 && i < npass) el[i * ES + 16 * tt + n] = hround(acc[r]);
+            }
+            __syncthreads();
+            const QkvEpi& qe = a.qkv;
+            const int hh = cb;  // head of this block: q heads, then k heads, then v heads
+            for (int i = wv; i < npass; i += WPB) {
+                const int m = pb + i;
+                float v0 = el[i * ES + 2 * lane], v1 = el[i * ES + 2 * lane + 1];
+                if (hh < qe.nQ + qe.nKV) {
+                    const float ss = wave_sum(v0 * v0 + v1 * v1);
+                    const float scl = 1.0f / sqrtf(ss / 128.0f + qe.eps);
+                    const uint16_t* wn = hh < qe.nQ ? qe.q_norm_w : qe.k_norm_w;
+                    const uint32_t wpair = *(const uint32_t*)(wn + 2 * lane);
+                    v0 = v0 * scl * h2f((uint16_t)wpair);
+                    v1 = v1 * scl * h2f((uint16_t)(wpair >> 16));
+                    const int rd = qe.rope_dim;
+                    if (rd > 0) {
+                        const int half = rd / 2;
+                        const float u0 = __shfl_xor(v0, half / 2, MJ_WAVE);
+                        const float u1 = __shfl_xor(v1, half / 2, MJ_WAVE);
+                        const float pos = (float)(qe.sd->L + qe.sd->depth[m]);
+                        const int j0 = 2 * lane;
+                        if (j0 < rd) {
+                            const int f0 = j0 < half ? j0 : j0 - half;
+                            const float t0 = pos * qe.inv_freq[f0], t1 = pos * qe.inv_freq[f0 + 1];
+                            const float c0 = cosf(t0), s0 = sinf(t0), c1 = cosf(t1), s1 = sinf(t1);
+                            if (j0 < half) {
+                                v0 = v0 * c0 - u0 * s0;
+                                v1 = v1 * c1 - u1 * s1;
+                            } else {
+                                v0 = v0 * c0 + u0 * s0;
+                                v1 = v1 * c1 + u1 * s1;
+                            }
+                        }
+                    }
+                }
+                const uint32_t o = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
+                if (hh < qe.nQ) {
+                    *(uint32_t*)(qe.qbuf + ((size_t)m * qe.nQ + hh) * 128 + 2 * lane) = o;
+                } else {
+                    const int g = hh < qe.nQ + qe.nKV ? hh - qe.nQ : hh - qe.nQ - qe.nKV;
+                    const int64_t slot = (qe.sd->L + m) % qe.C;
+                    uint16_t* dst = hh < qe.nQ + qe.nKV ? qe.kc : qe.vc;
+                    *(uint32_t*)(dst + ((size_t)g * qe.C + slot) * 128 + 2 * lane) = o;
+                }
+            }
+        } else {
+            const int col = (cb * TPB + tt) * 16 + n;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 4 * q + r;
+                if (kh == 0 && i < npass) {
+                    uint16_t* yp = a.y + (size_t)s_pair[i] * a.N + col;
+                    if constexpr (EPI == EPI_ADD)
+                        *yp = f2h(h2f(*yp) + hround(acc[r]));
+                    else
+                        *yp = f2h(acc[r]);
+                }
+            }
+        }
+    };
+
+    run_pass(0, npass0);
+    for (int pb = R; pb < np; pb += R) {
+        __syncthreads();  // the previous pass is done with LDS
+        const int npass = min(R, np - pb);
+        stage_load(pb, npass);
+        run_pass(pb, npass);
+    }
+}
+
+template <int KPL, int GS, int EPI, int WPB, int KS>
+static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStream_t st) {
+    using S = G5Shape<KPL, GS, EPI, WPB, KS>;
+    const int ncb = a.N / (16 * S::TPB);
+    const int RA = rows < S::R ? (rows < 1 ? 1 : rows) : S::R;
+    const size_t lds = S::lds(RA);
+    hipLaunchKernelGGL((k_gather5<KPL, GS, EPI, WPB, KS>), dim3(n_buckets * ncb), dim3(WPB * 64),
+                       lds, st, a, RA);
+    return hipGetLastError();
+}
+
+// Shapes the tile kernel covers: SWIGLU / QKV / ADD at K = 2048, STORE at K = 1024 or 2048;
+// N a multiple of the block's rows; group size 64 or 128.
+bool gather3_supported(int epi, int K, int N, int gs) {
+    if (gs != 64 && gs != 128) return false;
+    switch (epi) {
+        case EPI_SWIGLU: return K == 2048 && N % 64 == 0;
+        case EPI_QKV: return K == 2048 && N % 128 == 0;
+        case EPI_ADD: return K == 2048 && N % 64 == 0;
+        case EPI_STORE: return (K == 1024 || K == 2048) && N % 64 == 0;
+    }
+    return false;
+}
+
+hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets,
+                          hipStream_t st) {
+    if (!gather3_supported(epi, a.K, a.N, a.gs)) return hipErrorInvalidValue;
+    const int rows = max_rows_per_bucket;
+#define MJ_G5(KPL, E, W, KS64, KS128)                                                      \
+    return a.gs == 64 ? launch_g5<KPL, 64, E, W, KS64>(a, rows, n_buckets, st)              \
+                      : launch_g5<KPL, 128, E, W, KS128>(a, rows, n_buckets, st);
+    switch (epi) {
+        case EPI_SWIGLU: MJ_G5(8, EPI_SWIGLU, 8, 2, 2)
+        case EPI_QKV: MJ_G5(8, EPI_QKV, 8, 1, 1)
+        case EPI_ADD: MJ_G5(8, EPI_ADD, 8, 2, 2)
+        case EPI_STORE:
+            if (a.K == 1024) { MJ_G5(4, EPI_STORE, 8, 2, 1) }
+            MJ_G5(8, EPI_STORE, 8, 2, 2)
+    }
+#undef MJ_G5
+    return hipErrorInvalidValue;
+}
+
+template <int KPL, int GS, int EPI, int WPB, int KS>
+static hipError_t g5_attr() {
+    return hipFuncSetAttribute((const void*)k_gather5<KPL, GS, EPI, WPB, KS>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)G5Shape<KPL, GS, EPI, WPB, KS>::lds(16));
+}
+
+hipError_t set_gather3_attributes() {
+    hipError_t e = hipSuccess;
+#define MJ_A(KPL, E, W, KS64, KS128)                           \
+    if (e == hipSuccess) e = g5_attr<KPL, 64, E, W, KS64>();    \
+    if (e == hipSuccess) e = g5_attr<KPL, 128, E, W, KS128>();
+    MJ_A(8, EPI_SWIGLU, 8, 2, 2) MJ_A(8, EPI_QKV, 8, 1, 1) MJ_A(8, EPI_ADD, 8, 2, 2)
+    MJ_A(4, EPI_STORE, 8, 2, 1) MJ_A(8, EPI_STORE, 8, 2, 2)
+#undef MJ_A
+    return e;
+}

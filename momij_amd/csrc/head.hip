@@ -298,7 +298,7 @@ hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H,
 }
 
 hipError_t set_attn_attributes();
-hipError_t set_gather_attributes();
+hipError_t set_gather3_attributes();
 hipError_t set_moe_attributes();
 
 hipError_t set_kernel_attributes() {
@@ -310,7 +310,7 @@ hipError_t set_kernel_attributes() {
         e = hipFuncSetAttribute((const void*)k_lm_head<2>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
-    if (e == hipSuccess) e = set_gather_attributes();
+    if (e == hipSuccess) e = set_gather3_attributes();
     if (e == hipSuccess) e = set_moe_attributes();
     if (e == hipSuccess) done = true;
     return e;

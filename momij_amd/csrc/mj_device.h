@@ -41,12 +41,33 @@ __device__ __forceinline__ void unpack16(uint32_t w, uint32_t v[8]) {
     v[7] = (s4 & 0x03000300u) | 0x44004400u;
 }
 
+// unpack16 with its masks and magic constants held in VGPRs (an AND-OR with a VGPR constant
+// is one v_and_or_b32; with inline literals it is two instructions on this target).
+struct UnpackK {
+    uint32_t m1, m2, c1, c2;
+};
+__device__ __forceinline__ void unpack16k(uint32_t w, uint32_t v[8], const UnpackK& k) {
+    const uint32_t s1 = w << 6, s2 = w << 2, s3 = w >> 2, s4 = w >> 6;
+    v[0] = (s1 & k.m1) | k.c1;
+    v[1] = (s1 & k.m2) | k.c2;
+    v[2] = (s2 & k.m1) | k.c1;
+    v[3] = (s2 & k.m2) | k.c2;
+    v[4] = (s3 & k.m1) | k.c1;
+    v[5] = (s3 & k.m2) | k.c2;
+    v[6] = (s4 & k.m1) | k.c1;
+    v[7] = (s4 & k.m2) | k.c2;
+}
+
 // Value the optimiser cannot see through: keeps loop-invariant code expansion from being
 // hoisted out of a loop (and held live across it) when registers are the scarce resource.
 __device__ __forceinline__ uint32_t opaque(uint32_t x) {
     asm volatile("" : "+v"(x));
     return x;
 }
+
+// Pins a float at this point of the program: computations feeding it cannot be sunk past it
+// (keeps unrolled accumulation chains from being deferred until every operand is live).
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
 // base of permuted pair i (16 for even code index, 4 for odd)
 __device__ __forceinline__ float code_base(int i) { return (i & 1) ? 4.0f : 16.0f; }
@@ -135,6 +156,10 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
             i = oi;
         }
     }
+}
+
+__device__ __forceinline__ f4 mfma16x16x4f32(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {

@@ -16,7 +16,7 @@ struct Buckets {
     int pair[MJ_MAX_PAIRS];
 };
 
-enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
 #define MJ_ROWS 64  // == MJ_MAX_ROWS of the C ABI
 
@@ -48,6 +48,21 @@ struct StepResult {
     int32_t argmax[MJ_ROWS];
 };
 
+// EPI_QKV: the dense qkv projection finishes each head in place -- per-head RMSNorm and RoPE
+// of q and k at the row's position, q to qbuf, k and v appended to the KV cache.
+struct QkvEpi {
+    const uint16_t* q_norm_w;  // [128]
+    const uint16_t* k_norm_w;  // [128]
+    const float* inv_freq;     // [rope_dim/2]
+    const StepDesc* sd;        // L, depth
+    uint16_t* qbuf;            // [M][nQ][128]
+    uint16_t* kc;              // [nKV][C][128]
+    uint16_t* vc;
+    int64_t C;
+    int nQ, nKV, rope_dim;
+    float eps;
+};
+
 struct GatherArgs {
     const uint16_t* xperm;  // qx activations [rows_x][K]
     const float2* xsum;     // [rows_x][K/64] {sum x, sum base*x}
@@ -61,6 +76,7 @@ struct GatherArgs {
     int K, N, gs;
     int x_div;              // x row of pair p = p / x_div
     const int* abort;
+    QkvEpi qkv;             // EPI_QKV only
 };
 
 struct QmvArgs {
@@ -77,10 +93,17 @@ struct QmvArgs {
 // qmm2.hip
 hipError_t launch_qx_prep(const uint16_t* x, uint16_t* xperm, float2* xsum, int rows, int K,
                           const int* abort, hipStream_t st);
+hipError_t launch_qx_sums(const uint16_t* xperm, float2* xsum, int rows, int K, const int* abort,
+                          hipStream_t st);
 hipError_t launch_qmv2(const QmvArgs& a, int epi, hipStream_t st);
 hipError_t launch_gather(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets_max,
                          hipStream_t st);
 hipError_t launch_selftest_mfma(const uint16_t* A, const uint16_t* B, float* D, hipStream_t st);
+
+// gather.hip: the tile gather (one 16-row weight tile over the whole K per wave)
+bool gather3_supported(int epi, int K, int N, int gs);
+hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets,
+                          hipStream_t st);
 
 struct AttnArgs {
     const uint16_t* qkv;     // [M][(nQ+2nKV)*128] projection output (plain)

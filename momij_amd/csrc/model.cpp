@@ -105,8 +105,24 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, hipStream_t st) {
     q.x_div = 1;
     q.abort = ab;
     Prof* pf = m->profiling ? &m->prof : nullptr;
+    // the qkv tile kernel finishes q/k-norm, RoPE and the KV append in its epilogue
+    const bool fused_qkv = gather3_supported(EPI_QKV, H, qkvN, c.gs);
+    if (fused_qkv) {
+        q.qkv.q_norm_w = (const uint16_t*)w.attn.q_norm_w;
+        q.qkv.k_norm_w = (const uint16_t*)w.attn.k_norm_w;
+        q.qkv.inv_freq = m->inv_freq;
+        q.qkv.sd = m->sd_dev;
+        q.qkv.qbuf = m->qbuf;
+        q.qkv.kc = m->kv + (int64_t)l * m->layer_stride;
+        q.qkv.vc = q.qkv.kc + (int64_t)nKV * c.kv_capacity * 128;
+        q.qkv.C = c.kv_capacity;
+        q.qkv.nQ = nQ;
+        q.qkv.nKV = nKV;
+        q.qkv.rope_dim = c.rope_dim;
+        q.qkv.eps = c.eps;
+    }
     if (pf) pf->begin(PROF_DENSE, st);
-    s = mj_hip(ctx, launch_gather(q, EPI_STORE, M, 1, st), "qkv");
+    s = mj_hip(ctx, launch_gather(q, fused_qkv ? EPI_QKV : EPI_STORE, M, 1, st), "qkv");
     if (pf) pf->end(st);
     if (s != MJ_OK) return s;
     AttnArgs a{};
@@ -132,8 +148,10 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, hipStream_t st) {
     a.eps = c.eps;
     a.scale = (float)std::pow((double)D, -0.5);
     a.abort = ab;
-    s = mj_hip(ctx, launch_qknorm_rope_kv(a, st), "qk norm rope");
-    if (s != MJ_OK) return s;
+    if (!fused_qkv) {
+        s = mj_hip(ctx, launch_qknorm_rope_kv(a, st), "qk norm rope");
+        if (s != MJ_OK) return s;
+    }
     if (pf) pf->begin(PROF_ATTN, st);
     s = mj_hip(ctx, launch_attn(a, st), "attention");
     if (pf) pf->end(st);
@@ -633,7 +651,22 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
     q.gs = c.gs;
     q.x_div = 1;
     q.abort = ab;
-    s = mj_hip(ctx, launch_gather(q, EPI_STORE, M, 1, st), "qkv");
+    const bool fused_qkv = gather3_supported(EPI_QKV, H, qkvN, c.gs);
+    if (fused_qkv) {
+        q.qkv.q_norm_w = (const uint16_t*)w->q_norm_w;
+        q.qkv.k_norm_w = (const uint16_t*)w->k_norm_w;
+        q.qkv.inv_freq = (const float*)p[9];
+        q.qkv.sd = (const StepDesc*)p[8];
+        q.qkv.qbuf = (uint16_t*)p[3];
+        q.qkv.kc = (uint16_t*)kcache;
+        q.qkv.vc = (uint16_t*)vcache;
+        q.qkv.C = c.kv_capacity;
+        q.qkv.nQ = nQ;
+        q.qkv.nKV = nKV;
+        q.qkv.rope_dim = c.rope_dim;
+        q.qkv.eps = c.eps;
+    }
+    s = mj_hip(ctx, launch_gather(q, fused_qkv ? EPI_QKV : EPI_STORE, M, 1, st), "qkv");
     if (s != MJ_OK) return s;
     AttnArgs a{};
     a.qkv = (uint16_t*)p[2];
@@ -658,7 +691,7 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
     a.eps = c.eps;
     a.scale = (float)std::pow(128.0, -0.5);
     a.abort = ab;
-    s = mj_hip(ctx, launch_qknorm_rope_kv(a, st), "qk norm rope");
+    if (!fused_qkv) s = mj_hip(ctx, launch_qknorm_rope_kv(a, st), "qk norm rope");
     if (s == MJ_OK) s = mj_hip(ctx, launch_attn(a, st), "attention");
     if (s != MJ_OK) return s;
     GatherArgs o{};

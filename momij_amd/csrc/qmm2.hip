@@ -66,6 +66,35 @@ __global__ __launch_bounds__(256) void k_qx_prep(const uint16_t* __restrict__ x,
     if ((lane & 7) == 0) xsum[(size_t)row * (K / 64) + 8 * c + (lane >> 3)] = make_float2(X, Bx);
 }
 
+// Block sums {sum x, sum base*x} of rows already in qx order (one thread per 64-block).
+__global__ __launch_bounds__(256) void k_qx_sums(const uint16_t* __restrict__ xperm,
+                                                 float2* __restrict__ xsum, int rows, int K,
+                                                 const int* abort) {
+    if (aborted(abort)) return;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * (K / 64)) return;
+    const uint16_t* xr = xperm + (size_t)i * 64;
+    float X = 0.0f, Bx = 0.0f;
+    for (int c = 0; c < 8; ++c) {
+        const u4v v = *(const u4v*)(xr + 8 * c);
+        for (int j = 0; j < 4; ++j) {
+            const float base = ((4 * c + j) & 1) ? 4.0f : 16.0f;  // pair (x_i, x_{i+8}), i = (4c+j)%8
+            const float lo = h2f((uint16_t)v[j]), hi = h2f((uint16_t)(v[j] >> 16));
+            X += lo + hi;
+            Bx += base * (lo + hi);
+        }
+    }
+    xsum[i] = make_float2(X, Bx);
+}
+
+hipError_t launch_qx_sums(const uint16_t* xperm, float2* xsum, int rows, int K, const int* abort,
+                          hipStream_t st) {
+    const int n = rows * (K / 64);
+    hipLaunchKernelGGL(k_qx_sums, dim3((n + 255) / 256), dim3(256), 0, st, xperm, xsum, rows, K,
+                       abort);
+    return hipGetLastError();
+}
+
 hipError_t launch_qx_prep(const uint16_t* x, uint16_t* xperm, float2* xsum, int rows, int K,
                           const int* abort, hipStream_t st) {
     const int waves = rows * (K / 512);
@@ -368,256 +397,6 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 256) void k_gather(Gather
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// MFMA gather GEMM with K split across waves.
-// Block = 8 waves = 2 tile groups x 4 K-slices; block = (bucket u, BT = 2T tiles of 16 output
-// rows).  Wave (tg, ks) owns super-steps [ks*KS/4, (ks+1)*KS/4) of K (KS = K/256) for the T
-// tiles of group tg, and issues every code, scale and bias load of its slice before it
-// computes.  The bucket's activation rows (<= 4*RG per pass) sit in LDS in qx order; the four
-// K-slice partials are summed in LDS in slice order (deterministic).
-// EPI_SWIGLU: BT = 8 tiles = one 64-wide block of the intermediate dim (tile i: up rows
-// j0+8i..+7 and gate rows I+j0+8i..+7); act is written in qx order with its block sums.
-// ---------------------------------------------------------------------------------------
-#define G2_SMAX 2  // super-steps per wave: K <= 2048
-
-template <int RG, int T, int EPI>
-__global__ __launch_bounds__(512) void k_gather2(GatherArgs a) {
-    constexpr int BT = 2 * T;
-    constexpr int R = RG * 4;
-    static_assert(EPI != EPI_ADD || BT * R * 16 <= 512, "one residual element per thread");
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tid = threadIdx.x;
-    const int tg = wv >> 2, ks = wv & 3;
-    const int nq = lane >> 4, nn = lane & 15;
-    const Buckets* bk = a.bk;
-    const int nbk = bk ? bk->count : 1;
-    const int nblk_per_bucket = a.N / (16 * BT);
-    const int u = blockIdx.x / nblk_per_bucket;
-    const int tb = blockIdx.x % nblk_per_bucket;
-    if (u >= nbk) return;  // whole block
-    const int I = a.N / 2;
-    const int e = bk ? bk->expert[u] : 0;
-    const int p0 = bk ? bk->start[u] : 0;
-    const int np = bk ? bk->start[u + 1] - p0 : a.dense_rows;
-    const int K = a.K, kb_n = K >> 6, kw = K >> 4, kg = K / a.gs;
-    const int KS = K >> 8;
-    const int t0 = ks * KS / 4, t1 = (ks + 1) * KS / 4;
-    const int xm = lane & 3;
-    const bool arow = ((lane & 15) >> 2) == nq;
-    const int XS = K + 8;
-
-    extern __shared__ uint16_t g2lds[];
-    uint16_t* xs = g2lds;                                    // [R][K+8] qx rows
-    float2* xsum = (float2*)(xs + R * XS);                   // [R][K/64]
-    float* red = (float*)(xsum + R * kb_n);                  // [4][BT][R][16]
-    float* actl = red + 4 * BT * R * 16;                     // [R][65] (SWIGLU)
-    __shared__ int s_pair[R];
-    __shared__ int s_abort;
-
-    u4v cw[T][G2_SMAX];
-    uint32_t sb[T][G2_SMAX];  // scale | bias << 16
-#pragma unroll
-    for (int i = 0; i < T; ++i) {
-        const int ti = tg * T + i;  // tile within block
-        int nrow;
-        if constexpr (EPI == EPI_SWIGLU) {
-            const int j0 = tb * 64 + 8 * ti;
-            nrow = nn < 8 ? j0 + nn : I + j0 + nn - 8;
-        } else {
-            nrow = (tb * BT + ti) * 16 + nn;
-        }
-        const size_t rr = (size_t)e * a.N + nrow;
-        const u4v* wp = (const u4v*)(a.w + rr * kw);
-#pragma unroll
-        for (int s = 0; s < G2_SMAX; ++s) {
-            const int t = t0 + s;
-            if (t < t1) {
-                const int kb = 4 * t + nq;
-                cw[i][s] = wp[kb];
-                const int gi = (kb * 64) / a.gs;
-                sb[i][s] = (uint32_t)a.s[rr * kg + gi] | ((uint32_t)a.b[rr * kg + gi] << 16);
-            }
-        }
-    }
-
-    // staging: thread -> activation row sr = tid / 32, 16-byte parts (tid % 32) + 32 i
-    const int sr = tid >> 5, sl = tid & 31;
-    for (int pb = 0; pb < np; pb += R) {
-        const int npass = min(R, np - pb);
-        {
-            const bool ok = sr < npass;
-            int pr = 0;
-            if (ok) pr = bk ? bk->pair[p0 + pb + sr] : pb + sr;
-            const int src = pr / a.x_div;
-            u4v xv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int part = sl + 32 * i;
-                xv[i] = (u4v){0u, 0u, 0u, 0u};
-                if (ok && part < (K >> 3)) xv[i] = *(const u4v*)(a.xperm + (size_t)src * K + 8 * part);
-            }
-            float2 xsv = make_float2(0.0f, 0.0f);
-            if (ok && sl < kb_n) xsv = a.xsum[(size_t)src * kb_n + sl];
-            if (pb == 0 && tid == 0) s_abort = a.abort ? *a.abort : 0;
-            if (sr < R) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const int part = sl + 32 * i;
-                    if (part < (K >> 3)) *(u4v*)(xs + sr * XS + 8 * part) = xv[i];
-                }
-                if (sl < kb_n) xsum[sr * kb_n + sl] = xsv;
-                if (sl == 0) s_pair[sr] = pr;
-            }
-        }
-        __syncthreads();
-        if (s_abort) return;  // block-uniform
-
-        // residual of this thread's output element (EPI_ADD), fetched before the math
-        uint16_t yold = 0;
-        if constexpr (EPI == EPI_ADD) {
-            const int i = tid / (R * 16), rem = tid % (R * 16), r = rem / 16, n = rem % 16;
-            if (i < BT && r < npass)
-                yold = a.y[(size_t)s_pair[r] * a.N + (tb * BT + i) * 16 + n];
-        }
-
-        float acc[T][RG][4];
-#pragma unroll
-        for (int i = 0; i < T; ++i)
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[i][rg][r] = 0.0f;
-
-#pragma unroll
-        for (int s = 0; s < G2_SMAX; ++s) {
-            const int t = t0 + s;
-            if (t >= t1) break;
-            const int kb = 4 * t + nq;
-            float2 xv[RG][4];
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) xv[rg][r] = xsum[(rg * 4 + r) * kb_n + kb];
-            f4 d[T][RG];
-#pragma unroll
-            for (int i = 0; i < T; ++i)
-#pragma unroll
-                for (int rg = 0; rg < RG; ++rg) d[i][rg] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int wd = 0; wd < 4; ++wd) {
-                // activation operands of 32 k of this 64-block: shared by the T tiles
-                u4v av[RG][2];
-#pragma unroll
-                for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        av[rg][h] = (u4v){0u, 0u, 0u, 0u};
-                        if (arow)
-                            av[rg][h] = *(const u4v*)(xs + (rg * 4 + xm) * XS + 64 * kb +
-                                                      8 * (2 * wd + h));
-                    }
-#pragma unroll
-                for (int i = 0; i < T; ++i) {
-                    uint32_t v[8];
-                    unpack16(opaque(cw[i][s][wd]), v);
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        u4v bv;
-                        bv.x = v[4 * h + 0];
-                        bv.y = v[4 * h + 1];
-                        bv.z = v[4 * h + 2];
-                        bv.w = v[4 * h + 3];
-#pragma unroll
-                        for (int rg = 0; rg < RG; ++rg)
-                            d[i][rg] = mfma16x16x32(as_h8(av[rg][h]), as_h8(bv), d[i][rg]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < T; ++i) {
-                const float sc = h2f(sb[i][s] & 0xFFFFu), bi = h2f(sb[i][s] >> 16);
-#pragma unroll
-                for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[i][rg][r] += sc * (d[i][rg][r] - xv[rg][r].y) + bi * xv[rg][r].x;
-            }
-        }
-        // quarters -> lanes 0..15, then the K-slices through LDS
-#pragma unroll
-        for (int i = 0; i < T; ++i)
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float v = acc[i][rg][r];
-                    v += __shfl_xor(v, 16, MJ_WAVE);
-                    v += __shfl_xor(v, 32, MJ_WAVE);
-                    if (nq == 0) red[((ks * BT + tg * T + i) * R + rg * 4 + r) * 16 + nn] = v;
-                }
-        __syncthreads();
-        for (int idx = tid; idx < BT * R * 16; idx += 512) {
-            const int i = idx / (R * 16), rem = idx % (R * 16), r = rem / 16, n = rem % 16;
-            if (r >= npass) continue;
-            const float tot = ((red[((0 * BT + i) * R + r) * 16 + n] +
-                                red[((1 * BT + i) * R + r) * 16 + n]) +
-                               red[((2 * BT + i) * R + r) * 16 + n]) +
-                              red[((3 * BT + i) * R + r) * 16 + n];
-            const int pr = s_pair[r];
-            if constexpr (EPI == EPI_SWIGLU) {
-                if (n < 8) {
-                    const float gate_raw = ((red[((0 * BT + i) * R + r) * 16 + n + 8] +
-                                             red[((1 * BT + i) * R + r) * 16 + n + 8]) +
-                                            red[((2 * BT + i) * R + r) * 16 + n + 8]) +
-                                           red[((3 * BT + i) * R + r) * 16 + n + 8];
-                    float up = hround(tot);
-                    float g = hround(gate_raw);
-                    g = fminf(g, 7.0f);
-                    up = fminf(fmaxf(up, -7.0f), 7.0f);
-                    const float act = hround(g / (1.0f + expf(-g)) * up);
-                    const int j = tb * 64 + 8 * i + n;
-                    a.y[(size_t)pr * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
-                    actl[r * 65 + 8 * i + n] = act;
-                }
-            } else {
-                const int col = (tb * BT + i) * 16 + n;
-                uint16_t* yp = a.y + (size_t)pr * a.N + col;
-                if constexpr (EPI == EPI_ADD)
-                    *yp = f2h(h2f(yold) + hround(tot));
-                else
-                    *yp = f2h(tot);
-            }
-        }
-        if constexpr (EPI == EPI_SWIGLU) {
-            __syncthreads();
-            if (tid < npass) {
-                float X = 0.0f, Bx = 0.0f;
-                for (int c = 0; c < 64; ++c) {
-                    const float v = actl[tid * 65 + c];
-                    X += v;
-                    Bx += ((c & 1) ? 4.0f : 16.0f) * v;
-                }
-                a.ysum[(size_t)s_pair[tid] * (I / 64) + tb] = make_float2(X, Bx);
-            }
-        }
-        __syncthreads();  // LDS reuse by the next pass
-    }
-}
-
-template <int RG, int T, int EPI>
-static size_t g2_lds(int K) {
-    constexpr int R = RG * 4;
-    return (size_t)R * (K + 8) * 2 + (size_t)R * (K / 64) * 8 + (size_t)4 * 2 * T * R * 16 * 4 +
-           (EPI == EPI_SWIGLU ? (size_t)R * 65 * 4 : 0);
-}
-
-template <int RG, int T, int EPI>
-static hipError_t launch_gather2_t(const GatherArgs& a, int n_buckets_max, hipStream_t st) {
-    const int blocks = n_buckets_max * (a.N / (16 * 2 * T));
-    const size_t lds = g2_lds<RG, T, EPI>(a.K);
-    hipLaunchKernelGGL((k_gather2<RG, T, EPI>), dim3(blocks), dim3(512), lds, st, a);
-    return hipGetLastError();
-}
-
 template <int RG, int EPI>
 static hipError_t launch_gather_t(const GatherArgs& a, int n_buckets_max, hipStream_t st) {
     constexpr int TPW = 2;
@@ -634,27 +413,10 @@ static hipError_t launch_gather_t(const GatherArgs& a, int n_buckets_max, hipStr
 
 hipError_t launch_gather(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets_max,
                          hipStream_t st) {
+    if (gather3_supported(epi, a.K, a.N, a.gs))
+        return launch_gather3(a, epi, max_rows_per_bucket, n_buckets_max, st);
+    // generic fallback (any K % 256 == 0, N % 16 == 0): K inside each wave, RG row groups
     const int rows = max_rows_per_bucket;
-    if (a.K <= 2048 && a.K % 256 == 0) {
-        // K split over 4 waves per tile group; SWIGLU blocks cover 8 tiles (64 intermediate
-        // columns); STORE/ADD blocks cover 2T tiles with T * RG <= 4
-        if (epi == EPI_SWIGLU) {
-            if (rows <= 4) return launch_gather2_t<1, 4, EPI_SWIGLU>(a, n_buckets_max, st);
-            if (rows <= 8) return launch_gather2_t<2, 4, EPI_SWIGLU>(a, n_buckets_max, st);
-            // larger buckets: passes of 12 rows (16-row passes would spill registers)
-            return launch_gather2_t<3, 4, EPI_SWIGLU>(a, n_buckets_max, st);
-        }
-        if (a.N % 128 == 0) {
-#define MJ_G2(E)                                                                 \
-    if (rows <= 4) return launch_gather2_t<1, 4, E>(a, n_buckets_max, st);       \
-    if (rows <= 8) return launch_gather2_t<2, 2, E>(a, n_buckets_max, st);       \
-    if (rows <= 12) return launch_gather2_t<3, 1, E>(a, n_buckets_max, st);      \
-    return launch_gather2_t<4, 1, E>(a, n_buckets_max, st);
-            if (epi == EPI_STORE) { MJ_G2(EPI_STORE) }
-            if (epi == EPI_ADD) { MJ_G2(EPI_ADD) }
-#undef MJ_G2
-        }
-    }
     const int rg = rows <= 4 ? 1 : (rows <= 8 ? 2 : 4);
 #define MJ_G(R, E)                                      \
     if (rg == R && epi == E) return launch_gather_t<R, E>(a, n_buckets_max, st);
@@ -663,20 +425,6 @@ hipError_t launch_gather(const GatherArgs& a, int epi, int max_rows_per_bucket, 
     MJ_G(1, EPI_SWIGLU) MJ_G(2, EPI_SWIGLU) MJ_G(4, EPI_SWIGLU)
 #undef MJ_G
     return hipErrorInvalidValue;
-}
-
-hipError_t set_gather_attributes() {
-    hipError_t e = hipSuccess;
-#define MJ_A(R, T, E)                                                                       \
-    if (e == hipSuccess)                                                                    \
-        e = hipFuncSetAttribute((const void*)k_gather2<R, T, E>,                            \
-                                hipFuncAttributeMaxDynamicSharedMemorySize,                 \
-                                (int)g2_lds<R, T, E>(2048));
-    MJ_A(1, 4, EPI_SWIGLU) MJ_A(2, 4, EPI_SWIGLU) MJ_A(3, 4, EPI_SWIGLU)
-    MJ_A(1, 4, EPI_STORE) MJ_A(2, 2, EPI_STORE) MJ_A(3, 1, EPI_STORE) MJ_A(4, 1, EPI_STORE)
-    MJ_A(1, 4, EPI_ADD) MJ_A(2, 2, EPI_ADD) MJ_A(3, 1, EPI_ADD) MJ_A(4, 1, EPI_ADD)
-#undef MJ_A
-    return e;
 }
 
 // ---------------------------------------------------------------------------------------

@@ -1,0 +1,110 @@
+"""Summaries of rocprofv3 CSV output for the verify pass.
+
+A model pass starts with its token-embedding kernel (k_embed, one workgroup per pass row), so
+a kernel trace or a counter collection splits into passes at each k_embed dispatch and the
+row count of a pass is that dispatch's workgroup count.  The summaries below keep only this
+library's kernels of the passes with a given row count (9 = y plus an 8-token chain draft).
+
+    python -m momij_amd.profiling trace    <run_kernel_trace.csv>       --rows 9 [--last N]
+    python -m momij_amd.profiling counters <run_counter_collection.csv> --rows 9 --scale F
+
+`trace` prints, per kernel and grid size, launches per pass and the mean / median duration;
+`--last N` restricts it to the last N passes of that row count (the eager, event-timed passes
+bench.py runs after its graph-replayed steps).  `counters` prints the mean counter value per
+dispatch in MB, multiplied by `--scale` (the calibration factor of the counter: the ratio of a
+plain copy's known bytes to what the counter reports for it).
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import statistics
+
+
+def _ours(name: str) -> bool:
+    return name.startswith("k_") or name.startswith("void k_")
+
+
+def _key(name: str, grid: int, wg: int) -> str:
+    return f"{name.split('(')[0]} [{grid // max(wg, 1)} wg]"
+
+
+def split_passes(rows, grid_col: str, wg_col: str):
+    """[(rows of the pass, [csv rows of its kernels])] in dispatch order."""
+    passes, cur = [], None
+    for r in rows:
+        name = r["Kernel_Name"]
+        if name.startswith("k_embed"):
+            cur = (int(r[grid_col]) // int(r[wg_col]), [])
+            passes.append(cur)
+        if cur is not None and _ours(name):
+            cur[1].append(r)
+    return passes
+
+
+def trace_summary(path: str, n_rows: int, last: int | None = None) -> str:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    passes = [p for p in split_passes(rows, "Grid_Size_X", "Workgroup_Size_X") if p[0] == n_rows]
+    if last:
+        passes = passes[-last:]
+    if not passes:
+        return f"no passes with {n_rows} rows"
+    stat = collections.defaultdict(list)
+    spans = []
+    for _, ks in passes:
+        t0 = int(ks[0]["Start_Timestamp"])
+        t1 = max(int(k["End_Timestamp"]) for k in ks)
+        spans.append((t1 - t0) / 1e3)
+        for k in ks:
+            d = (int(k["End_Timestamp"]) - int(k["Start_Timestamp"])) / 1e3
+            stat[_key(k["Kernel_Name"], int(k["Grid_Size_X"]), int(k["Workgroup_Size_X"]))].append(d)
+    n = len(passes)
+    out = [f"passes with {n_rows} rows: {n}; pass span (first start to last end) median "
+           f"{statistics.median(spans):.1f} us",
+           f"{'kernel [workgroups]':44s} {'per pass':>8s} {'mean us':>9s} {'median us':>9s} "
+           f"{'us/pass':>9s}"]
+    total = 0.0
+    for k, v in sorted(stat.items(), key=lambda kv: -sum(kv[1])):
+        per = len(v) / n
+        total += statistics.mean(v) * per
+        out.append(f"{k:44s} {per:8.1f} {statistics.mean(v):9.2f} {statistics.median(v):9.2f} "
+                   f"{statistics.mean(v) * per:9.1f}")
+    out.append(f"{'sum of kernel time per pass':44s} {'':8s} {'':9s} {'':9s} {total:9.1f}")
+    return "\n".join(out)
+
+
+def counter_summary(path: str, n_rows: int, scale: float) -> str:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    counter = rows[0]["Counter_Name"] if rows else "?"
+    passes = [p for p in split_passes(rows, "Grid_Size", "Workgroup_Size") if p[0] == n_rows]
+    by = collections.defaultdict(list)
+    for _, ks in passes:
+        for r in ks:
+            by[_key(r["Kernel_Name"], int(r["Grid_Size"]), int(r["Workgroup_Size"]))].append(
+                float(r["Counter_Value"]) * scale * 1024 / 1e6)
+    out = [f"{counter} x {scale:g} per dispatch, passes with {n_rows} rows: {len(passes)}",
+           f"{'kernel [workgroups]':44s} {'dispatches':>10s} {'mean MB':>10s} {'median MB':>10s}"]
+    for k, v in sorted(by.items(), key=lambda kv: -statistics.mean(kv[1])):
+        out.append(f"{k:44s} {len(v):10d} {statistics.mean(v):10.3f} {statistics.median(v):10.3f}")
+    return "\n".join(out)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("kind", choices=["trace", "counters"])
+    ap.add_argument("csv")
+    ap.add_argument("--rows", type=int, default=9)
+    ap.add_argument("--last", type=int, default=None)
+    ap.add_argument("--scale", type=float, default=1.0)
+    a = ap.parse_args()
+    if a.kind == "trace":
+        print(trace_summary(a.csv, a.rows, a.last))
+    else:
+        print(counter_summary(a.csv, a.rows, a.scale))
+
+
+if __name__ == "__main__":
+    main()
