@@ -268,9 +268,12 @@ mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void
     MoeScratch ms;
     mj_status s = moe_scratch(ctx, H, I, E, k, M, ms);
     if (s != MJ_OK) return s;
+    // the op-level scratch is shared with other entry points: expert counts start from zero
+    s = mj_hip(ctx, launch_zero_i32(ms.ecnt[0], E, ctx->stream), "count clear");
+    if (s != MJ_OK) return s;
     return run_moe(ctx, w, (const uint16_t*)x, (uint16_t*)y, M, flags, ms,
                    out_inds ? out_inds : ms.inds, out_scores ? out_scores : ms.scores,
-                   ctx->stream);
+                   ctx->stream, 0, false);
 }
 
 mj_status mj_selftest_mfma(mj_ctx* ctx, const void* A, const void* B, float* D) {
@@ -298,6 +301,9 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
         ms.act = (uint16_t*)a.take((size_t)M * k * I * 2);
         ms.act_sum = (float2*)a.take((size_t)M * k * (I / 64) * sizeof(float2));
         ms.down = (uint16_t*)a.take((size_t)M * k * H * 2);
+        ms.ecnt[0] = (int*)a.take((size_t)E * 4);
+        ms.ecnt[1] = (int*)a.take((size_t)E * 4);
+        ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
     };
     layout(ar);
     mj_status s = mj_scratch_reserve(ctx, ar.off);
@@ -309,7 +315,7 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
 
 mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
                   int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st,
-                  Prof* prof) {
+                  int slot, bool clear_other, Prof* prof) {
     const int H = w->H, I = w->I, E = w->E, k = w->top_k;
     const int* ab = ctx->abort_dev;
     const uint16_t* xn = x;
@@ -325,7 +331,9 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.xsum = M > 1 ? ms.xsum : nullptr;
         ra.inds = inds;
         ra.scores = scores;
-        ra.bk = M > 1 ? ms.bk : nullptr;
+        ra.ecnt = ms.ecnt[slot];
+        ra.eplist = ms.eplist;
+        ra.ecnt_clear = clear_other ? ms.ecnt[slot ^ 1] : nullptr;
         ra.M = M;
         ra.E = E;
         ra.k = k;
@@ -394,14 +402,26 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
                        "topk");
             if (s != MJ_OK) return s;
         }
+        // the tile kernels find each expert's rows themselves; the fallback kernels take the
+        // buckets (built here unless the unfused router already did)
+        const bool up_tile = gather3_supported(EPI_SWIGLU, H, 2 * I, w->gs);
+        const bool dn_tile = gather3_supported(EPI_STORE, I, H, w->gs);
         const int nb = M * k < E ? M * k : E;
+        // expert lists come from the fused route; the unfused one leaves buckets instead
+        const bool lists = fused;
+        if (lists && (!up_tile || !dn_tile)) {
+            s = mj_hip(ctx, launch_bucket_inds(inds, M * k, ms.bk, ab, st), "bucket");
+            if (s != MJ_OK) return s;
+        }
         GatherArgs up{};
         up.xperm = ms.xperm;
         up.xsum = ms.xsum;
         up.w = w->up_gate_w;
         up.s = (const uint16_t*)w->up_gate_s;
         up.b = (const uint16_t*)w->up_gate_b;
-        up.bk = ms.bk;
+        up.ecnt = up_tile && lists ? ms.ecnt[slot] : nullptr;
+        up.eplist = ms.eplist;
+        up.bk = up.ecnt ? nullptr : ms.bk;
         up.y = ms.act;
         up.ysum = ms.act_sum;
         up.K = H;
@@ -410,13 +430,11 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         up.x_div = k;
         up.abort = ab;
         if (prof) prof->begin(PROF_UP, st);
-        s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, nb, st), "up gather");
+        s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, up.ecnt ? E : nb, st), "up gather");
         if (prof) prof->end(st);
         if (s != MJ_OK) return s;
         // the tile kernel's SwiGLU epilogue writes act without block sums: the tile down
         // kernel forms them from its staged rows, any other down kernel gets them here
-        const bool up_tile = gather3_supported(EPI_SWIGLU, H, 2 * I, w->gs);
-        const bool dn_tile = gather3_supported(EPI_STORE, I, H, w->gs);
         if (up_tile && !dn_tile) {
             s = mj_hip(ctx, launch_qx_sums(ms.act, ms.act_sum, M * k, I, ab, st), "act sums");
             if (s != MJ_OK) return s;
@@ -427,7 +445,9 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         dn.w = w->down_w;
         dn.s = (const uint16_t*)w->down_s;
         dn.b = (const uint16_t*)w->down_b;
-        dn.bk = ms.bk;
+        dn.ecnt = dn_tile && lists ? ms.ecnt[slot] : nullptr;
+        dn.eplist = ms.eplist;
+        dn.bk = dn.ecnt ? nullptr : ms.bk;
         dn.y = ms.down;
         dn.K = I;
         dn.N = H;
@@ -435,7 +455,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         dn.x_div = 1;
         dn.abort = ab;
         if (prof) prof->begin(PROF_DOWN, st);
-        s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, nb, st), "down gather");
+        s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, dn.ecnt ? E : nb, st), "down gather");
         if (prof) prof->end(st);
         if (s != MJ_OK) return s;
     }

@@ -7,8 +7,8 @@
 // every load of its weights (codes, scales, biases) before its first wait and needs no
 // cross-wave reduction.  Lane (n = lane % 16, q = lane / 16) streams the contiguous quarter
 // q of row n: K/256 64-blocks = K/16 bytes of codes, one vector of scales and one of biases.
-// A block is WPB such waves over one expert bucket (or the dense projection): it stages the
-// bucket's activation rows (qx order, <= 4*RG per pass) in LDS once for all its waves.
+// A block is WPB such waves over one expert (or the dense projection): it stages the rows
+// routed to the expert (qx order, <= 16 per pass) in LDS once for all its waves.
 // The MFMA A operand carries activation row m only on the A rows 4q+m of k-quarter q, so one
 // MFMA yields a separate sum per quarter (= per lane 64-block) and every 64-block keeps its
 // own scale and bias; the quarters are added after the K loop.
@@ -50,7 +50,7 @@ struct G5Shape {
     // K-slice partials: in a wave's own tile area when a bucket is one pass (RA < R), else in
     // their own region (later passes reuse the tiles)
     static constexpr int RED = (KS - 1) * TPB * 64 * 16;
-    static size_t lds(int RA) {
+    __host__ __device__ static size_t lds(int RA) {
         return (size_t)WPB * WAVE_BYTES + (size_t)RA * XS * 2 + (size_t)RA * SS * 8 +
                (EPI == EPI_QKV ? (size_t)R * ES * 4 : 0) + (RA == R ? RED : 0);
     }
@@ -112,21 +112,27 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
     const int tt = wv % TPB, kh = wv / TPB;   // weight tile and K-slice of this wave
     const int ncb = a.N / (16 * TPB);
     const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
-    const Buckets* bk = a.bk;
     const bool own_sums = a.xsum == nullptr;  // block sums formed here from the staged rows
 
-    // bucket header and abort word together
-    int e = 0, p0 = 0, np = a.dense_rows;
+    // Expert mode: block u serves expert u (an expert nobody picked ends here).  Bucket mode:
+    // block u serves the u-th expert of a Buckets table.  Dense: rows 0 .. dense_rows-1.
+    const int* plist = nullptr;
+    int e = 0, np = a.dense_rows;
     {
         const int ab = a.abort ? *a.abort : 0;
-        if (bk != nullptr) {
+        if (a.ecnt != nullptr) {
+            e = u;
+            np = a.ecnt[u];
+            plist = a.eplist + u * MJ_ROWS;
+        } else if (a.bk != nullptr) {
+            const Buckets* bk = a.bk;
             const int cnt = bk->count, ee = bk->expert[u], s0 = bk->start[u], s1 = bk->start[u + 1];
             if (u >= cnt) return;  // whole block
             e = ee;
-            p0 = s0;
             np = s1 - s0;
+            plist = bk->pair + s0;
         }
-        if (ab) return;  // whole block
+        if (ab || np <= 0) return;  // whole block
     }
 
     extern __shared__ __align__(16) char g5lds[];
@@ -144,7 +150,7 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
     // MFMA output rows that are discarded).  Wave w stages rows w, w + WPB, ...
     auto stage_load = [&](int pb, int npass) {
         const int myr = min(pb + (lane < R ? lane : 0), np - 1);
-        const int prl = bk ? bk->pair[p0 + myr] : myr;
+        const int prl = plist ? plist[myr] : myr;
 #pragma unroll
         for (int j = 0; j < R / WPB; ++j) {
             const int r = wv + WPB * j;

@@ -63,14 +63,20 @@ struct QkvEpi {
     float eps;
 };
 
+// Row sets of a gather launch (grid = groups x column blocks):
+//   ecnt != nullptr (tile kernel): group u = expert u with ecnt[u] pairs listed, in no particular
+//   order, at eplist[u * MJ_ROWS ..] (an expert takes each row at most once);
+//   bk != nullptr: group u = bucket u of the table;  neither: dense, one group of dense_rows.
 struct GatherArgs {
     const uint16_t* xperm;  // qx activations [rows_x][K]
     const float2* xsum;     // [rows_x][K/64] {sum x, sum base*x}
     const uint32_t* w;      // [E][N][K/16]
     const uint16_t* s;      // [E][N][K/gs]
     const uint16_t* b;
-    const Buckets* bk;      // nullptr: dense, one bucket (expert 0) with pairs 0..dense_rows-1
-    int dense_rows;
+    const Buckets* bk;      // fallback kernel: rows grouped by expert (nullptr: dense)
+    const int* ecnt;        // tile kernel: pairs per expert [E]
+    const int* eplist;      // tile kernel: pair lists [E][MJ_ROWS]
+    int dense_rows;         // dense: rows 0 .. dense_rows-1 of expert 0
     uint16_t* y;            // STORE/ADD: [pairs][N] ; SWIGLU: act qx [pairs][I]
     float2* ysum;           // SWIGLU: act sums [pairs][I/64]
     int K, N, gs;
@@ -174,12 +180,15 @@ struct RouteArgs {
     float2* xsum;            // [M][H/64]
     int32_t* inds;           // [M][k]
     float* scores;           // [M][k]
-    Buckets* bk;             // optional
+    int* ecnt;               // pairs per expert [E] (zero on entry; counted here)
+    int* eplist;             // pair lists [E][MJ_ROWS]
+    int* ecnt_clear;         // counts of the next route launch, zeroed here (nullable)
     int M, E, k;
     float eps;
     const int* abort;
 };
 bool route_supported(int H, int E, int k);
+hipError_t launch_zero_i32(int* p, int n, hipStream_t st);  // fill kernel (graph-safe)
 hipError_t launch_route(const RouteArgs& a, int H, hipStream_t st);
 hipError_t launch_score_combine(const uint16_t* down, const float* scores, const uint16_t* x_resid,
                                 uint16_t* y, int M, int k, int H, const int* abort,

@@ -176,8 +176,9 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, hipStream_t st) {
     if (s != MJ_OK) return s;
     int32_t* inds = m->inds_all + (size_t)l * MJ_MAX_ROWS * c.top_k;
     float* scores = m->scores_all + (size_t)l * MJ_MAX_ROWS * c.top_k;
+    // alternate layers use alternate expert-count buffers; each route clears the other one
     return run_moe(ctx, &w.moe, m->h, m->h, M, MJ_MOE_PRENORM | MJ_MOE_RESIDUAL, m->ms, inds,
-                   scores, st, pf);
+                   scores, st, l & 1, true, pf);
 }
 
 static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
@@ -208,6 +209,12 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                        "capture");
             if (s != MJ_OK) return s;
         }
+    }
+    // layer l fills expert-count buffer l & 1 and clears the other: with an odd layer count
+    // the last layer used buffer 0, which the next pass starts from
+    if (c.n_layers & 1) {
+        s = mj_hip(ctx, launch_zero_i32(m->ms.ecnt[0], c.E, st), "count clear");
+        if (s != MJ_OK) return s;
     }
     if (kind != PASS_PREFILL) {
         s = mj_hip(ctx, launch_rmsnorm_qx(m->h, m->final_norm, c.eps, m->xf, nullptr, nullptr, M,
@@ -377,6 +384,9 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         ms.act = (uint16_t*)a.take((size_t)R * c.top_k * c.I * 2);
         ms.act_sum = (float2*)a.take((size_t)R * c.top_k * (c.I / 64) * 8);
         ms.down = (uint16_t*)a.take((size_t)R * c.top_k * H * 2);
+        ms.ecnt[0] = (int*)a.take((size_t)c.E * 4);
+        ms.ecnt[1] = (int*)a.take((size_t)c.E * 4);
+        ms.eplist = (int*)a.take((size_t)c.E * MJ_MAX_ROWS * 4);
     };
     Arena count;
     layout(count);

@@ -249,249 +249,185 @@ hipError_t launch_score_combine(const uint16_t* down, const float* scores, const
     return hipGetLastError();
 }
 
-// ---------------------------------------------------------------------------------------
-// Fused MoE front: RMSNorm of the pass rows, router logits on MFMA, softmax / top-k per row
-// and the expert buckets, in one 512-thread block (the whole step is a few hundred KB, so
-// one launch with every load issued up front beats four dependent launches).
-// Arithmetic as above except the order of the logit sum (MFMA over 32-element k slices,
-// then the two K-halves in order).  H = 2048: rows go in chunks of 16 (wave w normalises
-// rows w and w + 8 of the chunk); for the router the 8 waves are 4 expert tiles x 2 K-halves
-// of 1024 and each keeps its slice of the router rows of one 64-expert chunk in registers.
-// ---------------------------------------------------------------------------------------
 #define RT_H 2048
-#define RT_XS (RT_H + 8)  // LDS row stride (halves)
-#define RT_NS 32          // MFMA k-steps per wave (1024 / 32)
 
-static constexpr size_t route_lds_bytes() {
-    return (size_t)16 * RT_XS * 2 + 2 * 16 * 64 * 4 + 16 * MJ_MAX_EXPERTS * 4 +
-           MJ_MAX_EXPERTS * 8 + MJ_MAX_PAIRS * 4 + MJ_MAX_EXPERTS * 4 + 16;
-}
+// ---------------------------------------------------------------------------------------
+// MoE front, one 512-thread block per pass row: RMSNorm of the row (written plain and in qx
+// order with its block sums), its E router logits and its top-k, with no dependency between
+// blocks.  Every block reads the whole router (E x 2048 fp16, L2-resident after the first
+// rows) -- the price of needing no grid-wide synchronisation.
+// Arithmetic as maple_rms_norm / maple_batched_gemv / maple_route_top8: fp32 sums (the logit
+// sums in v_dot2 lane partials and a fixed shuffle tree), softmax with max subtraction, top-k
+// by logit with the lowest index winning ties, weights renormalised over the k in rank order.
+// The top-k ranks every expert against all E logits (broadcast LDS reads), so the selection
+// comes out sorted without a chain of cross-lane reductions.
+// ---------------------------------------------------------------------------------------
+#define RR_EPW 8  // router rows per wave per round (8 waves -> 64 experts a round)
 
-__global__ __launch_bounds__(512) void k_route(RouteArgs a) {
+__global__ __launch_bounds__(512) void k_route_row(RouteArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int M = a.M, E = a.E, k = a.k;
-    extern __shared__ __align__(16) char rt_lds[];
-    uint16_t* xs = (uint16_t*)rt_lds;                                  // [16][RT_XS]
-    float* red = (float*)(xs + 16 * RT_XS);                            // [2][16][64]
-    float* lg = red + 2 * 16 * 64;                                     // [16][E]
-    unsigned long long* s_mask = (unsigned long long*)(lg + 16 * MJ_MAX_EXPERTS);  // [E]
-    int* s_inds = (int*)(s_mask + MJ_MAX_EXPERTS);                     // [M*k]
-    int* s_start = s_inds + MJ_MAX_PAIRS;                              // [E]
-    int* s_abort = s_start + MJ_MAX_EXPERTS;
+    const int r = blockIdx.x, E = a.E, k = a.k;
+    // the other count buffer is cleared for the next launch even when this one is aborted (the
+    // launch that used it has completed: stream order)
+    if (blockIdx.x == 0 && a.ecnt_clear)
+        for (int e = tid; e < E; e += 512) a.ecnt_clear[e] = 0;
+    __shared__ __align__(16) uint16_t xn[RT_H];
+    __shared__ float s_ss[4];
+    __shared__ __align__(16) float s_lg[MJ_MAX_EXPERTS];
+    __shared__ float s_gate[8];
+    if (aborted(a.abort)) return;  // whole grid: the abort word is fixed during a launch
 
-    const int et = wv & 3, kh = wv >> 2;
-    const int ecol = et * 16 + (lane & 15);
-    const int kl = kh * 1024 + 8 * (lane >> 4);
-    u4v wr[RT_NS];
-#pragma unroll
-    for (int s = 0; s < RT_NS; ++s)
-        wr[s] = *(const u4v*)(a.W + (size_t)ecol * RT_H + kl + 32 * s);
-    for (int e = tid; e < MJ_MAX_EXPERTS; e += 512) s_mask[e] = 0ull;
-
-    for (int c0 = 0; c0 < M; c0 += 16) {
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int rl = wv + 8 * half, r = c0 + rl;
-            u4v o[4];
-            if (r < M) {
-                const uint16_t* xr = a.x + (size_t)r * RT_H;
-                u4v nw[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    o[c] = *(const u4v*)(xr + 512 * c + 8 * lane);
-                    nw[c] = a.norm_w ? *(const u4v*)(a.norm_w + 512 * c + 8 * lane)
-                                     : (u4v){0u, 0u, 0u, 0u};
-                }
-                if (a.norm_w) {
-                    float ss = 0.0f;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const float x0 = h2f(o[c][j] & 0xFFFFu), x1 = h2f(o[c][j] >> 16);
-                            ss += x0 * x0;
-                            ss += x1 * x1;
-                        }
-                    ss = wave_sum(ss);
-                    const float inv = 1.0f / sqrtf(ss / (float)RT_H + a.eps);
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const float x0 = h2f(o[c][j] & 0xFFFFu) * inv * h2f(nw[c][j] & 0xFFFFu);
-                            const float x1 = h2f(o[c][j] >> 16) * inv * h2f(nw[c][j] >> 16);
-                            o[c][j] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
-                        }
-                }
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) o[c] = (u4v){0u, 0u, 0u, 0u};
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) *(u4v*)(xs + rl * RT_XS + 512 * c + 8 * lane) = o[c];
-        }
-        if (c0 == 0 && tid == 0) *s_abort = a.abort ? *a.abort : 0;
-        __syncthreads();
-        if (*s_abort) {
-            if (tid == 0 && a.bk) a.bk->count = 0;
-            return;  // block-uniform
-        }
-        // normed rows out (plain and / or qx)
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int rl = wv + 8 * half, r = c0 + rl;
-            if (r < M && (a.xn || a.xperm)) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int k0 = 512 * c + 8 * lane;
-                    const u4v o = *(const u4v*)(xs + rl * RT_XS + k0);
-                    if (a.xn) *(u4v*)(a.xn + (size_t)r * RT_H + k0) = o;
-                    if (a.xperm)
-                        emit_qx(o, lane, a.xperm + (size_t)r * RT_H,
-                                a.xsum + (size_t)r * (RT_H / 64), k0);
-                }
-            }
-        }
-        for (int e0 = 0; e0 < E; e0 += 64) {
-            if (e0 > 0 || c0 > 0) {
-#pragma unroll
-                for (int s = 0; s < RT_NS; ++s)
-                    wr[s] = *(const u4v*)(a.W + (size_t)(e0 + ecol) * RT_H + kl + 32 * s);
-            }
-            f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < RT_NS; ++s) {
-                const u4v av = *(const u4v*)(xs + (lane & 15) * RT_XS + kl + 32 * s);
-                d = mfma16x16x32(as_h8(av), as_h8(wr[s]), d);
-            }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) red[(kh * 16 + 4 * (lane >> 4) + q) * 64 + ecol] = d[q];
-            __syncthreads();
-#pragma unroll
-            for (int rep = 0; rep < 2; ++rep) {
-                const int idx = tid + 512 * rep, row = idx >> 6, col = idx & 63;
-                lg[row * E + e0 + col] =
-                    red[(0 * 16 + row) * 64 + col] + red[(1 * 16 + row) * 64 + col];
-            }
-            __syncthreads();
-        }
-        // softmax + top-k, wave wv <-> rows wv and wv + 8 of the chunk
-        for (int half = 0; half < 2; ++half) {
-            const int rl = wv + 8 * half, r = c0 + rl;
-            if (r >= M) continue;
-            const float* lr = lg + rl * E;
-            float lv[4], work[4], g[4];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = lane + 64 * i;
-                lv[i] = e < E ? lr[e] : -INFINITY;
-                mx = fmaxf(mx, lv[i]);
-            }
-            mx = wave_max(mx);
-            float z = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = lane + 64 * i;
-                g[i] = e < E ? expf(lv[i] - mx) : 0.0f;
-                z += g[i];
-                work[i] = lv[i];
-            }
-            z = wave_sum(z);
-            // lane j keeps the j-th pick
-            float mysel = 0.0f, ssum = 0.0f;
-            int myidx = 0;
-            for (int j = 0; j < k; ++j) {
-                float bv = work[0];
-                int bi = lane;
-#pragma unroll
-                for (int i = 1; i < 4; ++i)
-                    if (work[i] > bv) {
-                        bv = work[i];
-                        bi = lane + 64 * i;
-                    }
-                wave_argmax(bv, bi);
-                float gsel = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (lane + 64 * i == bi) {
-                        work[i] = -INFINITY;
-                        gsel = g[i] / z;
-                    }
-                gsel = __shfl(gsel, bi & 63, MJ_WAVE);
-                ssum += gsel;
-                if (lane == j) {
-                    mysel = gsel;
-                    myidx = bi;
-                }
-            }
-            if (lane < k) {
-                a.inds[r * k + lane] = myidx;
-                a.scores[r * k + lane] = mysel / ssum;
-                s_inds[r * k + lane] = myidx;
-                atomicOr(&s_mask[myidx], 1ull << r);
-            }
-        }
-        __syncthreads();  // xs / lg reuse, masks complete
+    // row r: threads 0..255 hold 8 consecutive elements each
+    u4v xv = {0u, 0u, 0u, 0u}, nw = {0u, 0u, 0u, 0u};
+    if (tid < 256) {
+        xv = *(const u4v*)(a.x + (size_t)r * RT_H + 8 * tid);
+        if (a.norm_w) nw = *(const u4v*)(a.norm_w + 8 * tid);
     }
-    if (a.bk == nullptr) return;
-    Buckets* bk = a.bk;
-    // experts in increasing id; each bucket lists its pairs in increasing (row, slot) order
-    if (wv == 0) {
-        int cnt[4], tot = 0, nz = 0;
+    // the first round of router rows: expert wv + 8 j, k = 512 c + 8 lane .. +7
+    u4v wr[RR_EPW][4];
+    auto load_round = [&](int e0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = 4 * lane + i;
-            cnt[i] = e < E ? __popcll(s_mask[e]) : 0;
-            tot += cnt[i];
-            nz += cnt[i] > 0;
+        for (int j = 0; j < RR_EPW; ++j) {
+            const int e = min(e0 + wv + 8 * j, E - 1);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                wr[j][c] = *(const u4v*)(a.W + (size_t)e * RT_H + 512 * c + 8 * lane);
         }
-        int ptot = tot, pnz = nz;
+    };
+    load_round(0);
+
+    // RMSNorm
+    if (a.norm_w) {
+        float ss = 0.0f;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int t1 = __shfl_up(ptot, o, MJ_WAVE), t2 = __shfl_up(pnz, o, MJ_WAVE);
-            if (lane >= o) {
-                ptot += t1;
-                pnz += t2;
+        for (int q = 0; q < 4; ++q) {
+            const float x0 = h2f(xv[q] & 0xFFFFu), x1 = h2f(xv[q] >> 16);
+            ss += x0 * x0;
+            ss += x1 * x1;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0 && wv < 4) s_ss[wv] = ss;
+        __syncthreads();
+        const float tot = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+        const float inv = 1.0f / sqrtf(tot / (float)RT_H + a.eps);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float x0 = h2f(xv[q] & 0xFFFFu) * inv * h2f(nw[q] & 0xFFFFu);
+            const float x1 = h2f(xv[q] >> 16) * inv * h2f(nw[q] >> 16);
+            xv[q] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
+        }
+    }
+    if (tid < 256) {
+        *(u4v*)(xn + 8 * tid) = xv;
+        if (a.xn) *(u4v*)(a.xn + (size_t)r * RT_H + 8 * tid) = xv;
+        if (a.xperm)
+            emit_qx(xv, lane, a.xperm + (size_t)r * RT_H, a.xsum + (size_t)r * (RT_H / 64), 8 * tid);
+    }
+    __syncthreads();
+
+    // logits: all partial dot products of a round, then their reductions together
+    u4v xa[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xa[c] = *(const u4v*)(xn + 512 * c + 8 * lane);
+    for (int e0 = 0; e0 < E; e0 += 8 * RR_EPW) {
+        if (e0 > 0) load_round(e0);
+        float acc[RR_EPW];
+#pragma unroll
+        for (int j = 0; j < RR_EPW; ++j) {
+            acc[j] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[j] = dot2(wr[j][c][q], xa[c][q], acc[j]);
+        }
+#pragma unroll
+        for (int m = 32; m > 0; m >>= 1)
+#pragma unroll
+            for (int j = 0; j < RR_EPW; ++j) acc[j] += __shfl_xor(acc[j], m, MJ_WAVE);
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < RR_EPW; ++j) {
+                const int e = e0 + wv + 8 * j;
+                if (e < E) s_lg[e] = acc[j];
             }
-        }
-        int pos = ptot - tot, u = pnz - nz;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = 4 * lane + i;
-            if (e < E) s_start[e] = pos;
-            if (cnt[i] > 0) {
-                bk->expert[u] = e;
-                bk->start[u] = pos;
-                ++u;
-            }
-            pos += cnt[i];
-        }
-        if (lane == 63) {
-            bk->count = pnz;
-            bk->start[pnz] = ptot;
         }
     }
     __syncthreads();
-    for (int p = tid; p < M * k; p += 512) {
-        const int e = s_inds[p], r = p / k;
-        const int rank = __popcll(s_mask[e] & ((1ull << r) - 1ull));
-        bk->pair[s_start[e] + rank] = p;
+    if (wv != 0) return;
+
+    // top-k of the row (wave 0): lane holds experts lane + 64 i
+    float lv[4];
+    int rank[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        lv[i] = e < E ? s_lg[e] : -INFINITY;
+        mx = fmaxf(mx, lv[i]);
+        rank[i] = 0;
+    }
+    for (int e2 = 0; e2 < E; e2 += 4) {
+        const f4 o = *(const f4*)(s_lg + e2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int e = lane + 64 * i;
+                rank[i] += (int)(o[c] > lv[i]) + (int)(o[c] == lv[i]) * (int)(e2 + c < e);
+            }
+    }
+    mx = wave_max(mx);
+    float z = 0.0f, g[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        g[i] = e < E ? expf(lv[i] - mx) : 0.0f;
+        z += g[i];
+    }
+    z = wave_sum(z);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && rank[i] < k) {
+            s_gate[rank[i]] = g[i] / z;
+            a.inds[r * k + rank[i]] = e;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < k) {
+        float ssum = 0.0f;
+        for (int j = 0; j < k; ++j) ssum += s_gate[j];  // in rank order
+        a.scores[r * k + lane] = s_gate[lane] / ssum;
+    }
+    // append (row, slot) pairs to the experts' lists (order inside a list is immaterial: every
+    // pair's output is computed the same way wherever it sits)
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        if (e < E && rank[i] < k) {
+            const int pos = atomicAdd(&a.ecnt[e], 1);
+            a.eplist[e * MJ_ROWS + pos] = r * k + rank[i];
+        }
     }
 }
 
-bool route_supported(int H, int E, int k) {
-    return H == RT_H && E % 64 == 0 && E <= MJ_MAX_EXPERTS && k >= 1 && k <= 8;
+__global__ void k_zero_i32(int* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
 }
 
-hipError_t launch_route(const RouteArgs& a, int H, hipStream_t st) {
-    if (!route_supported(H, a.E, a.k) || a.M < 1 || a.M > MJ_ROWS || a.M * a.k > MJ_MAX_PAIRS)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_route, dim3(1), dim3(512), route_lds_bytes(), st, a);
+hipError_t launch_zero_i32(int* p, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_zero_i32, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
     return hipGetLastError();
 }
 
-hipError_t set_moe_attributes() {
-    return hipFuncSetAttribute((const void*)k_route, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)route_lds_bytes());
+bool route_supported(int H, int E, int k) {
+    return H == RT_H && E >= 8 && E <= MJ_MAX_EXPERTS && E % 4 == 0 && k >= 1 && k <= 8 && k <= E;
 }
+
+hipError_t launch_route(const RouteArgs& a, int H, hipStream_t st) {
+    if (!route_supported(H, a.E, a.k) || a.M < 1 || a.M > MJ_ROWS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route_row, dim3(a.M), dim3(512), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t set_moe_attributes() { return hipSuccess; }
