@@ -15,6 +15,11 @@
 #include "mj_abi_internal.h"
 #include "mj_internal.h"
 
+TimedLaunch& timed_launch() {
+    static thread_local TimedLaunch t;
+    return t;
+}
+
 mj_status mj_fail(mj_ctx* ctx, mj_status st, const char* fmt, ...) {
     if (ctx) {
         char buf[512];

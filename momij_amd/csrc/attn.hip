@@ -332,7 +332,7 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
     const int nqt = (a.M * gqa + 15) / 16;
     const size_t lds = (size_t)(nqt * 16 * QSTR + AK * QSTR + HD * VSTR + 4 * 16 * VSTR) * 2 +
                        AK * (8 + 4) + 16;
-    hipLaunchKernelGGL(k_attn_chunk, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a);
+    launch_timed(k_attn_chunk, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.M * a.nQ), dim3(256), 0, st, a);

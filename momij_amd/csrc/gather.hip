@@ -416,8 +416,8 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     const int ncb = a.N / (16 * S::TPB);
     const int RA = rows < S::R ? (rows < 1 ? 1 : rows) : S::R;
     const size_t lds = S::lds(RA);
-    hipLaunchKernelGGL((k_gather5<KPL, GS, EPI, WPB, KS>), dim3(n_buckets * ncb), dim3(WPB * 64),
-                       lds, st, a, RA);
+    launch_timed(k_gather5<KPL, GS, EPI, WPB, KS>, dim3(n_buckets * ncb), dim3(WPB * 64), lds, st,
+                 a, RA);
     return hipGetLastError();
 }
 

@@ -175,10 +175,10 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
                    logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
         if (mg <= 16) {
             const size_t lds = (size_t)16 * (K + 8) * 2;
-            hipLaunchKernelGGL(k_lm_head<1>, dim3(nb), dim3(512), lds, st, a);
+            launch_timed(k_lm_head<1>, dim3(nb), dim3(512), lds, st, a);
         } else {
             const size_t lds = (size_t)32 * (K + 8) * 2;
-            hipLaunchKernelGGL(k_lm_head<2>, dim3(nb), dim3(512), lds, st, a);
+            launch_timed(k_lm_head<2>, dim3(nb), dim3(512), lds, st, a);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -294,6 +294,22 @@ __global__ __launch_bounds__(256) void k_embed(const uint16_t* table, const Step
 hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
                         const int* abort, hipStream_t st) {
     hipLaunchKernelGGL(k_embed, dim3(M), dim3(256), 0, st, table, sd, M, H, h, abort);
+    return hipGetLastError();
+}
+
+// The wall clock (s_memrealtime) ticks at 100 MHz; the loop also stops after a fixed number
+// of sleeps, so it ends even if the clock were not to advance.
+__global__ __launch_bounds__(64) void k_hold(unsigned ticks) {
+    const unsigned long long t0 = wall_clock64();
+    for (int i = 0; i < (1 << 22); ++i) {
+        if (wall_clock64() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(8);
+    }
+}
+
+hipError_t launch_hold(unsigned us, hipStream_t st) {
+    if (us > 100000) us = 100000;
+    hipLaunchKernelGGL(k_hold, dim3(1), dim3(64), 0, st, us * 100u);
     return hipGetLastError();
 }
 

@@ -40,19 +40,27 @@ struct MoeScratch {
 };
 
 // Optional per-kernel-class event timing of eager passes (classes of mj_model_kernel_ms).
-enum { PROF_UP = 0, PROF_DOWN = 1, PROF_HEAD = 2, PROF_ATTN = 3, PROF_DENSE = 4, PROF_CLASSES = 5 };
+enum {
+    PROF_UP = 0, PROF_DOWN = 1, PROF_HEAD = 2, PROF_ATTN = 3, PROF_DENSE = 4,
+    PROF_EMPTY = 5,  // event pairs around nothing: the cost of the timer itself
+    PROF_CLASSES = 6
+};
 struct Prof {
     hipEvent_t* pool = nullptr;
     int cap = 0, used = 0;
     int cls[1024];
-    void begin(int c, hipStream_t st) {
+    bool valid[1024];
+    // arms the next timing-aware launch with the event pair of this slot
+    void begin(int c, hipStream_t) {
         if (!pool || used + 2 > cap) return;
         cls[used / 2] = c;
-        hipEventRecord(pool[used], st);
+        timed_launch() = TimedLaunch{pool[used], pool[used + 1], true};
     }
-    void end(hipStream_t st) {
+    void end(hipStream_t) {
         if (!pool || used + 2 > cap) return;
-        hipEventRecord(pool[used + 1], st);
+        TimedLaunch& t = timed_launch();
+        valid[used / 2] = !t.armed;  // the launch consumed the events
+        t.armed = false;
         used += 2;
     }
 };

@@ -1,7 +1,30 @@
 // mj_internal.h -- launchers shared between the kernel files and the C ABI layer.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+// Kernel-duration timing for measurement: when armed, the next launch made through
+// launch_timed() passes `start` / `stop` to hipExtLaunchKernel, which stamps the kernel's own
+// start and end (the interval a kernel trace reports, without the dispatch gap an event pair
+// recorded around the launch would add); the launch disarms it.
+struct TimedLaunch {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool armed = false;
+};
+TimedLaunch& timed_launch();  // per host thread
+
+template <typename K, typename... Args>
+inline void launch_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st,
+                         Args... args) {
+    TimedLaunch& t = timed_launch();
+    if (t.armed) {
+        t.armed = false;
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, st, t.start, t.stop, 0u, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+    }
+}
 
 #define MJ_MAX_EXPERTS 256
 #define MJ_MAX_PAIRS 512  // rows * top_k per pass
@@ -149,6 +172,9 @@ hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, in
                             hipStream_t st);
 hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
                         const int* abort, hipStream_t st);
+// One wave that waits `us` microseconds of wall-clock time (bounded), so that the host can
+// queue the launches that follow it before the GPU reaches them.
+hipError_t launch_hold(unsigned us, hipStream_t st);
 
 // sample.hip
 hipError_t launch_accept_sampled(const float* logits, int rows, int V, const int32_t* draft,

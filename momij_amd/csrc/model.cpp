@@ -55,8 +55,8 @@ struct mj_model {
     float last_ms = -1.0f;
     bool profiling = false;
     Prof prof;
-    double prof_ms[PROF_CLASSES] = {0, 0, 0, 0, 0};
-    long prof_n[PROF_CLASSES] = {0, 0, 0, 0, 0};
+    double prof_ms[PROF_CLASSES] = {};
+    long prof_n[PROF_CLASSES] = {};
 };
 
 static mj_status model_fail(mj_model* m, mj_status s, const char* what) {
@@ -265,6 +265,19 @@ static mj_status run_pass(mj_model* m, int kind, int M) {
     const bool capture_ok =
         m->graphs && !m->cap_h && !m->cap_inds && !m->cap_logits && !m->profiling;
     m->prof.used = 0;
+    // A profiled pass is queued behind a hold, so every kernel starts as soon as its
+    // predecessor ends: its event pair then brackets the kernel, not the host's launch gap.
+    if (m->profiling && !capture_ok) {
+        s = mj_hip(ctx, launch_hold(15000, st), "hold");
+        if (s != MJ_OK) return s;
+        for (int j = 0; j < 8 && m->prof.used + 2 <= m->prof.cap; ++j) {
+            Prof& p = m->prof;
+            p.cls[p.used / 2] = PROF_EMPTY;
+            p.valid[p.used / 2] = hipEventRecord(p.pool[p.used], st) == hipSuccess &&
+                                  hipEventRecord(p.pool[p.used + 1], st) == hipSuccess;
+            p.used += 2;
+        }
+    }
     hipEventRecord(m->ev0, st);
     if (capture_ok) {
         const int key = kind * 1000 + M;
@@ -296,7 +309,8 @@ static mj_status run_pass(mj_model* m, int kind, int M) {
     if (m->profiling) {
         for (int i = 0; i + 1 < m->prof.used; i += 2) {
             float ms = 0.0f;
-            if (hipEventElapsedTime(&ms, m->prof.pool[i], m->prof.pool[i + 1]) == hipSuccess) {
+            if (m->prof.valid[i / 2] &&
+                hipEventElapsedTime(&ms, m->prof.pool[i], m->prof.pool[i + 1]) == hipSuccess) {
                 m->prof_ms[m->prof.cls[i / 2]] += ms;
                 m->prof_n[m->prof.cls[i / 2]] += 1;
             }
@@ -478,8 +492,11 @@ mj_status mj_model_profile(mj_model* m, int enable) {
     if (enable && !m->prof.pool) {
         m->prof.cap = 2048;
         m->prof.pool = new hipEvent_t[m->prof.cap];
+        // timing-only events: no system-scope cache write-back / invalidate at each record,
+        // which would otherwise sit inside every bracketed kernel's measured time
         for (int i = 0; i < m->prof.cap; ++i)
-            if (hipEventCreate(&m->prof.pool[i]) != hipSuccess)
+            if (hipEventCreateWithFlags(&m->prof.pool[i], hipEventDisableSystemFence) !=
+                hipSuccess)
                 return mj_fail(m->ctx, MJ_HIP_ERROR, "profile events");
     }
     m->profiling = enable != 0;

@@ -402,11 +402,11 @@ static hipError_t launch_gather_t(const GatherArgs& a, int n_buckets_max, hipStr
     constexpr int TPW = 2;
     if constexpr (EPI == EPI_SWIGLU) {
         const int blocks = n_buckets_max * (a.N / 2 / 64);
-        hipLaunchKernelGGL((k_gather<RG, EPI, TPW>), dim3(blocks), dim3(512), 0, st, a);
+        launch_timed(k_gather<RG, EPI, TPW>, dim3(blocks), dim3(512), 0, st, a);
     } else {
         const int groups = (a.N / 16 + TPW - 1) / TPW;
         const int waves = n_buckets_max * groups;
-        hipLaunchKernelGGL((k_gather<RG, EPI, TPW>), dim3((waves + 3) / 4), dim3(256), 0, st, a);
+        launch_timed(k_gather<RG, EPI, TPW>, dim3((waves + 3) / 4), dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }
