@@ -144,9 +144,16 @@ class VerifyEngine:
         return acc.value, tok.value
 
 
-def random_model(cfg: MapleLikeConfig, seed: int = 0, device: str = "cuda"):
+def random_model(cfg: MapleLikeConfig, seed: int = 0, device: str = "cuda",
+                 embed_std: float = 1.0):
     """Random-init weights of the configuration on the device (same distributions as the
-    2-bit workloads); returns (layers, embed, final_norm_w, lm_head)."""
+    2-bit workloads); returns (layers, embed, final_norm_w, lm_head).
+
+    The embedding is ~N(0, embed_std), by default N(0, 1) like the activations of the
+    single-layer workloads: token identity then dominates the residual stream, so the rows of a
+    verify pass route independently (about 45 of 64 experts per layer at 9 rows).  With a small
+    embedding (0.02) the random layers' attention output, common to all rows, dominates after
+    two layers and every row picks the same ~9 experts, which understates expert traffic."""
     import torch
 
     from . import synth
@@ -170,7 +177,7 @@ def random_model(cfg: MapleLikeConfig, seed: int = 0, device: str = "cuda"):
                    up_gate_w=ugw, up_gate_s=ugs, up_gate_b=ugb, down_w=dw, down_s=ds, down_b=db,
                    E=cfg.E, top_k=cfg.top_k, H=H, I=cfg.I, gs=cfg.gs, eps=cfg.eps)
         layers.append(dict(attn=attn, moe=moe))
-    embed = synth.torch_normal(gen, (cfg.vocab, H), 0.02, device)
+    embed = synth.torch_normal(gen, (cfg.vocab, H), embed_std, device)
     final_norm = (1.0 + 0.1 * torch.randn(H, generator=gen, device=device)).half()
     lm_head = synth.torch_normal(gen, (cfg.vocab, H), 0.02, device)
     return layers, embed, final_norm, lm_head
