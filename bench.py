@@ -33,6 +33,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 TREE16 = [-1, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 10, 11, 12, 13, 14]
 METRIC = "verify-step tokens/s (K=8, 1 GPU) + 2-bit gather-qmm HBM GB/s vs peak"
+UP_KERNEL = "void k_gather5<8, 64, 2, 8, 2>"  # the up||gate tile gather with the SwiGLU epilogue
 
 
 def log(*a):
@@ -239,6 +240,15 @@ def main():
     log(f"expert up {up_gbs:.0f} GB/s, down {dn_gbs:.0f} GB/s, head {hd_gbs:.0f} GB/s, "
         f"unique experts/layer {uniq.mean():.1f}")
 
+    # HBM bytes per launch of the same kernel, from the FETCH_SIZE / WRITE_SIZE collections
+    # summarised under profiles/ (counter runs cannot share a process with this timing)
+    traffic, tpath = None, os.path.join(ROOT, "profiles", "expert_up_gather_k8_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        if t.get("kernel") == UP_KERNEL and t.get("rows") == M:
+            traffic = t["traffic_bytes_per_launch"]
+
     cpu = None
     if not args.no_cpu:
         try:
@@ -269,12 +279,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "expert up||gate gather + SwiGLU (k_gather5<8,64,SWIGLU,8,2>)",
+            "kernel": "expert up||gate gather + SwiGLU (" + UP_KERNEL + ")",
             "achieved": round(up_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(up_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_launch": int(up_b.mean()),
             "ms_per_launch": round(up_ms / max(up_n, 1), 5),
             "timer_ms_per_launch": round(ev_each, 5),

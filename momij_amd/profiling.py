@@ -7,12 +7,17 @@ library's kernels of the passes with a given row count (9 = y plus an 8-token ch
 
     python -m momij_amd.profiling trace    <run_kernel_trace.csv>       --rows 9 [--last N]
     python -m momij_amd.profiling counters <run_counter_collection.csv> --rows 9 --scale F
+    python -m momij_amd.profiling traffic  <fetch.csv> <write.csv> --rows 9 --kernel NAME
+                                           --copy-mb 512 [--out FILE.json]
 
 `trace` prints, per kernel and grid size, launches per pass and the mean / median duration;
 `--last N` restricts it to the last N passes of that row count (the eager, event-timed passes
 bench.py runs after its graph-replayed steps).  `counters` prints the mean counter value per
 dispatch in MB, multiplied by `--scale` (the calibration factor of the counter: the ratio of a
-plain copy's known bytes to what the counter reports for it).
+plain copy's known bytes to what the counter reports for it).  `traffic` takes a FETCH_SIZE and
+a WRITE_SIZE collection of runs that end with one plain device copy of `--copy-mb` MiB
+(bench.py --copy-calib-mb), derives each counter's factor from that copy, and reports the HBM
+bytes per dispatch of the kernel whose name starts with NAME.
 """
 from __future__ import annotations
 
@@ -23,7 +28,8 @@ import statistics
 
 
 def _ours(name: str) -> bool:
-    return name.startswith("k_") or name.startswith("void k_")
+    # k_hold only delays a profiled pass (it runs before the pass's k_embed); not pass work
+    return (name.startswith("k_") or name.startswith("void k_")) and not name.startswith("k_hold")
 
 
 def _key(name: str, grid: int, wg: int) -> str:
@@ -92,18 +98,63 @@ def counter_summary(path: str, n_rows: int, scale: float) -> str:
     return "\n".join(out)
 
 
+def copy_scale(path: str, copy_bytes: int) -> float:
+    """Known bytes / counted bytes of the largest plain copy dispatch in a collection."""
+    rows = [r for r in csv.DictReader(open(path)) if "copyBuffer" in r["Kernel_Name"]]
+    if not rows:
+        raise SystemExit(f"{path}: no copy dispatch to calibrate against")
+    counted = max(float(r["Counter_Value"]) * 1024 for r in rows)
+    return copy_bytes / counted
+
+
+def kernel_bytes(path: str, n_rows: int, kernel: str, scale: float) -> tuple[float, int]:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    vals = [float(r["Counter_Value"]) * 1024 * scale
+            for n, ks in split_passes(rows, "Grid_Size", "Workgroup_Size") if n == n_rows
+            for r in ks if r["Kernel_Name"].startswith(kernel)]
+    if not vals:
+        raise SystemExit(f"{path}: no dispatch of {kernel!r} in passes of {n_rows} rows")
+    return statistics.mean(vals), len(vals)
+
+
+def traffic_summary(fetch_csv: str, write_csv: str, n_rows: int, kernel: str,
+                    copy_mb: int) -> dict:
+    copy_bytes = copy_mb << 20
+    fs, ws = copy_scale(fetch_csv, copy_bytes), copy_scale(write_csv, copy_bytes)
+    fb, nf = kernel_bytes(fetch_csv, n_rows, kernel, fs)
+    wb, nw = kernel_bytes(write_csv, n_rows, kernel, ws)
+    return {"kernel": kernel, "rows": n_rows, "fetch_bytes_per_launch": round(fb),
+            "write_bytes_per_launch": round(wb), "traffic_bytes_per_launch": round(fb + wb),
+            "fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
+            "dispatches": [nf, nw], "copy_bytes": copy_bytes}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("kind", choices=["trace", "counters"])
+    ap.add_argument("kind", choices=["trace", "counters", "traffic"])
     ap.add_argument("csv")
+    ap.add_argument("csv2", nargs="?")
+    ap.add_argument("--kernel", default="void k_gather5<8, 64, 2, 8, 2>")
+    ap.add_argument("--copy-mb", type=int, default=512)
+    ap.add_argument("--out", default=None)
     ap.add_argument("--rows", type=int, default=9)
     ap.add_argument("--last", type=int, default=None)
     ap.add_argument("--scale", type=float, default=1.0)
     a = ap.parse_args()
     if a.kind == "trace":
         print(trace_summary(a.csv, a.rows, a.last))
-    else:
+    elif a.kind == "counters":
         print(counter_summary(a.csv, a.rows, a.scale))
+    else:
+        import json
+
+        t = traffic_summary(a.csv, a.csv2, a.rows, a.kernel, a.copy_mb)
+        print(json.dumps(t, indent=1))
+        if a.out:
+            with open(a.out, "w") as f:
+                json.dump(t, f, indent=1)
+                f.write("\n")
 
 
 if __name__ == "__main__":
