@@ -247,15 +247,16 @@ float mj_model_last_pass_ms(const mj_model* model);
 /* Per-kernel timing for measurement: when enabled, verify passes run without graphs and record
  * HIP events around each launch of the classes below on the model stream (counters reset on
  * every call).  A profiled pass waits behind a 15 ms hold kernel, so its launches are queued
- * before the GPU reaches them, and starts with 8 event pairs around nothing: each bracketed
- * time is then the kernel's duration plus the timer's own cost, which MJ_KERNEL_EVENT_PAIR
- * measures.  mj_model_kernel_ms returns the summed milliseconds and the launch count. */
+ * before the GPU reaches them, and starts with 8 brackets around a kernel that waits 20 us of
+ * wall-clock time: each bracketed time is the kernel's duration plus the timer's own cost, and
+ * MJ_KERNEL_TIMER minus 20 us per launch is that cost.  mj_model_kernel_ms returns the summed
+ * milliseconds and the launch count. */
 #define MJ_KERNEL_EXPERT_UP 0   /* bucketed up||gate gather + SwiGLU */
 #define MJ_KERNEL_EXPERT_DOWN 1 /* bucketed down gather */
 #define MJ_KERNEL_LM_HEAD 2     /* fp16 lm_head + argmax partials */
 #define MJ_KERNEL_ATTENTION 3   /* split-K attention + combine */
 #define MJ_KERNEL_DENSE 4       /* qkv and o projections */
-#define MJ_KERNEL_EVENT_PAIR 5  /* event pairs with nothing between them (timer cost) */
+#define MJ_KERNEL_TIMER 5       /* the same bracket around a 20 us wall-clock hold */
 mj_status mj_model_profile(mj_model* model, int enable);
 float mj_model_kernel_ms(const mj_model* model, int kernel_class, int64_t* launches);
 

@@ -3,15 +3,14 @@
 // Semantics as k_qmv2 / k_gather (gqmm2_rows, SeedlessMetal.swift:2168-2221): per 64-input
 // block, y += s * (sum q*x) + b * (sum x), fp32.
 //
-// Layout of the work: one wave owns a tile of 16 weight rows over the whole K, so it issues
-// every load of its weights (codes, scales, biases) before its first wait and needs no
-// cross-wave reduction.  Lane (n = lane % 16, q = lane / 16) streams the contiguous quarter
-// q of row n: K/256 64-blocks = K/16 bytes of codes, one vector of scales and one of biases.
-// A block is WPB such waves over one expert (or the dense projection): it stages the rows
-// routed to the expert (qx order, <= 16 per pass) in LDS once for all its waves.
-// The MFMA A operand carries activation row m only on the A rows 4q+m of k-quarter q, so one
-// MFMA yields a separate sum per quarter (= per lane 64-block) and every 64-block keeps its
-// own scale and bias; the quarters are added after the K loop.
+// Layout of the work: a block serves one expert (or the dense projection) and a strip of
+// its output rows.  It stages the activation rows routed to that expert (qx order, up to 16
+// per pass, read from the expert's pair list) in LDS once for all its waves.  Each wave owns
+// a tile of 16 weight rows over one K-slice (KS slices per tile, summed through LDS at the
+// end).  It issues every load of its weight tile (scales, biases, then the codes in 1 KB
+// column groups, global -> LDS directly) before its first wait, and runs the MFMAs of a
+// column group as soon as that group has landed.  Blocks of experts that no row picked exit
+// at once, so only routed experts are read, each once per pass.
 //
 // Epilogues: STORE y = half(acc); ADD y = half(y + half(acc)) (o-proj residual,
 // gqmm2_rows_fold_add 3488-3543); SWIGLU clamped SwiGLU of the up || gate row pair

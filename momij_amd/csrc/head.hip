@@ -309,7 +309,7 @@ __global__ __launch_bounds__(64) void k_hold(unsigned ticks) {
 
 hipError_t launch_hold(unsigned us, hipStream_t st) {
     if (us > 100000) us = 100000;
-    hipLaunchKernelGGL(k_hold, dim3(1), dim3(64), 0, st, us * 100u);
+    launch_timed(k_hold, dim3(1), dim3(64), 0, st, us * 100u);
     return hipGetLastError();
 }
 

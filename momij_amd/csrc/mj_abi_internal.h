@@ -42,9 +42,10 @@ struct MoeScratch {
 // Optional per-kernel-class event timing of eager passes (classes of mj_model_kernel_ms).
 enum {
     PROF_UP = 0, PROF_DOWN = 1, PROF_HEAD = 2, PROF_ATTN = 3, PROF_DENSE = 4,
-    PROF_EMPTY = 5,  // event pairs around nothing: the cost of the timer itself
+    PROF_TIMER = 5,  // brackets around a hold of PROF_TIMER_US: bracket - hold = timer cost
     PROF_CLASSES = 6
 };
+constexpr unsigned PROF_TIMER_US = 20;
 struct Prof {
     hipEvent_t* pool = nullptr;
     int cap = 0, used = 0;

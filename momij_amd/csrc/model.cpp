@@ -270,12 +270,12 @@ static mj_status run_pass(mj_model* m, int kind, int M) {
     if (m->profiling && !capture_ok) {
         s = mj_hip(ctx, launch_hold(15000, st), "hold");
         if (s != MJ_OK) return s;
-        for (int j = 0; j < 8 && m->prof.used + 2 <= m->prof.cap; ++j) {
-            Prof& p = m->prof;
-            p.cls[p.used / 2] = PROF_EMPTY;
-            p.valid[p.used / 2] = hipEventRecord(p.pool[p.used], st) == hipSuccess &&
-                                  hipEventRecord(p.pool[p.used + 1], st) == hipSuccess;
-            p.used += 2;
+        // timer calibration: the same event bracket around holds of known length
+        for (int j = 0; j < 8; ++j) {
+            m->prof.begin(PROF_TIMER, st);
+            s = mj_hip(ctx, launch_hold(PROF_TIMER_US, st), "hold");
+            m->prof.end(st);
+            if (s != MJ_OK) return s;
         }
     }
     hipEventRecord(m->ev0, st);

@@ -94,7 +94,7 @@ class VerifyEngine:
     def last_pass_ms(self) -> float:
         return float(self.lib.mj_model_last_pass_ms(self.h))
 
-    KERNEL_CLASSES = ("expert_up", "expert_down", "lm_head", "attention", "dense", "event_pair")
+    KERNEL_CLASSES = ("expert_up", "expert_down", "lm_head", "attention", "dense", "timer")
 
     def profile(self, enable: bool):
         self.ctx.check(self.lib.mj_model_profile(self.h, int(enable)))
