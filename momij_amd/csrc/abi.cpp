@@ -273,12 +273,9 @@ mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void
     MoeScratch ms;
     mj_status s = moe_scratch(ctx, H, I, E, k, M, ms);
     if (s != MJ_OK) return s;
-    // the op-level scratch is shared with other entry points: expert counts start from zero
-    s = mj_hip(ctx, launch_zero_i32(ms.ecnt[0], E, ctx->stream), "count clear");
-    if (s != MJ_OK) return s;
     return run_moe(ctx, w, (const uint16_t*)x, (uint16_t*)y, M, flags, ms,
                    out_inds ? out_inds : ms.inds, out_scores ? out_scores : ms.scores,
-                   ctx->stream, 0, false);
+                   ctx->stream);
 }
 
 mj_status mj_selftest_mfma(mj_ctx* ctx, const void* A, const void* B, float* D) {
@@ -306,8 +303,7 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
         ms.act = (uint16_t*)a.take((size_t)M * k * I * 2);
         ms.act_sum = (float2*)a.take((size_t)M * k * (I / 64) * sizeof(float2));
         ms.down = (uint16_t*)a.take((size_t)M * k * H * 2);
-        ms.ecnt[0] = (int*)a.take((size_t)E * 4);
-        ms.ecnt[1] = (int*)a.take((size_t)E * 4);
+        ms.ecnt = (int*)a.take((size_t)E * 4);
         ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
     };
     layout(ar);
@@ -320,12 +316,16 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
 
 mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
                   int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st,
-                  int slot, bool clear_other, Prof* prof) {
+                  Prof* prof, const NormOut* next) {
     const int H = w->H, I = w->I, E = w->E, k = w->top_k;
     const int* ab = ctx->abort_dev;
     const uint16_t* xn = x;
     mj_status s;
     const bool fused = route_supported(H, E, k);
+    const bool up_tile = gather3_supported(EPI_SWIGLU, H, 2 * I, w->gs);
+    const bool dn_tile = gather3_supported(EPI_STORE, I, H, w->gs);
+    // tile path: the top-k launch also lists each expert's (row, slot) pairs for the gathers
+    const bool tile = fused && M > 1 && M <= MJ_MAX_ROWS && up_tile && dn_tile;
     if (fused) {
         RouteArgs ra{};
         ra.x = x;
@@ -336,15 +336,17 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.xsum = M > 1 ? ms.xsum : nullptr;
         ra.inds = inds;
         ra.scores = scores;
-        ra.ecnt = ms.ecnt[slot];
-        ra.eplist = ms.eplist;
-        ra.ecnt_clear = clear_other ? ms.ecnt[slot ^ 1] : nullptr;
+        ra.logits = ms.logits;
+        ra.ecnt = tile ? ms.ecnt : nullptr;
+        ra.eplist = tile ? ms.eplist : nullptr;
         ra.M = M;
         ra.E = E;
         ra.k = k;
         ra.eps = w->eps;
         ra.abort = ab;
-        s = mj_hip(ctx, launch_route(ra, H, st), "route");
+        s = mj_hip(ctx, launch_route_logits(ra, H, st), "route");
+        if (s != MJ_OK) return s;
+        s = mj_hip(ctx, launch_route_topk(ra, st), "route top-k");
         if (s != MJ_OK) return s;
         if (M == 1 && (flags & MJ_MOE_PRENORM)) xn = ms.xn;
     }
@@ -406,27 +408,23 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
             s = mj_hip(ctx, launch_topk_bucket(ms.logits, M, E, k, inds, scores, ms.bk, ab, st),
                        "topk");
             if (s != MJ_OK) return s;
-        }
-        // the tile kernels find each expert's rows themselves; the fallback kernels take the
-        // buckets (built here unless the unfused router already did)
-        const bool up_tile = gather3_supported(EPI_SWIGLU, H, 2 * I, w->gs);
-        const bool dn_tile = gather3_supported(EPI_STORE, I, H, w->gs);
-        const int nb = M * k < E ? M * k : E;
-        // expert lists come from the fused route; the unfused one leaves buckets instead
-        const bool lists = fused;
-        if (lists && (!up_tile || !dn_tile)) {
+        } else if (!tile) {
             s = mj_hip(ctx, launch_bucket_inds(inds, M * k, ms.bk, ab, st), "bucket");
             if (s != MJ_OK) return s;
         }
+        const int nb = M * k < E ? M * k : E;
         GatherArgs up{};
         up.xperm = ms.xperm;
         up.xsum = ms.xsum;
         up.w = w->up_gate_w;
         up.s = (const uint16_t*)w->up_gate_s;
         up.b = (const uint16_t*)w->up_gate_b;
-        up.ecnt = up_tile && lists ? ms.ecnt[slot] : nullptr;
-        up.eplist = ms.eplist;
-        up.bk = up.ecnt ? nullptr : ms.bk;
+        if (tile) {
+            up.ecnt = ms.ecnt;
+            up.eplist = ms.eplist;
+        } else {
+            up.bk = ms.bk;
+        }
         up.y = ms.act;
         up.ysum = ms.act_sum;
         up.K = H;
@@ -435,7 +433,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         up.x_div = k;
         up.abort = ab;
         if (prof) prof->begin(PROF_UP, st);
-        s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, up.ecnt ? E : nb, st), "up gather");
+        s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, tile ? E : nb, st), "up gather");
         if (prof) prof->end(st);
         if (s != MJ_OK) return s;
         // the tile kernel's SwiGLU epilogue writes act without block sums: the tile down
@@ -444,27 +442,28 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
             s = mj_hip(ctx, launch_qx_sums(ms.act, ms.act_sum, M * k, I, ab, st), "act sums");
             if (s != MJ_OK) return s;
         }
-        GatherArgs dn{};
+        GatherArgs dn = up;
         dn.xperm = ms.act;
         dn.xsum = dn_tile ? nullptr : ms.act_sum;
         dn.w = w->down_w;
         dn.s = (const uint16_t*)w->down_s;
         dn.b = (const uint16_t*)w->down_b;
-        dn.ecnt = dn_tile && lists ? ms.ecnt[slot] : nullptr;
-        dn.eplist = ms.eplist;
-        dn.bk = dn.ecnt ? nullptr : ms.bk;
         dn.y = ms.down;
+        dn.ysum = nullptr;
         dn.K = I;
         dn.N = H;
-        dn.gs = w->gs;
         dn.x_div = 1;
-        dn.abort = ab;
         if (prof) prof->begin(PROF_DOWN, st);
-        s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, dn.ecnt ? E : nb, st), "down gather");
+        s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, tile ? E : nb, st), "down gather");
         if (prof) prof->end(st);
         if (s != MJ_OK) return s;
     }
-    return mj_hip(ctx, launch_score_combine(ms.down, scores,
-                                            (flags & MJ_MOE_RESIDUAL) ? x : nullptr, y, M, k, H,
-                                            ab, st), "combine");
+    const uint16_t* resid = (flags & MJ_MOE_RESIDUAL) ? x : nullptr;
+    if (next && H == 2048)
+        return mj_hip(ctx, launch_combine_norm(ms.down, scores, resid, y, M, k, H, *next, ab, st),
+                      "combine + norm");
+    s = mj_hip(ctx, launch_score_combine(ms.down, scores, resid, y, M, k, H, ab, st), "combine");
+    if (s != MJ_OK || !next) return s;
+    return mj_hip(ctx, launch_rmsnorm_qx(y, next->w, next->eps, next->plain, next->xperm,
+                                         next->xsum, M, H, ab, st), "next norm");
 }

@@ -27,8 +27,9 @@ __device__ __forceinline__ void load_lds16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
 }
 
-// Launch shape: R = 16 activation rows per pass (the MFMA M dimension), RA <= R rows staged in
-// LDS (the rows a bucket can hold), K = 256 * KPL.  A block has WPB waves = TPB tiles of 16
+// Launch shape: R = 16 activation rows at most per pass (the MFMA M dimension), RA <= R rows
+// staged in LDS per pass (a bucket with more rows takes several passes; `multi` says whether
+// any can), K = 256 * KPL.  A block has WPB waves = TPB tiles of 16
 // weight rows x KS K-slices: wave w owns tile w % TPB and K-slice w / TPB.
 template <int KPL, int GS, int EPI, int WPB, int KS>
 struct G5Shape {
@@ -46,12 +47,12 @@ struct G5Shape {
     static constexpr int WAVE_BYTES = WCODE + 2 * WSB;
     static constexpr int SS = KB + 2;          // LDS row stride of block sums (float2)
     static_assert(WAVE_BYTES >= 64 * 16, "a K-slice partial fits in its wave's tile area");
-    // K-slice partials: in a wave's own tile area when a bucket is one pass (RA < R), else in
-    // their own region (later passes reuse the tiles)
+    // K-slice partials: in a wave's own tile area when every bucket is one pass, else in their
+    // own region (later passes reuse the tiles)
     static constexpr int RED = (KS - 1) * TPB * 64 * 16;
-    __host__ __device__ static size_t lds(int RA) {
+    __host__ __device__ static size_t lds(int RA, bool multi) {
         return (size_t)WPB * WAVE_BYTES + (size_t)RA * XS * 2 + (size_t)RA * SS * 8 +
-               (EPI == EPI_QKV ? (size_t)R * ES * 4 : 0) + (RA == R ? RED : 0);
+               (EPI == EPI_QKV ? (size_t)R * ES * 4 : 0) + (multi ? RED : 0);
     }
 };
 
@@ -97,7 +98,7 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <int KPL, int GS, int EPI, int WPB, int KS>
-__global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
+__global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int multi) {
     using S = G5Shape<KPL, GS, EPI, WPB, KS>;
     constexpr int R = S::R, K = S::K, KB = S::KB, KBW = S::KBW, TPB = S::TPB, XS = S::XS;
     constexpr int ES = S::ES, SCW = S::SCW;
@@ -113,16 +114,19 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
     const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
     const bool own_sums = a.xsum == nullptr;  // block sums formed here from the staged rows
 
-    // Expert mode: block u serves expert u (an expert nobody picked ends here).  Bucket mode:
-    // block u serves the u-th expert of a Buckets table.  Dense: rows 0 .. dense_rows-1.
+    // Expert mode: block u serves expert u, whose ecnt[u] (row, slot) pairs are listed at
+    // eplist[u * MJ_ROWS ..]; count and list are loaded together (lane j: pair j), and an
+    // expert nobody picked ends here.  Bucket mode: block u serves the u-th expert of a Buckets
+    // table.  Dense: rows 0 .. dense_rows-1.
     const int* plist = nullptr;
+    int lpair = 0;  // expert mode: pair j of the list in lane j
     int e = 0, np = a.dense_rows;
     {
         const int ab = a.abort ? *a.abort : 0;
         if (a.ecnt != nullptr) {
             e = u;
             np = a.ecnt[u];
-            plist = a.eplist + u * MJ_ROWS;
+            lpair = a.eplist[u * MJ_ROWS + lane];
         } else if (a.bk != nullptr) {
             const Buckets* bk = a.bk;
             const int cnt = bk->count, ee = bk->expert[u], s0 = bk->start[u], s1 = bk->start[u + 1];
@@ -142,14 +146,14 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
     uint16_t* xs = (uint16_t*)(g5lds + (size_t)WPB * S::WAVE_BYTES);  // [RA][XS] qx rows
     float2* xsl = (float2*)(xs + RA * XS);                 // [RA][SS] {sum x, sum base*x}
     float* el = (float*)(xsl + RA * S::SS);                // [R][ES] QKV epilogue staging
-    char* red = (char*)el + (EPI == EPI_QKV ? R * ES * 4 : 0);  // [KS-1][TPB][64] f4 (RA == R)
+    char* red = (char*)el + (EPI == EPI_QKV ? R * ES * 4 : 0);  // [KS-1][TPB][64] f4 (multi)
     __shared__ int s_pair[R];
 
     // ---- activation rows of a pass, straight into LDS: rows < npass only (the rest feed
     // MFMA output rows that are discarded).  Wave w stages rows w, w + WPB, ...
     auto stage_load = [&](int pb, int npass) {
         const int myr = min(pb + (lane < R ? lane : 0), np - 1);
-        const int prl = plist ? plist[myr] : myr;
+        const int prl = a.ecnt ? __shfl(lpair, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
 #pragma unroll
         for (int j = 0; j < R / WPB; ++j) {
             const int r = wv + WPB * j;
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
         }
     };
 
-    const int npass0 = min(R, np);
+    const int npass0 = min(RA, np);
     stage_load(0, npass0);  // in flight ahead of the weight stream (loads return in issue order)
 
     // ---- this wave's weight tile, coalesced into LDS
@@ -304,8 +308,8 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
             // K-slices of a tile meet in LDS (a slice's partial goes into its own wave's tile
             // area, free once its MFMAs are done); slice 0 adds them in slice order
             auto slot = [&](int k2) -> f4* {
-                return (f4*)(RA == R ? red + ((k2 - 1) * TPB + tt) * 1024
-                                     : g5lds + (size_t)(k2 * TPB + tt) * S::WAVE_BYTES) + lane;
+                return (f4*)(multi ? red + ((k2 - 1) * TPB + tt) * 1024
+                                   : g5lds + (size_t)(k2 * TPB + tt) * S::WAVE_BYTES) + lane;
             };
             if (kh > 0) *slot(kh) = (f4){acc[0], acc[1], acc[2], acc[3]};
             lds_barrier<0>();
@@ -401,9 +405,9 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA) {
     };
 
     run_pass(0, npass0);
-    for (int pb = R; pb < np; pb += R) {
+    for (int pb = RA; pb < np; pb += RA) {
         __syncthreads();  // the previous pass is done with LDS
-        const int npass = min(R, np - pb);
+        const int npass = min(RA, np - pb);
         stage_load(pb, npass);
         run_pass(pb, npass);
     }
@@ -413,10 +417,15 @@ template <int KPL, int GS, int EPI, int WPB, int KS>
 static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStream_t st) {
     using S = G5Shape<KPL, GS, EPI, WPB, KS>;
     const int ncb = a.N / (16 * S::TPB);
-    const int RA = rows < S::R ? (rows < 1 ? 1 : rows) : S::R;
-    const size_t lds = S::lds(RA);
-    launch_timed(k_gather5<KPL, GS, EPI, WPB, KS>, dim3(n_buckets * ncb), dim3(WPB * 64), lds, st,
-                 a, RA);
+    // staged rows per pass: for the expert products as many as keep two blocks per CU (more
+    // rows on one expert are rare and take extra passes); dense projections take up to 16
+    const int want = rows < 1 ? 1 : rows;
+    int RA = want < S::R ? want : S::R;
+    if ((EPI == EPI_SWIGLU || EPI == EPI_STORE) && a.ecnt)
+        while (RA > 1 && S::lds(RA, want > RA) + 256 > 80 * 1024) --RA;
+    const bool multi = want > RA;
+    launch_timed(k_gather5<KPL, GS, EPI, WPB, KS>, dim3(n_buckets * ncb), dim3(WPB * 64),
+                 S::lds(RA, multi), st, a, RA, (int)multi);
     return hipGetLastError();
 }
 
@@ -445,7 +454,7 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
         case EPI_QKV: MJ_G5(8, EPI_QKV, 8, 1, 1)
         case EPI_ADD: MJ_G5(8, EPI_ADD, 8, 2, 2)
         case EPI_STORE:
-            if (a.K == 1024) { MJ_G5(4, EPI_STORE, 8, 2, 1) }
+            if (a.K == 1024) { MJ_G5(4, EPI_STORE, 8, 1, 1) }
             MJ_G5(8, EPI_STORE, 8, 2, 2)
     }
 #undef MJ_G5
@@ -456,7 +465,7 @@ template <int KPL, int GS, int EPI, int WPB, int KS>
 static hipError_t g5_attr() {
     return hipFuncSetAttribute((const void*)k_gather5<KPL, GS, EPI, WPB, KS>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)G5Shape<KPL, GS, EPI, WPB, KS>::lds(16));
+                               (int)G5Shape<KPL, GS, EPI, WPB, KS>::lds(16, true));
 }
 
 hipError_t set_gather3_attributes() {
@@ -465,7 +474,7 @@ hipError_t set_gather3_attributes() {
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, W, KS64>();    \
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, W, KS128>();
     MJ_A(8, EPI_SWIGLU, 8, 2, 2) MJ_A(8, EPI_QKV, 8, 1, 1) MJ_A(8, EPI_ADD, 8, 2, 2)
-    MJ_A(4, EPI_STORE, 8, 2, 1) MJ_A(8, EPI_STORE, 8, 2, 2)
+    MJ_A(4, EPI_STORE, 8, 1, 1) MJ_A(8, EPI_STORE, 8, 2, 2)
 #undef MJ_A
     return e;
 }

@@ -297,6 +297,24 @@ hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H,
     return hipGetLastError();
 }
 
+// Token embedding of a 2048-wide row followed by the first layer's input RMSNorm.
+__global__ __launch_bounds__(256) void k_embed_norm(const uint16_t* table, const StepDesc* sd,
+                                                    uint16_t* h, NormOut no, const int* abort) {
+    if (aborted(abort)) return;
+    const int r = blockIdx.x, t = threadIdx.x;
+    const int tok = sd->tokens[r];
+    const u4v v = *(const u4v*)(table + (size_t)tok * 2048 + 8 * t);
+    *(u4v*)(h + (size_t)r * 2048 + 8 * t) = v;
+    norm_row_2048(v, no, r);
+}
+
+hipError_t launch_embed_norm(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
+                             const NormOut& no, const int* abort, hipStream_t st) {
+    if (H != 2048) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed_norm, dim3(M), dim3(256), 0, st, table, sd, h, no, abort);
+    return hipGetLastError();
+}
+
 // The wall clock (s_memrealtime) ticks at 100 MHz; the loop also stops after a fixed number
 // of sleeps, so it ends even if the clock were not to advance.
 __global__ __launch_bounds__(64) void k_hold(unsigned ticks) {

@@ -35,7 +35,7 @@ struct MoeScratch {
     uint16_t* act;       // [M*k][I] (qx for M > 1, plain for M == 1)
     float2* act_sum;     // [M*k][I/64]
     uint16_t* down;      // [M*k][H]
-    int* ecnt[2];        // pairs per expert [E], two buffers used by alternate layers
+    int* ecnt;           // pairs per expert [E]
     int* eplist;         // pair lists per expert [E][MJ_ROWS]
 };
 
@@ -71,8 +71,7 @@ mj_status mj_hip(mj_ctx* ctx, hipError_t e, const char* what);
 mj_status mj_scratch_reserve(mj_ctx* ctx, size_t bytes);
 mj_status mj_check_abort(mj_ctx* ctx);
 mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms);
-// slot: which expert-count buffer the route fills (the other one is cleared for the next
-// launch when clear_other is set; otherwise the caller zeroes the slot beforehand)
+// next: also normalise the block's output y into these outputs (the following RMSNorm).
 mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
                   int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st,
-                  int slot, bool clear_other, Prof* prof = nullptr);
+                  Prof* prof = nullptr, const NormOut* next = nullptr);

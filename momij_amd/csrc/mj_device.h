@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mj_internal.h"
+
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -211,3 +213,34 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
 }
 
 __device__ __forceinline__ float u01(uint32_t x) { return (float)(x >> 8) * 0x1p-24f; }
+
+// RMSNorm of one 2048-element row held by a 256-thread block (thread t: elements 8t .. 8t+7,
+// packed fp16 in hv), as k_rmsnorm_qx: out = half(x * (1 / sqrt(mean x^2 + eps)) * w), written
+// plain and / or in qx order with its block sums (NormOut).  Every thread of the block must
+// call it.
+__device__ __forceinline__ void norm_row_2048(const u4v hv, const NormOut& no, int row) {
+    const int t = threadIdx.x, lane = t & 63;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float a = h2f(hv[j] & 0xFFFFu), b = h2f(hv[j] >> 16);
+        ss += a * a;
+        ss += b * b;
+    }
+    ss = wave_sum(ss);
+    __shared__ float red[4];
+    if (lane == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / sqrtf(tot / 2048.0f + no.eps);
+    const u4v wv = *(const u4v*)(no.w + 8 * t);
+    u4v o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float a = h2f(hv[j] & 0xFFFFu) * inv * h2f(wv[j] & 0xFFFFu);
+        const float b = h2f(hv[j] >> 16) * inv * h2f(wv[j] >> 16);
+        o[j] = (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
+    }
+    if (no.plain) *(u4v*)(no.plain + (size_t)row * 2048 + 8 * t) = o;
+    if (no.xperm) emit_qx(o, lane, no.xperm + (size_t)row * 2048, no.xsum + (size_t)row * 32, 8 * t);
+}

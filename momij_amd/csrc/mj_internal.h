@@ -41,6 +41,16 @@ struct Buckets {
 
 enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
+// Outputs of a fused RMSNorm over 2048-element rows: out = half(x * rsqrt(mean x^2 + eps) * w)
+// written plain and / or in qx order with its per-64 block sums.
+struct NormOut {
+    const uint16_t* w;   // [2048]
+    float eps;
+    uint16_t* plain;     // [rows][2048] (nullable)
+    uint16_t* xperm;     // [rows][2048] qx (nullable)
+    float2* xsum;        // [rows][32]
+};
+
 #define MJ_ROWS 64  // == MJ_MAX_ROWS of the C ABI
 
 // Per-pass parameters read by the kernels from device memory, so one captured graph serves
@@ -87,8 +97,8 @@ struct QkvEpi {
 };
 
 // Row sets of a gather launch (grid = groups x column blocks):
-//   ecnt != nullptr (tile kernel): group u = expert u with ecnt[u] pairs listed, in no particular
-//   order, at eplist[u * MJ_ROWS ..] (an expert takes each row at most once);
+//   ecnt != nullptr (tile kernel): group u = expert u with ecnt[u] pairs listed, in no
+//   particular order, at eplist[u * MJ_ROWS ..] (pair = row * top_k + slot);
 //   bk != nullptr: group u = bucket u of the table;  neither: dense, one group of dense_rows.
 struct GatherArgs {
     const uint16_t* xperm;  // qx activations [rows_x][K]
@@ -172,6 +182,8 @@ hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, in
                             hipStream_t st);
 hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
                         const int* abort, hipStream_t st);
+hipError_t launch_embed_norm(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
+                             const NormOut& no, const int* abort, hipStream_t st);  // H = 2048
 // One wave that waits `us` microseconds of wall-clock time (bounded), so that the host can
 // queue the launches that follow it before the GPU reaches them.
 hipError_t launch_hold(unsigned us, hipStream_t st);
@@ -206,16 +218,23 @@ struct RouteArgs {
     float2* xsum;            // [M][H/64]
     int32_t* inds;           // [M][k]
     float* scores;           // [M][k]
-    int* ecnt;               // pairs per expert [E] (zero on entry; counted here)
-    int* eplist;             // pair lists [E][MJ_ROWS]
-    int* ecnt_clear;         // counts of the next route launch, zeroed here (nullable)
+    float* logits;           // [M][E] router logits
+    int* ecnt;               // pairs per expert [E] (route lists)
+    int* eplist;             // pair lists [E][MJ_ROWS] (route lists)
     int M, E, k;
     float eps;
     const int* abort;
 };
 bool route_supported(int H, int E, int k);
-hipError_t launch_zero_i32(int* p, int n, hipStream_t st);  // fill kernel (graph-safe)
-hipError_t launch_route(const RouteArgs& a, int H, hipStream_t st);
+hipError_t launch_route_logits(const RouteArgs& a, int H, hipStream_t st);
+// inds and scores of every row from the logits, and (when a.ecnt is set, M <= MJ_ROWS) the
+// per-expert pair lists ecnt / eplist
+hipError_t launch_route_topk(const RouteArgs& a, hipStream_t st);
+// y = [x_resid +] combine of the k expert rows (as launch_score_combine), then the norm of y
+// into `no`; H must be 2048.
+hipError_t launch_combine_norm(const uint16_t* down, const float* scores, const uint16_t* x_resid,
+                               uint16_t* y, int M, int k, int H, const NormOut& no,
+                               const int* abort, hipStream_t st);
 hipError_t launch_score_combine(const uint16_t* down, const float* scores, const uint16_t* x_resid,
                                 uint16_t* y, int M, int k, int H, const int* abort,
                                 hipStream_t st);

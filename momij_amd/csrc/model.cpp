@@ -79,7 +79,10 @@ static mj_status fill_tree(mj_ctx* ctx, StepDesc* sd, const int32_t* parents, in
 
 hipError_t set_kernel_attributes();
 
-static mj_status enqueue_layer(mj_model* m, int l, int M, hipStream_t st) {
+// Layer l of a pass.  Its input norm (attention RMSNorm into xperm / xsum) was written by
+// whatever produced h: the embedding for layer 0, the previous layer's expert combine
+// otherwise; its own expert combine writes the next one (or the final norm into xf).
+static mj_status enqueue_layer(mj_model* m, int l, int M, int kind, hipStream_t st) {
     mj_ctx* ctx = m->ctx;
     const mj_model_config& c = m->cfg;
     const mj_layer_weights& w = m->layers[l];
@@ -87,9 +90,6 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, hipStream_t st) {
     const int qkvN = (nQ + 2 * nKV) * D;
     const int* ab = ctx->abort_dev;
     mj_status s;
-    s = mj_hip(ctx, launch_rmsnorm_qx(m->h, (const uint16_t*)w.attn.norm_w, c.eps, nullptr,
-                                      m->xperm, m->xsum, M, H, ab, st), "attn norm");
-    if (s != MJ_OK) return s;
     GatherArgs q{};
     q.xperm = m->xperm;
     q.xsum = m->xsum;
@@ -176,9 +176,15 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, hipStream_t st) {
     if (s != MJ_OK) return s;
     int32_t* inds = m->inds_all + (size_t)l * MJ_MAX_ROWS * c.top_k;
     float* scores = m->scores_all + (size_t)l * MJ_MAX_ROWS * c.top_k;
-    // alternate layers use alternate expert-count buffers; each route clears the other one
+    NormOut next{};
+    const bool last = l + 1 == c.n_layers;
+    if (!last)
+        next = NormOut{(const uint16_t*)m->layers[l + 1].attn.norm_w, c.eps, nullptr, m->xperm,
+                       m->xsum};
+    else
+        next = NormOut{m->final_norm, c.eps, m->xf, nullptr, nullptr};
     return run_moe(ctx, &w.moe, m->h, m->h, M, MJ_MOE_PRENORM | MJ_MOE_RESIDUAL, m->ms, inds,
-                   scores, st, l & 1, true, pf);
+                   scores, st, pf, (last && kind == PASS_PREFILL) ? nullptr : &next);
 }
 
 static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
@@ -186,7 +192,18 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
     const mj_model_config& c = m->cfg;
     const int H = c.H;
     const int* ab = ctx->abort_dev;
-    mj_status s = mj_hip(ctx, launch_embed(m->embed, m->sd_dev, M, H, m->h, ab, st), "embed");
+    mj_status s;
+    const NormOut first{(const uint16_t*)m->layers[0].attn.norm_w, c.eps, nullptr, m->xperm,
+                        m->xsum};
+    if (H == 2048) {
+        s = mj_hip(ctx, launch_embed_norm(m->embed, m->sd_dev, M, H, m->h, first, ab, st),
+                   "embed + norm");
+    } else {
+        s = mj_hip(ctx, launch_embed(m->embed, m->sd_dev, M, H, m->h, ab, st), "embed");
+        if (s == MJ_OK)
+            s = mj_hip(ctx, launch_rmsnorm_qx(m->h, first.w, c.eps, nullptr, m->xperm, m->xsum, M,
+                                              H, ab, st), "attn norm");
+    }
     if (s != MJ_OK) return s;
     if (m->cap_h) {
         s = mj_hip(ctx, hipMemcpyAsync(m->cap_h, m->h, (size_t)M * H * 2, hipMemcpyDeviceToDevice,
@@ -194,7 +211,7 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
         if (s != MJ_OK) return s;
     }
     for (int l = 0; l < c.n_layers; ++l) {
-        s = enqueue_layer(m, l, M, st);
+        s = enqueue_layer(m, l, M, kind, st);
         if (s != MJ_OK) return s;
         if (m->cap_h) {
             s = mj_hip(ctx, hipMemcpyAsync((uint16_t*)m->cap_h + (size_t)(l + 1) * MJ_MAX_ROWS * H,
@@ -210,16 +227,8 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
             if (s != MJ_OK) return s;
         }
     }
-    // layer l fills expert-count buffer l & 1 and clears the other: with an odd layer count
-    // the last layer used buffer 0, which the next pass starts from
-    if (c.n_layers & 1) {
-        s = mj_hip(ctx, launch_zero_i32(m->ms.ecnt[0], c.E, st), "count clear");
-        if (s != MJ_OK) return s;
-    }
     if (kind != PASS_PREFILL) {
-        s = mj_hip(ctx, launch_rmsnorm_qx(m->h, m->final_norm, c.eps, m->xf, nullptr, nullptr, M,
-                                          H, ab, st), "final norm");
-        if (s != MJ_OK) return s;
+        // the last layer's expert combine wrote the final norm into xf
         float* logits = (kind == PASS_SAMPLED || m->cap_logits) ? m->logits : nullptr;
         if (m->profiling) m->prof.begin(PROF_HEAD, st);
         s = mj_hip(ctx, launch_lm_head(m->xf, m->lm_head, M, H, c.vocab, nullptr, 0, logits,
@@ -398,8 +407,7 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         ms.act = (uint16_t*)a.take((size_t)R * c.top_k * c.I * 2);
         ms.act_sum = (float2*)a.take((size_t)R * c.top_k * (c.I / 64) * 8);
         ms.down = (uint16_t*)a.take((size_t)R * c.top_k * H * 2);
-        ms.ecnt[0] = (int*)a.take((size_t)c.E * 4);
-        ms.ecnt[1] = (int*)a.take((size_t)c.E * 4);
+        ms.ecnt = (int*)a.take((size_t)c.E * 4);
         ms.eplist = (int*)a.take((size_t)c.E * MJ_MAX_ROWS * 4);
     };
     Arena count;

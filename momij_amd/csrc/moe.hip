@@ -249,54 +249,94 @@ hipError_t launch_score_combine(const uint16_t* down, const float* scores, const
     return hipGetLastError();
 }
 
+// The expert combine of one row followed by the next RMSNorm (of the next layer's attention,
+// or the final norm), H = 2048: one 256-thread block per row, thread t owns elements
+// 8t .. 8t+7.  The combine is k_score_combine's arithmetic, the norm k_rmsnorm_qx's.
+__global__ __launch_bounds__(256) void k_combine_norm(const uint16_t* __restrict__ down,
+                                                      const float* __restrict__ scores,
+                                                      const uint16_t* x_resid, uint16_t* y, int k,
+                                                      NormOut no, const int* abort) {
+    if (aborted(abort)) return;
+    const int r = blockIdx.x, t = threadIdx.x;
+    constexpr int H = 2048;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        const float sc = scores[r * k + j];
+        const u4v d = *(const u4v*)(down + ((size_t)r * k + j) * H + 8 * t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc[2 * q] += h2f(d[q] & 0xFFFFu) * sc;
+            acc[2 * q + 1] += h2f(d[q] >> 16) * sc;
+        }
+    }
+    u4v hv;
+    if (x_resid) {
+        const u4v xr = *(const u4v*)(x_resid + (size_t)r * H + 8 * t);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            hv[q] = (uint32_t)f2h(h2f(xr[q] & 0xFFFFu) + hround(acc[2 * q])) |
+                    ((uint32_t)f2h(h2f(xr[q] >> 16) + hround(acc[2 * q + 1])) << 16);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            hv[q] = (uint32_t)f2h(acc[2 * q]) | ((uint32_t)f2h(acc[2 * q + 1]) << 16);
+    }
+    *(u4v*)(y + (size_t)r * H + 8 * t) = hv;
+    norm_row_2048(hv, no, r);
+}
+
+hipError_t launch_combine_norm(const uint16_t* down, const float* scores, const uint16_t* x_resid,
+                               uint16_t* y, int M, int k, int H, const NormOut& no,
+                               const int* abort, hipStream_t st) {
+    if (H != 2048) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_combine_norm, dim3(M), dim3(256), 0, st, down, scores, x_resid, y, k, no,
+                       abort);
+    return hipGetLastError();
+}
+
 #define RT_H 2048
 
 // ---------------------------------------------------------------------------------------
-// MoE front, one 512-thread block per pass row: RMSNorm of the row (written plain and in qx
-// order with its block sums), its E router logits and its top-k, with no dependency between
-// blocks.  Every block reads the whole router (E x 2048 fp16, L2-resident after the first
-// rows) -- the price of needing no grid-wide synchronisation.
+// MoE front, two launches:
+//   k_route_logits  one 256-thread block per (row, group of RS_EPB experts), M * E / RS_EPB
+//                   blocks: RMSNorm of the row (the group-0 block writes it out, plain and in
+//                   qx order with its block sums) and the logits of the group's experts.  The
+//                   router matrix is read in 32 KB pieces by many CUs (a single CU streams only
+//                   a few tens of GB/s).
+//   k_route_topk    one wave per row: top-k of the row's logits, renormalised scores, and the
+//                   row's (row, slot) pairs appended to the experts' lists.
+// The kernel boundary orders the two: a grid-wide handoff inside one kernel needs a device-
+// scope release (an L2 write-back on this chip), which costs more than the launch.
 // Arithmetic as maple_rms_norm / maple_batched_gemv / maple_route_top8: fp32 sums (the logit
 // sums in v_dot2 lane partials and a fixed shuffle tree), softmax with max subtraction, top-k
 // by logit with the lowest index winning ties, weights renormalised over the k in rank order.
 // The top-k ranks every expert against all E logits (broadcast LDS reads), so the selection
 // comes out sorted without a chain of cross-lane reductions.
 // ---------------------------------------------------------------------------------------
-#define RR_EPW 8  // router rows per wave per round (8 waves -> 64 experts a round)
+#define RS_EPB 8  // router rows (experts) per block: two per wave
 
-__global__ __launch_bounds__(512) void k_route_row(RouteArgs a) {
+__global__ __launch_bounds__(256) void k_route_logits(RouteArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int r = blockIdx.x, E = a.E, k = a.k;
-    // the other count buffer is cleared for the next launch even when this one is aborted (the
-    // launch that used it has completed: stream order)
-    if (blockIdx.x == 0 && a.ecnt_clear)
-        for (int e = tid; e < E; e += 512) a.ecnt_clear[e] = 0;
+    const int E = a.E, S = E / RS_EPB;
+    const int r = blockIdx.x / S, grp = blockIdx.x - r * S;
     __shared__ __align__(16) uint16_t xn[RT_H];
     __shared__ float s_ss[4];
-    __shared__ __align__(16) float s_lg[MJ_MAX_EXPERTS];
-    __shared__ float s_gate[8];
-    if (aborted(a.abort)) return;  // whole grid: the abort word is fixed during a launch
+    if (aborted(a.abort)) return;
 
-    // row r: threads 0..255 hold 8 consecutive elements each
-    u4v xv = {0u, 0u, 0u, 0u}, nw = {0u, 0u, 0u, 0u};
-    if (tid < 256) {
-        xv = *(const u4v*)(a.x + (size_t)r * RT_H + 8 * tid);
-        if (a.norm_w) nw = *(const u4v*)(a.norm_w + 8 * tid);
-    }
-    // the first round of router rows: expert wv + 8 j, k = 512 c + 8 lane .. +7
-    u4v wr[RR_EPW][4];
-    auto load_round = [&](int e0) {
+    // router rows of this wave first (k = 512 c + 8 lane .. +7), then the row
+    const int e0 = grp * RS_EPB + 2 * wv;
+    u4v wr[2][4];
 #pragma unroll
-        for (int j = 0; j < RR_EPW; ++j) {
-            const int e = min(e0 + wv + 8 * j, E - 1);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                wr[j][c] = *(const u4v*)(a.W + (size_t)e * RT_H + 512 * c + 8 * lane);
-        }
-    };
-    load_round(0);
+        for (int c = 0; c < 4; ++c)
+            wr[j][c] = *(const u4v*)(a.W + (size_t)(e0 + j) * RT_H + 512 * c + 8 * lane);
+    u4v xv = *(const u4v*)(a.x + (size_t)r * RT_H + 8 * tid);
+    u4v nw = {0u, 0u, 0u, 0u};
+    if (a.norm_w) nw = *(const u4v*)(a.norm_w + 8 * tid);
 
-    // RMSNorm
     if (a.norm_w) {
         float ss = 0.0f;
 #pragma unroll
@@ -306,7 +346,7 @@ __global__ __launch_bounds__(512) void k_route_row(RouteArgs a) {
             ss += x1 * x1;
         }
         ss = wave_sum(ss);
-        if (lane == 0 && wv < 4) s_ss[wv] = ss;
+        if (lane == 0) s_ss[wv] = ss;
         __syncthreads();
         const float tot = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
         const float inv = 1.0f / sqrtf(tot / (float)RT_H + a.eps);
@@ -317,45 +357,64 @@ __global__ __launch_bounds__(512) void k_route_row(RouteArgs a) {
             xv[q] = (uint32_t)f2h(x0) | ((uint32_t)f2h(x1) << 16);
         }
     }
-    if (tid < 256) {
-        *(u4v*)(xn + 8 * tid) = xv;
+    *(u4v*)(xn + 8 * tid) = xv;
+    if (grp == 0) {
         if (a.xn) *(u4v*)(a.xn + (size_t)r * RT_H + 8 * tid) = xv;
         if (a.xperm)
             emit_qx(xv, lane, a.xperm + (size_t)r * RT_H, a.xsum + (size_t)r * (RT_H / 64), 8 * tid);
     }
     __syncthreads();
 
-    // logits: all partial dot products of a round, then their reductions together
     u4v xa[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) xa[c] = *(const u4v*)(xn + 512 * c + 8 * lane);
-    for (int e0 = 0; e0 < E; e0 += 8 * RR_EPW) {
-        if (e0 > 0) load_round(e0);
-        float acc[RR_EPW];
+    float acc[2];
 #pragma unroll
-        for (int j = 0; j < RR_EPW; ++j) {
-            acc[j] = 0.0f;
+    for (int j = 0; j < 2; ++j) {
+        acc[j] = 0.0f;
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[j] = dot2(wr[j][c][q], xa[c][q], acc[j]);
-        }
-#pragma unroll
-        for (int m = 32; m > 0; m >>= 1)
-#pragma unroll
-            for (int j = 0; j < RR_EPW; ++j) acc[j] += __shfl_xor(acc[j], m, MJ_WAVE);
-        if (lane == 0) {
-#pragma unroll
-            for (int j = 0; j < RR_EPW; ++j) {
-                const int e = e0 + wv + 8 * j;
-                if (e < E) s_lg[e] = acc[j];
-            }
-        }
+            for (int q = 0; q < 4; ++q) acc[j] = dot2(wr[j][c][q], xa[c][q], acc[j]);
     }
-    __syncthreads();
-    if (wv != 0) return;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[j] += __shfl_xor(acc[j], m, MJ_WAVE);
+    if (lane == 0) *(float2*)(a.logits + (size_t)r * E + e0) = make_float2(acc[0], acc[1]);
+}
 
-    // top-k of the row (wave 0): lane holds experts lane + 64 i
+// Top-k of one row's E logits on one wave (lane holds experts lane + 64 i): experts in rank
+// order into inds[0..k), softmax weights renormalised over the k (summed in rank order) into
+// gate[0..k).  Ranking: higher logit first, the lower index on equal logits.
+__device__ __forceinline__ void row_topk(const float* s_lg, int E, int k, int* s_ind,
+                                         float* s_gate) {
+    const int lane = threadIdx.x & 63;
+    if (E <= 64) {
+        // one expert per lane: ranks from the 64 logits broadcast one by one (readlane)
+        const float l = lane < E ? s_lg[lane] : -INFINITY;
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+            const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), j));
+            rank += (int)(o > l) + (int)(o == l) * (int)(j < lane);
+        }
+        const float mx = wave_max(l);
+        const float g = lane < E ? expf(l - mx) : 0.0f;
+        const float z = wave_sum(g);
+        if (lane < E && rank < k) {
+            s_gate[rank] = g / z;
+            s_ind[rank] = lane;
+        }
+        __builtin_amdgcn_wave_barrier();
+        float ssum = 0.0f;
+        for (int j = 0; j < k; ++j) ssum += s_gate[j];  // in rank order
+        const float mine = lane < k ? s_gate[lane] / ssum : 0.0f;
+        __builtin_amdgcn_wave_barrier();
+        if (lane < k) s_gate[lane] = mine;
+        __builtin_amdgcn_wave_barrier();
+        return;
+    }
     float lv[4];
     int rank[4];
     float mx = -INFINITY;
@@ -390,44 +449,73 @@ __global__ __launch_bounds__(512) void k_route_row(RouteArgs a) {
         const int e = lane + 64 * i;
         if (e < E && rank[i] < k) {
             s_gate[rank[i]] = g[i] / z;
-            a.inds[r * k + rank[i]] = e;
+            s_ind[rank[i]] = e;
         }
     }
     __builtin_amdgcn_wave_barrier();
-    if (lane < k) {
-        float ssum = 0.0f;
-        for (int j = 0; j < k; ++j) ssum += s_gate[j];  // in rank order
-        a.scores[r * k + lane] = s_gate[lane] / ssum;
-    }
-    // append (row, slot) pairs to the experts' lists (order inside a list is immaterial: every
-    // pair's output is computed the same way wherever it sits)
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E && rank[i] < k) {
-            const int pos = atomicAdd(&a.ecnt[e], 1);
-            a.eplist[e * MJ_ROWS + pos] = r * k + rank[i];
+    float ssum = 0.0f;
+    for (int j = 0; j < k; ++j) ssum += s_gate[j];  // in rank order
+    const float mine = lane < k ? s_gate[lane] / ssum : 0.0f;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < k) s_gate[lane] = mine;
+    __builtin_amdgcn_wave_barrier();
+}
+
+// inds and scores of every row, and the per-expert pair lists of the tile gathers: one
+// 512-thread block, wave w ranks rows w, w + 8, ...  Pairs are grouped by expert with LDS
+// atomics and the lists written out with plain stores (every count rewritten each launch, so
+// nothing needs clearing).  Order inside a list is immaterial: every pair's output is computed
+// the same way wherever it sits.
+__global__ __launch_bounds__(512) void k_route_topk(RouteArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, E = a.E, k = a.k;
+    extern __shared__ __align__(16) float s_lg[];  // [M][E]: all rows in one round of loads
+    __shared__ float s_gate[8][8];
+    __shared__ int s_ind[8][8];
+    __shared__ int s_cnt[MJ_MAX_EXPERTS];
+    if (aborted(a.abort)) return;
+    for (int e = tid; e < E; e += 512) s_cnt[e] = 0;
+    for (int i = tid; i < a.M * E; i += 512) s_lg[i] = a.logits[i];
+    __syncthreads();
+    for (int r = wv; r < a.M; r += 8) {
+        row_topk(s_lg + (size_t)r * E, E, k, s_ind[wv], s_gate[wv]);
+        if (lane < k) {
+            const int e = s_ind[wv][lane];
+            a.inds[r * k + lane] = e;
+            a.scores[r * k + lane] = s_gate[wv][lane];
+            if (a.ecnt) {
+                const int pos = atomicAdd(&s_cnt[e], 1);
+                a.eplist[e * MJ_ROWS + pos] = r * k + lane;
+            }
         }
+        __builtin_amdgcn_wave_barrier();
     }
-}
-
-__global__ void k_zero_i32(int* p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0;
-}
-
-hipError_t launch_zero_i32(int* p, int n, hipStream_t st) {
-    hipLaunchKernelGGL(k_zero_i32, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
-    return hipGetLastError();
+    if (!a.ecnt) return;
+    __syncthreads();
+    for (int e = tid; e < E; e += 512) a.ecnt[e] = s_cnt[e];
 }
 
 bool route_supported(int H, int E, int k) {
-    return H == RT_H && E >= 8 && E <= MJ_MAX_EXPERTS && E % 4 == 0 && k >= 1 && k <= 8 && k <= E;
+    return H == RT_H && E >= RS_EPB && E <= MJ_MAX_EXPERTS && E % RS_EPB == 0 && k >= 1 &&
+           k <= 8 && k <= E;
 }
 
-hipError_t launch_route(const RouteArgs& a, int H, hipStream_t st) {
+hipError_t launch_route_logits(const RouteArgs& a, int H, hipStream_t st) {
     if (!route_supported(H, a.E, a.k) || a.M < 1 || a.M > MJ_ROWS) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_route_row, dim3(a.M), dim3(512), 0, st, a);
+    if (!a.logits) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route_logits, dim3(a.M * (a.E / RS_EPB)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
-hipError_t set_moe_attributes() { return hipSuccess; }
+hipError_t launch_route_topk(const RouteArgs& a, hipStream_t st) {
+    if (a.E > MJ_MAX_EXPERTS || a.k > 8 || a.M < 1 || (a.ecnt && a.M > MJ_ROWS))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route_topk, dim3(1), dim3(512), (size_t)a.M * a.E * 4, st, a);
+    return hipGetLastError();
+}
+
+hipError_t set_moe_attributes() {
+    // the top-k block stages every row's logits: up to MJ_ROWS x MJ_MAX_EXPERTS floats
+    return hipFuncSetAttribute((const void*)k_route_topk,
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               MJ_ROWS * MJ_MAX_EXPERTS * 4);
+}

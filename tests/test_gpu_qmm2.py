@@ -130,6 +130,30 @@ def test_moe_block(ctx, orc, M, flags):
     assert rel < 5e-3
 
 
+@pytest.mark.parametrize("M", [9, 20, 40])
+def test_moe_block_all_rows_on_each_expert(ctx, orc, M):
+    """8 experts with top-8: every row picks every expert, so each expert's gather serves all M
+    rows -- more than one pass of staged rows (9 per pass) for M = 20 and 40."""
+    import torch
+
+    print(f"case: moe all experts M={M}", flush=True)
+    rng = np.random.default_rng(300 + M)
+    E, H, I, gs, k = 8, 2048, 1024, 64, 8
+    mw = synth.moe_weights(rng, E, H, I, gs, top_k=k)
+    x = synth.normal_f16(rng, (M, H))
+    ref_y, ref_i, ref_s = orc.moe_block(mw, x, prenorm=True, residual=True)
+    dmw = _moe_dev(mw)
+    dx = dev(x)
+    y = torch.empty_like(dx)
+    inds = torch.empty((M, k), dtype=torch.int32, device="cuda")
+    scores = torch.empty((M, k), dtype=torch.float32, device="cuda")
+    _run(ctx, lambda: ctx.moe_block(dmw, dx, y, M, 3, inds, scores))
+    assert (host(inds) == ref_i).all()
+    assert np.allclose(host(scores), ref_s, rtol=1e-4, atol=1e-5)
+    rel, _ = assert_close(host(y), ref_y, what=f"moe all experts M={M}")
+    assert rel < 5e-3
+
+
 def test_abort_word_skips_work(ctx):
     import torch
 
