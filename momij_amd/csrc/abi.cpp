@@ -305,6 +305,8 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
         ms.down = (uint16_t*)a.take((size_t)M * k * H * 2);
         ms.ecnt = (int*)a.take((size_t)E * 4);
         ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
+        ms.elist = (int*)a.take((size_t)(E > 64 ? E : 64) * 4);
+        ms.ne = (int*)a.take(4);
     };
     layout(ar);
     mj_status s = mj_scratch_reserve(ctx, ar.off);
@@ -339,6 +341,8 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.logits = ms.logits;
         ra.ecnt = tile ? ms.ecnt : nullptr;
         ra.eplist = tile ? ms.eplist : nullptr;
+        ra.elist = tile ? ms.elist : nullptr;
+        ra.ne = tile ? ms.ne : nullptr;
         ra.M = M;
         ra.E = E;
         ra.k = k;
@@ -422,6 +426,8 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         if (tile) {
             up.ecnt = ms.ecnt;
             up.eplist = ms.eplist;
+            up.elist = ms.elist;
+            up.ne = ms.ne;
         } else {
             up.bk = ms.bk;
         }

@@ -37,6 +37,8 @@ struct MoeScratch {
     uint16_t* down;      // [M*k][H]
     int* ecnt;           // pairs per expert [E]
     int* eplist;         // pair lists per expert [E][MJ_ROWS]
+    int* elist;          // routed experts, increasing id [E]
+    int* ne;             // number of routed experts
 };
 
 // Optional per-kernel-class event timing of eager passes (classes of mj_model_kernel_ms).

@@ -109,6 +109,8 @@ struct GatherArgs {
     const Buckets* bk;      // fallback kernel: rows grouped by expert (nullptr: dense)
     const int* ecnt;        // tile kernel: pairs per expert [E]
     const int* eplist;      // tile kernel: pair lists [E][MJ_ROWS]
+    const int* elist;       // tile kernel, persistent: routed experts [64], their count *ne
+    const int* ne;
     int dense_rows;         // dense: rows 0 .. dense_rows-1 of expert 0
     uint16_t* y;            // STORE/ADD: [pairs][N] ; SWIGLU: act qx [pairs][I]
     float2* ysum;           // SWIGLU: act sums [pairs][I/64]
@@ -221,6 +223,8 @@ struct RouteArgs {
     float* logits;           // [M][E] router logits
     int* ecnt;               // pairs per expert [E] (route lists)
     int* eplist;             // pair lists [E][MJ_ROWS] (route lists)
+    int* elist;              // routed experts in increasing id [E] (nullable)
+    int* ne;                 // number of routed experts [1]
     int M, E, k;
     float eps;
     const int* abort;

@@ -492,6 +492,23 @@ __global__ __launch_bounds__(512) void k_route_topk(RouteArgs a) {
     if (!a.ecnt) return;
     __syncthreads();
     for (int e = tid; e < E; e += 512) a.ecnt[e] = s_cnt[e];
+    if (!a.elist) return;
+    // the routed experts in increasing id (a compact work list for the gathers) and their count
+    __shared__ int s_wsum[8];
+    int base = 0;
+    for (int e0 = 0; e0 < E; e0 += 512) {
+        const int e = e0 + tid;
+        const bool on = e < E && s_cnt[e] > 0;
+        const uint64_t bal = __ballot(on);
+        if (lane == 0) s_wsum[wv] = __popcll(bal);
+        __syncthreads();
+        int before = base;
+        for (int w = 0; w < wv; ++w) before += s_wsum[w];
+        if (on) a.elist[before + __popcll(bal & ((1ull << lane) - 1))] = e;
+        for (int w = 0; w < 8; ++w) base += s_wsum[w];
+        __syncthreads();
+    }
+    if (tid == 0) *a.ne = base;
 }
 
 bool route_supported(int H, int E, int k) {
