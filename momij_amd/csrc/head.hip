@@ -333,7 +333,6 @@ hipError_t launch_hold(unsigned us, hipStream_t st) {
 
 hipError_t set_attn_attributes();
 hipError_t set_gather3_attributes();
-hipError_t set_moe_attributes();
 
 hipError_t set_kernel_attributes() {
     static bool done = false;
@@ -345,7 +344,6 @@ hipError_t set_kernel_attributes() {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
     if (e == hipSuccess) e = set_gather3_attributes();
-    if (e == hipSuccess) e = set_moe_attributes();
     if (e == hipSuccess) done = true;
     return e;
 }

@@ -384,131 +384,218 @@ __global__ __launch_bounds__(256) void k_route_logits(RouteArgs a) {
     if (lane == 0) *(float2*)(a.logits + (size_t)r * E + e0) = make_float2(acc[0], acc[1]);
 }
 
-// Top-k of one row's E logits on one wave (lane holds experts lane + 64 i): experts in rank
-// order into inds[0..k), softmax weights renormalised over the k (summed in rank order) into
-// gate[0..k).  Ranking: higher logit first, the lower index on equal logits.
-__device__ __forceinline__ void row_topk(const float* s_lg, int E, int k, int* s_ind,
-                                         float* s_gate) {
+// Wave-wide reductions for the top-k, in DPP lane moves instead of LDS-routed shuffles: xor 1
+// and xor 2 inside each quad, the half-row and row mirrors (so every lane of a row of 16 holds
+// the row's result), then the four rows' results combined from lanes 0, 16, 32 and 48.  Every
+// lane returns the same value.
+template <class T>
+__device__ __forceinline__ T dpp_move(T v, int ctrl);
+template <>
+__device__ __forceinline__ float dpp_move<float>(float v, int ctrl) {
+    const int x = __float_as_int(v);
+    int r;
+    switch (ctrl) {  // the control word has to be a constant
+        case 0xB1: r = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false); break;
+        case 0x4E: r = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false); break;
+        case 0x141: r = __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false); break;
+        default: r = __builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false); break;
+    }
+    return __int_as_float(r);
+}
+template <>
+__device__ __forceinline__ uint64_t dpp_move<uint64_t>(uint64_t v, int ctrl) {
+    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+    int a, b;
+    switch (ctrl) {
+        case 0xB1:
+            a = __builtin_amdgcn_update_dpp(lo, lo, 0xB1, 0xF, 0xF, false);
+            b = __builtin_amdgcn_update_dpp(hi, hi, 0xB1, 0xF, 0xF, false);
+            break;
+        case 0x4E:
+            a = __builtin_amdgcn_update_dpp(lo, lo, 0x4E, 0xF, 0xF, false);
+            b = __builtin_amdgcn_update_dpp(hi, hi, 0x4E, 0xF, 0xF, false);
+            break;
+        case 0x141:
+            a = __builtin_amdgcn_update_dpp(lo, lo, 0x141, 0xF, 0xF, false);
+            b = __builtin_amdgcn_update_dpp(hi, hi, 0x141, 0xF, 0xF, false);
+            break;
+        default:
+            a = __builtin_amdgcn_update_dpp(lo, lo, 0x140, 0xF, 0xF, false);
+            b = __builtin_amdgcn_update_dpp(hi, hi, 0x140, 0xF, 0xF, false);
+            break;
+    }
+    return ((uint64_t)(uint32_t)b << 32) | (uint32_t)a;
+}
+__device__ __forceinline__ float lane_value(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ uint64_t lane_value(uint64_t v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce_dpp(T v, Op op) {
+    v = op(v, dpp_move(v, 0xB1));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_move(v, 0x4E));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_move(v, 0x141));  // row_half_mirror
+    v = op(v, dpp_move(v, 0x140));  // row_mirror
+    return op(op(lane_value(v, 0), lane_value(v, 16)), op(lane_value(v, 32), lane_value(v, 48)));
+}
+
+// Top-k of one row on one wave, lane holding experts lane + 64 i (i < NI; NI = 1 when E <= 64).
+// s_row holds the row's logits padded with -inf to 64 NI.  Lanes < k return the rank-order
+// expert and its softmax weight renormalised over the k (summed in rank order).  Ranking:
+// higher logit first, the lower index on equal logits.
+template <int NI>
+__device__ __forceinline__ void row_topk(const float* s_row, int E, int k, int* s_ind,
+                                         float* s_gate, int& ind, float& gate) {
     const int lane = threadIdx.x & 63;
-    if (E <= 64) {
-        // one expert per lane: ranks from the 64 logits broadcast one by one (readlane)
-        const float l = lane < E ? s_lg[lane] : -INFINITY;
-        int rank = 0;
+    const auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
+    const auto add_op = [](float x, float y) { return x + y; };
+    if constexpr (NI == 1) {
+        // rank = experts ahead of this lane's: larger logit, or an equal logit at a lower
+        // index.  The row is read as broadcast float4s issued together and "larger" counted
+        // from the sign of l - o (exact for distinct finite values, +0 for equal ones; -0 was
+        // folded into +0 when the row was staged).  Without ties the counts of the E experts
+        // are a permutation of 0..E-1; any other sum sends the row through the exact
+        // comparison rule.  Padding is -inf, which no real logit is below.
+        const float l = s_row[lane];
+        f4 o[16];
 #pragma unroll
-        for (int j = 0; j < 64; ++j) {
-            const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), j));
-            rank += (int)(o > l) + (int)(o == l) * (int)(j < lane);
+        for (int j4 = 0; j4 < 16; ++j4) o[j4] = *(const f4*)(s_row + 4 * j4);
+        uint32_t gt = 0;
+#pragma unroll
+        for (int j4 = 0; j4 < 16; ++j4)
+#pragma unroll
+            for (int c = 0; c < 4; c += 2)
+                gt += (__float_as_uint(l - o[j4][c]) >> 31) + (__float_as_uint(l - o[j4][c + 1]) >> 31);
+        int rank = (int)gt;
+        const float rsum = wave_reduce_dpp(lane < E ? (float)gt : 0.0f, add_op);
+        if (rsum != 0.5f * (float)(E * (E - 1))) {
+            rank = 0;
+            for (int jj = 0; jj < E; ++jj) {
+                const float oj = s_row[jj];
+                rank += (int)(oj > l) + (int)(oj == l && jj < lane);
+            }
         }
-        const float mx = wave_max(l);
+        const float mx = wave_reduce_dpp(l, fmax_op);
         const float g = lane < E ? expf(l - mx) : 0.0f;
-        const float z = wave_sum(g);
+        const float z = wave_reduce_dpp(g, add_op);
         if (lane < E && rank < k) {
             s_gate[rank] = g / z;
             s_ind[rank] = lane;
         }
-        __builtin_amdgcn_wave_barrier();
-        float ssum = 0.0f;
-        for (int j = 0; j < k; ++j) ssum += s_gate[j];  // in rank order
-        const float mine = lane < k ? s_gate[lane] / ssum : 0.0f;
-        __builtin_amdgcn_wave_barrier();
-        if (lane < k) s_gate[lane] = mine;
-        __builtin_amdgcn_wave_barrier();
-        return;
-    }
-    float lv[4];
-    int rank[4];
-    float mx = -INFINITY;
+    } else {
+        // k rounds of a wave arg-max over (logit, -index) keys give the selection in rank order
+        float lv[NI], mx = -INFINITY;
+        uint64_t key[NI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        lv[i] = e < E ? s_lg[e] : -INFINITY;
-        mx = fmaxf(mx, lv[i]);
-        rank[i] = 0;
-    }
-    for (int e2 = 0; e2 < E; e2 += 4) {
-        const f4 o = *(const f4*)(s_lg + e2);
+        for (int i = 0; i < NI; ++i) {
+            const int e = lane + 64 * i;
+            lv[i] = s_row[e];
+            mx = fmaxf(mx, lv[i]);
+            uint32_t o = __float_as_uint(lv[i] + 0.0f);
+            o = (o & 0x80000000u) ? ~o : (o | 0x80000000u);
+            key[i] = e < E ? ((uint64_t)o << 32) | (uint32_t)(0xffffu - e) : 0;
+        }
+        mx = wave_reduce_dpp(mx, fmax_op);
+        float z = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i) z += lane + 64 * i < E ? expf(lv[i] - mx) : 0.0f;
+        z = wave_reduce_dpp(z, add_op);
+        const auto umax_op = [](uint64_t x, uint64_t y) { return x > y ? x : y; };
+        for (int j = 0; j < k; ++j) {
+            uint64_t best = key[0];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * i;
-                rank[i] += (int)(o[c] > lv[i]) + (int)(o[c] == lv[i]) * (int)(e2 + c < e);
+            for (int i = 1; i < NI; ++i) best = key[i] > best ? key[i] : best;
+            best = wave_reduce_dpp(best, umax_op);
+            const int e = 0xffff - (int)(uint32_t)(best & 0xffffu);
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                if (key[i] == best) key[i] = 0;
+            if (lane == 0) {
+                s_gate[j] = expf(s_row[e] - mx) / z;
+                s_ind[j] = e;
             }
-    }
-    mx = wave_max(mx);
-    float z = 0.0f, g[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        g[i] = e < E ? expf(lv[i] - mx) : 0.0f;
-        z += g[i];
-    }
-    z = wave_sum(z);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E && rank[i] < k) {
-            s_gate[rank[i]] = g[i] / z;
-            s_ind[rank[i]] = e;
         }
     }
     __builtin_amdgcn_wave_barrier();
+    const f4 ga = *(const f4*)s_gate, gb = *(const f4*)(s_gate + 4);
     float ssum = 0.0f;
-    for (int j = 0; j < k; ++j) ssum += s_gate[j];  // in rank order
-    const float mine = lane < k ? s_gate[lane] / ssum : 0.0f;
-    __builtin_amdgcn_wave_barrier();
-    if (lane < k) s_gate[lane] = mine;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+        if (jj < k) ssum += jj < 4 ? ga[jj] : gb[jj - 4];  // in rank order
+    if (lane < k) {
+        gate = s_gate[lane] / ssum;
+        ind = s_ind[lane];
+    }
     __builtin_amdgcn_wave_barrier();
 }
 
 // inds and scores of every row, and the per-expert pair lists of the tile gathers: one
-// 512-thread block, wave w ranks rows w, w + 8, ...  Pairs are grouped by expert with LDS
-// atomics and the lists written out with plain stores (every count rewritten each launch, so
-// nothing needs clearing).  Order inside a list is immaterial: every pair's output is computed
-// the same way wherever it sits.
-__global__ __launch_bounds__(512) void k_route_topk(RouteArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, E = a.E, k = a.k;
-    extern __shared__ __align__(16) float s_lg[];  // [M][E]: all rows in one round of loads
-    __shared__ float s_gate[8][8];
-    __shared__ int s_ind[8][8];
+// 1024-thread block, wave w ranks rows w, w + 16, ... (M <= 64: at most four each, all their
+// logits requested before the first is ranked).  Pairs are grouped by expert with LDS atomics
+// and the lists written out with plain stores (every count rewritten each launch, so nothing
+// needs clearing).  Order inside a list is immaterial: every pair's output is computed the
+// same way wherever it sits.
+#define RT_WAVES 16
+template <int NI>
+__global__ __launch_bounds__(64 * RT_WAVES) void k_route_topk(RouteArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, E = a.E, k = a.k, M = a.M;
+    __shared__ __align__(16) float s_row[RT_WAVES][64 * NI];
+    __shared__ __align__(16) float s_gate[RT_WAVES][8];
+    __shared__ int s_ind[RT_WAVES][8];
     __shared__ int s_cnt[MJ_MAX_EXPERTS];
+    __shared__ int s_wsum[RT_WAVES];
     if (aborted(a.abort)) return;
-    for (int e = tid; e < E; e += 512) s_cnt[e] = 0;
-    for (int i = tid; i < a.M * E; i += 512) s_lg[i] = a.logits[i];
-    __syncthreads();
-    for (int r = wv; r < a.M; r += 8) {
-        row_topk(s_lg + (size_t)r * E, E, k, s_ind[wv], s_gate[wv]);
+    if (tid < E) s_cnt[tid] = 0;
+    // all of the wave's rows (at most four) requested up front, every load unconditional
+    // (clamped row and expert) so no branch waits on one
+    float v[4][NI];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            v[s][i] = a.logits[min(wv + RT_WAVES * s, M - 1) * E + min(lane + 64 * i, E - 1)];
+    __syncthreads();  // s_cnt cleared
+#pragma unroll 1
+    for (int s = 0, r = wv; r < M; ++s, r += RT_WAVES) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const float t = s == 0 ? v[0][i] : s == 1 ? v[1][i] : s == 2 ? v[2][i] : v[3][i];
+            s_row[wv][lane + 64 * i] = lane + 64 * i < E ? t + 0.0f : -INFINITY;
+        }
+        __builtin_amdgcn_wave_barrier();
+        int e = 0;
+        float gate = 0.0f;
+        row_topk<NI>(s_row[wv], E, k, s_ind[wv], s_gate[wv], e, gate);
         if (lane < k) {
-            const int e = s_ind[wv][lane];
             a.inds[r * k + lane] = e;
-            a.scores[r * k + lane] = s_gate[wv][lane];
+            a.scores[r * k + lane] = gate;
             if (a.ecnt) {
                 const int pos = atomicAdd(&s_cnt[e], 1);
                 a.eplist[e * MJ_ROWS + pos] = r * k + lane;
             }
         }
-        __builtin_amdgcn_wave_barrier();
     }
     if (!a.ecnt) return;
     __syncthreads();
-    for (int e = tid; e < E; e += 512) a.ecnt[e] = s_cnt[e];
+    if (tid < E) a.ecnt[tid] = s_cnt[tid];
     if (!a.elist) return;
     // the routed experts in increasing id (a compact work list for the gathers) and their count
-    __shared__ int s_wsum[8];
-    int base = 0;
-    for (int e0 = 0; e0 < E; e0 += 512) {
-        const int e = e0 + tid;
-        const bool on = e < E && s_cnt[e] > 0;
-        const uint64_t bal = __ballot(on);
-        if (lane == 0) s_wsum[wv] = __popcll(bal);
-        __syncthreads();
-        int before = base;
-        for (int w = 0; w < wv; ++w) before += s_wsum[w];
-        if (on) a.elist[before + __popcll(bal & ((1ull << lane) - 1))] = e;
-        for (int w = 0; w < 8; ++w) base += s_wsum[w];
-        __syncthreads();
+    const bool on = tid < E && s_cnt[tid] > 0;
+    const uint64_t bal = __ballot(on);
+    if (lane == 0) s_wsum[wv] = __popcll(bal);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < RT_WAVES; ++w) {
+        before += w < wv ? s_wsum[w] : 0;
+        total += s_wsum[w];
     }
-    if (tid == 0) *a.ne = base;
+    if (on) a.elist[before + __popcll(bal & ((1ull << lane) - 1))] = tid;
+    if (tid == 0) *a.ne = total;
 }
 
 bool route_supported(int H, int E, int k) {
@@ -524,15 +611,13 @@ hipError_t launch_route_logits(const RouteArgs& a, int H, hipStream_t st) {
 }
 
 hipError_t launch_route_topk(const RouteArgs& a, hipStream_t st) {
-    if (a.E > MJ_MAX_EXPERTS || a.k > 8 || a.M < 1 || (a.ecnt && a.M > MJ_ROWS))
+    // one block: 16 waves with at most four rows each
+    if (a.E < 1 || a.E > MJ_MAX_EXPERTS || a.k < 1 || a.k > 8 || a.k > a.E || a.M < 1 ||
+        a.M > 4 * RT_WAVES || a.M > MJ_ROWS)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_route_topk, dim3(1), dim3(512), (size_t)a.M * a.E * 4, st, a);
+    if (a.E <= 64)
+        hipLaunchKernelGGL(k_route_topk<1>, dim3(1), dim3(64 * RT_WAVES), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_route_topk<MJ_MAX_EXPERTS / 64>, dim3(1), dim3(64 * RT_WAVES), 0, st, a);
     return hipGetLastError();
-}
-
-hipError_t set_moe_attributes() {
-    // the top-k block stages every row's logits: up to MJ_ROWS x MJ_MAX_EXPERTS floats
-    return hipFuncSetAttribute((const void*)k_route_topk,
-                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                               MJ_ROWS * MJ_MAX_EXPERTS * 4);
 }

@@ -154,6 +154,33 @@ def test_moe_block_all_rows_on_each_expert(ctx, orc, M):
     assert rel < 5e-3
 
 
+@pytest.mark.parametrize("E,I,M", [(64, 1024, 9), (64, 1024, 64), (128, 1024, 17), (40, 1024, 5)])
+def test_moe_routing_ties(ctx, orc, E, I, M):
+    """Router rows repeated in pairs, so every logit is tied with another expert's: the lower
+    index has to rank first, exactly as in the oracle (ties reach the exact comparison rule of
+    the top-k; E = 128 takes the several-experts-per-lane path)."""
+    import torch
+
+    print(f"case: moe routing ties E={E} I={I} M={M}", flush=True)
+    rng = np.random.default_rng(400 + E + M)
+    H, gs, k = 2048, 64, 8
+    mw = synth.moe_weights(rng, E, H, I, gs, top_k=k)
+    mw["router_w"][1::2] = mw["router_w"][0::2]
+    x = synth.normal_f16(rng, (M, H))
+    ref_y, ref_i, ref_s = orc.moe_block(mw, x, prenorm=True, residual=True)
+    assert (ref_i[:, 0] % 2 == 0).all() and (ref_i[:, 1] == ref_i[:, 0] + 1).all()
+    dmw = _moe_dev(mw)
+    dx = dev(x)
+    y = torch.empty_like(dx)
+    inds = torch.empty((M, k), dtype=torch.int32, device="cuda")
+    scores = torch.empty((M, k), dtype=torch.float32, device="cuda")
+    _run(ctx, lambda: ctx.moe_block(dmw, dx, y, M, 3, inds, scores))
+    assert (host(inds) == ref_i).all()
+    assert np.allclose(host(scores), ref_s, rtol=1e-4, atol=1e-5)
+    rel, _ = assert_close(host(y), ref_y, what=f"moe ties E={E} M={M}")
+    assert rel < 5e-3
+
+
 def test_abort_word_skips_work(ctx):
     import torch
 
