@@ -305,8 +305,7 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
         ms.down = (uint16_t*)a.take((size_t)M * k * H * 2);
         ms.ecnt = (int*)a.take((size_t)E * 4);
         ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
-        ms.elist = (int*)a.take((size_t)(E > 64 ? E : 64) * 4);
-        ms.ne = (int*)a.take(4);
+        ms.srec = (int*)a.take((size_t)64 * 64 * 4);
     };
     layout(ar);
     mj_status s = mj_scratch_reserve(ctx, ar.off);
@@ -339,10 +338,10 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.inds = inds;
         ra.scores = scores;
         ra.logits = ms.logits;
-        ra.ecnt = tile ? ms.ecnt : nullptr;
-        ra.eplist = tile ? ms.eplist : nullptr;
-        ra.elist = tile ? ms.elist : nullptr;
-        ra.ne = tile ? ms.ne : nullptr;
+        // E <= 64: slot records for the persistent gathers; more experts: per-expert lists
+        ra.srec = tile && E <= 64 ? ms.srec : nullptr;
+        ra.ecnt = tile && E > 64 ? ms.ecnt : nullptr;
+        ra.eplist = tile && E > 64 ? ms.eplist : nullptr;
         ra.M = M;
         ra.E = E;
         ra.k = k;
@@ -424,10 +423,9 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         up.s = (const uint16_t*)w->up_gate_s;
         up.b = (const uint16_t*)w->up_gate_b;
         if (tile) {
-            up.ecnt = ms.ecnt;
-            up.eplist = ms.eplist;
-            up.elist = ms.elist;
-            up.ne = ms.ne;
+            up.srec = E <= 64 ? ms.srec : nullptr;
+            up.ecnt = E > 64 ? ms.ecnt : nullptr;
+            up.eplist = E > 64 ? ms.eplist : nullptr;
         } else {
             up.bk = ms.bk;
         }

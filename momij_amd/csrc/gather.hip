@@ -118,27 +118,27 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
     int cb = blockIdx.x % ncb;
     const bool own_sums = a.xsum == nullptr;  // block sums formed here from the staged rows
 
-    // Persistent expert mode (PER): the work items are (routed expert elist[i / ncb], column
-    // block i % ncb), i < ne * ncb; block b takes items b, b + gridDim.x, ...  Each item's count
-    // and pair list are fetched while the previous item computes.  Expert mode: block u serves
-    // expert u, whose ecnt[u] (row, slot) pairs are listed at eplist[u * MJ_ROWS ..]; count and
-    // list are loaded together (lane j: pair j), and an expert nobody picked ends here.  Bucket
-    // mode: block u serves the u-th expert of a Buckets table.  Dense: rows 0 .. dense_rows-1.
+    // Persistent expert mode (PER): the work items are (routed-expert slot i / ncb, column
+    // block i % ncb); block b takes items b, b + gridDim.x, ... until a slot with no pairs.
+    // One load per lane brings a slot's record: pair j in lane j, the expert id and the pair
+    // count in the high halves of lanes 0 and 1; the next item's record is fetched while the
+    // current item computes.  Expert mode: block u serves expert u, whose ecnt[u] (row, slot)
+    // pairs are listed at eplist[u * MJ_ROWS ..]; count and list are loaded together, and an
+    // expert nobody picked ends here.  Bucket mode: block u serves the u-th expert of a Buckets
+    // table.  Dense: rows 0 .. dense_rows-1.
     const int* plist = nullptr;
-    int lpair = 0;  // expert mode: pair j of the list in lane j
+    int lpair = 0;  // expert modes: pair j of the list in lane j
     int e = 0, np = a.dense_rows;
-    int item = blockIdx.x, nitems = 0, elv = 0;
-    int e_n = 0, cb_n = 0, np_n = 0, lpair_n = 0;  // the next item (persistent mode)
+    int item = blockIdx.x;
+    int rec_n = 0;  // the next item's record (persistent mode)
     {
         const int ab = a.abort ? *a.abort : 0;
         if constexpr (PER) {
-            nitems = *a.ne * ncb;
-            if (ab || item >= nitems) return;  // whole block
-            elv = a.elist[lane];
-            e = __builtin_amdgcn_readlane(elv, item / ncb);
+            const int rec = a.srec[min(item / ncb, 63) * MJ_ROWS + lane];
+            e = __builtin_amdgcn_readlane(rec, 0) >> 16;
+            np = item / ncb < 64 ? __builtin_amdgcn_readlane(rec, 1) >> 16 : 0;
+            lpair = rec & 0xFFFF;
             cb = item % ncb;
-            np = a.ecnt[e];
-            lpair = a.eplist[e * MJ_ROWS + lane];
         } else if (a.ecnt != nullptr) {
             e = u;
             np = a.ecnt[u];
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
     // MFMA output rows that are discarded).  Wave w stages rows w, w + WPB, ...
     auto stage_load = [&](int pb, int npass) {
         const int myr = min(pb + (lane < R ? lane : 0), np - 1);
-        const int prl = a.ecnt ? __shfl(lpair, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
+        const int prl = (PER || a.ecnt) ? __shfl(lpair, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
 #pragma unroll
         for (int j = 0; j < R / WPB; ++j) {
             const int r = wv + WPB * j;
@@ -256,17 +256,12 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
             own_block_sums(npass);
             lds_barrier<G + 2>();
         }
-        // persistent mode: the next item's count and pair list, fetched behind this item's
-        // weights (one vector load younger than them: PF)
+        // persistent mode: the next item's record, fetched behind this item's weights (one
+        // vector load younger than them: PF)
         constexpr int PF = PER ? 1 : 0;
         if constexpr (PER) {
-            if (pb == 0) {
-                const int nx = item + (int)gridDim.x < nitems ? item + (int)gridDim.x : item;
-                e_n = __builtin_amdgcn_readlane(elv, nx / ncb);
-                cb_n = nx % ncb;
-                np_n = a.ecnt[e_n];
-                lpair_n = a.eplist[e_n * MJ_ROWS + lane];
-            }
+            if (pb == 0)
+                rec_n = a.srec[min((item + (int)gridDim.x) / ncb, 63) * MJ_ROWS + lane];
         }
         wait_vmcnt<G + PF>();      // scales and biases have landed
         u4v sv[SCW], bv[SCW];
@@ -444,12 +439,13 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
     }
     if constexpr (!PER) break;
     item += gridDim.x;
-    if (item >= nitems) break;
+    if (item / ncb >= 64) break;
+    np = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
+    if (np <= 0) break;
     __syncthreads();  // this item is done with LDS
-    e = e_n;
-    cb = cb_n;
-    np = np_n;
-    lpair = lpair_n;
+    e = __builtin_amdgcn_readlane(rec_n, 0) >> 16;
+    cb = item % ncb;
+    lpair = rec_n & 0xFFFF;
   }
 }
 
@@ -477,8 +473,9 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     // rows on one expert are rare and take extra passes); dense projections take up to 16
     const int want = rows < 1 ? 1 : rows;
     int RA = want < S::R ? want : S::R;
-    const size_t limit = (EPI == EPI_SWIGLU || EPI == EPI_STORE) && a.ecnt ? 80 * 1024 - 256
-                                                                           : G5_LDS_MAX;
+    const bool expert = a.ecnt != nullptr || a.srec != nullptr;
+    const size_t limit =
+        (EPI == EPI_SWIGLU || EPI == EPI_STORE) && expert ? 80 * 1024 - 256 : G5_LDS_MAX;
     while (RA > 1 && S::lds(RA, want > RA) > limit) --RA;
     const bool multi = want > RA;
     int grid = n_buckets * ncb;
@@ -486,328 +483,6 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     launch_timed(k_gather5<KPL, GS, EPI, WPB, KS, PER>, dim3(grid), dim3(WPB * 64),
                  S::lds(RA, multi), st, a, RA, (int)multi);
     return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------------------
-// Register-landed tile gather for the expert products (SwiGLU up||gate, down).  The weight
-// stream goes straight into VGPRs, so LDS holds only the staged activation rows and a block
-// can keep more weight bytes in flight than LDS would hold: 8 waves = KS K-slices x CW wave
-// columns, each wave owning TPW 16-row tiles over its slice (block = CW * TPW tiles).
-// Lane (n, q) loads 64-block 4j + q of row n (a wave load covers 16 rows x 64 contiguous
-// bytes); a 4x4 word transpose across the lane quarters (v_permlane32_swap / 16_swap) then
-// gives lane (n, q) word q of blocks 4j .. 4j+3 -- the MFMA B layout of the tile kernel above.
-// Loads are issued group-major (group j of every tile, then j+1), and the activation operand of
-// a 64-block is read from LDS once for all the wave's tiles.  K-slices meet in LDS; slice-0
-// waves finish the tiles (epilogues as above).
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ u4v quarter_transpose(const u4v w) {
-    // before: quarter q holds words 0..3 of its own 64-block B_q; after: word q of B_0..B_3
-    auto x = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
-    auto y = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
-    auto c = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
-    auto d = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
-    return (u4v){c[0], c[1], d[0], d[1]};
-}
-
-template <int KPL, int GS, int EPI, int KS, int TPW>
-struct G7Shape {
-    static constexpr int WPB = 8;
-    static constexpr int R = 16;
-    static constexpr int K = KPL * 256;
-    static constexpr int KB = K / 64;
-    static constexpr int KBW = KB / KS;            // 64-blocks of a slice
-    static constexpr int CW = WPB / KS;            // wave columns
-    static constexpr int TPB = CW * TPW;           // tiles per block
-    static constexpr int SG = KBW * 64 / GS;       // scale groups of a row in a slice
-    static constexpr int XS = K + 8;
-    static constexpr int SS = KB + 2;
-    static constexpr int RED = (KS - 1) * TPB * 1024;  // K-slice partials
-    static_assert(KBW % 4 == 0 && SG % 8 == 0 && WPB % KS == 0, "shape");
-    __host__ __device__ static size_t lds(int RA) {
-        return (size_t)RA * XS * 2 + (size_t)RA * SS * 8 + (size_t)RED;
-    }
-};
-
-template <int KPL, int GS, int EPI, int KS, int TPW>
-__global__ __launch_bounds__(512) void k_gather7(GatherArgs a, int RA) {
-    using S = G7Shape<KPL, GS, EPI, KS, TPW>;
-    constexpr int R = S::R, K = S::K, KB = S::KB, KBW = S::KBW, CW = S::CW, TPB = S::TPB;
-    constexpr int XS = S::XS, SG = S::SG, WPB = S::WPB;
-    constexpr int NT = WPB * 64;
-    constexpr int PPR = K / 8;
-    constexpr int NG = KBW / 4;  // code groups (16 bytes per lane) of a tile slice
-    static_assert(EPI == EPI_SWIGLU || EPI == EPI_STORE, "expert epilogues only");
-    static_assert(PPR % 64 == 0 && R % WPB == 0, "shape");
-
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int q = lane >> 4, n = lane & 15;
-    const int kh = wv / CW, cw = wv % CW;  // K-slice and wave column
-    const int ncb = a.N / (16 * TPB);
-    const int u = blockIdx.x / ncb, cb = blockIdx.x % ncb;
-    const bool own_sums = a.xsum == nullptr;
-
-    const int* plist = nullptr;
-    int lpair = 0;
-    int e = 0, np = a.dense_rows;
-    {
-        const int ab = a.abort ? *a.abort : 0;
-        if (a.ecnt != nullptr) {
-            e = u;
-            np = a.ecnt[u];
-            lpair = a.eplist[u * MJ_ROWS + lane];
-        } else if (a.bk != nullptr) {
-            const Buckets* bk = a.bk;
-            const int cnt = bk->count, ee = bk->expert[u], s0 = bk->start[u], s1 = bk->start[u + 1];
-            if (u >= cnt) return;  // whole block
-            e = ee;
-            np = s1 - s0;
-            plist = bk->pair + s0;
-        }
-        if (ab || np <= 0) return;  // whole block
-    }
-
-    extern __shared__ __align__(16) char g7lds[];
-    uint16_t* xs = (uint16_t*)g7lds;                      // [RA][XS] qx rows
-    float2* xsl = (float2*)(xs + RA * XS);                // [RA][SS] block sums
-    char* red = (char*)(xsl + RA * S::SS);                // [KS-1][TPB][64] f4
-    __shared__ int s_pair[R];
-
-    auto stage_load = [&](int pb, int npass) {
-        const int myr = min(pb + (lane < R ? lane : 0), np - 1);
-        const int prl = a.ecnt ? __shfl(lpair, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
-#pragma unroll
-        for (int j = 0; j < R / WPB; ++j) {
-            const int r = wv + WPB * j;
-            const int pr = __builtin_amdgcn_readlane(prl, r);
-            if (lane == 0) s_pair[r] = pr;
-            if (r < npass) {
-                const char* src = (const char*)(a.xperm + (size_t)(pr / a.x_div) * K);
-#pragma unroll
-                for (int i = 0; i < PPR / 64; ++i)
-                    load_lds16(src + 1024 * i + 16 * lane, (char*)(xs + r * XS) + 1024 * i);
-                if (!own_sums && lane < KB / 2)
-                    load_lds16((const char*)(a.xsum + (size_t)(pr / a.x_div) * KB) + 16 * lane,
-                               xsl + r * S::SS);
-            }
-        }
-    };
-    auto own_block_sums = [&](int npass) {
-        for (int idx = tid; idx < npass * KB; idx += NT) {
-            const int r = idx % npass, b = idx / npass;
-            const uint16_t* xr = xs + r * XS + 64 * b;
-            float X = 0.0f, Bx = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const u4v v = *(const u4v*)(xr + 8 * c);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float base = ((4 * c + j) & 1) ? 4.0f : 16.0f;
-                    const float lo = h2f((uint16_t)v[j]), hi = h2f((uint16_t)(v[j] >> 16));
-                    X += lo + hi;
-                    Bx += base * (lo + hi);
-                }
-            }
-            lds_store_f2(xsl + r * S::SS + b, make_float2(X, Bx));
-        }
-    };
-
-    const int I = a.N / 2;
-    auto tile_row = [&](int t, int r) -> size_t {  // global row of row r of this wave's tile t
-        const int g = cb * TPB + cw * TPW + t;
-        if constexpr (EPI == EPI_SWIGLU)
-            return (size_t)e * a.N + (r < 8 ? g * 8 + r : I + g * 8 + r - 8);
-        else
-            return (size_t)e * a.N + g * 16 + r;
-    };
-
-    const int npass0 = min(RA, np);
-    stage_load(0, npass0);  // in flight ahead of the weight stream
-
-    // weights of this wave: scales and biases of row n (SG halves per tile), then the codes,
-    // group-major, straight into registers
-    u4v sv[TPW][SG / 8], bv[TPW][SG / 8], cw4[NG][TPW];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-        const uint16_t* sp = a.s + tile_row(t, n) * (K / GS) + kh * SG;
-        const uint16_t* bp = a.b + tile_row(t, n) * (K / GS) + kh * SG;
-#pragma unroll
-        for (int c = 0; c < SG / 8; ++c) {
-            sv[t][c] = *(const u4v*)(sp + 8 * c);
-            bv[t][c] = *(const u4v*)(bp + 8 * c);
-        }
-    }
-    {
-        const char* wg = (const char*)a.w;
-#pragma unroll
-        for (int j = 0; j < NG; ++j)
-#pragma unroll
-            for (int t = 0; t < TPW; ++t)
-                cw4[j][t] = *(const u4v*)(wg + tile_row(t, n) * (K / 4) +
-                                          16 * (kh * KBW + 4 * j + q));
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    const UnpackK uk = {opaque(0x00C000C0u), opaque(0x03000300u), opaque(0x4C004C00u),
-                        opaque(0x44004400u)};
-    const int xrow = min(n, RA - 1);
-    const uint16_t* xak = xs + xrow * XS + 16 * q + 64 * kh * KBW;  // A: row n, quarter q, slice
-
-    // weight loads issued after the first pass's staging (they may stay in flight past it)
-    constexpr int NW = 2 * TPW * (SG / 8) + NG * TPW;
-    static_assert(NW < 64, "vmcnt range");
-    // first_tag: std::true_type on the first pass (codes still to be transposed as they land)
-    auto run_pass = [&](int pb, int npass, auto first_tag) {
-        constexpr bool FIRST = decltype(first_tag)::value;
-        // every wave's staged rows visible
-        if constexpr (FIRST)
-            lds_barrier<NW>();
-        else
-            lds_barrier<0>();
-        if (own_sums) {
-            own_block_sums(npass);
-            if constexpr (FIRST)
-                lds_barrier<NW>();
-            else
-                lds_barrier<0>();
-        }
-        float acc[TPW][4];
-#pragma unroll
-        for (int t = 0; t < TPW; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NG; ++j) {
-            if constexpr (FIRST)
-#pragma unroll
-                for (int t = 0; t < TPW; ++t)
-                    cw4[j][t] = quarter_transpose(cw4[j][t]);
-#pragma unroll
-            for (int b4 = 0; b4 < 4; ++b4) {
-                const int B = 4 * j + b4;
-                u4v av[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) av[h] = *(const u4v*)(xak + 64 * B + 8 * h);
-                const int g = B * 64 / GS;
-#pragma unroll
-                for (int t = 0; t < TPW; ++t) {
-                    uint32_t v[8];
-                    unpack16k(opaque(cw4[j][t][b4]), v, uk);
-                    f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const u4v bq = {v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
-                        d = mfma16x16x32(as_h8(av[h]), as_h8(bq), d);
-                    }
-                    const uint32_t sw = sv[t][g / 8][(g % 8) / 2];
-                    const float sc = h2f((uint16_t)(sw >> (16 * (g & 1))));
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[t][r] += sc * d[r];
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < TPW; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) pin(acc[t][r]);
-        }
-        // + sum_B (b_B X_B - s_B Bx_B): fp32 MFMA chains over k = (block, term) pairs;
-        // A = activation sums of block 2i + q/2 (term q & 1), B = bias / -scale of row n
-        const bool hiq = q >= 2, bterm = (q & 1) == 0;
-        const float* xcs = (const float*)(xsl + xrow * S::SS + kh * KBW + (q >> 1)) + (q & 1);
-#pragma unroll
-        for (int t = 0; t < TPW; ++t) {
-            f4 corr[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-            for (int i = 0; i < KBW / 2; ++i) {
-                const float xa_k = xcs[4 * i];
-                const int g0 = (2 * i) * 64 / GS, g1 = (2 * i + 1) * 64 / GS;
-                const uint32_t s0 = (sv[t][g0 / 8][(g0 % 8) / 2] >> (16 * (g0 & 1))) & 0xFFFFu;
-                const uint32_t s1 = (sv[t][g1 / 8][(g1 % 8) / 2] >> (16 * (g1 & 1))) & 0xFFFFu;
-                const uint32_t b0 = (bv[t][g0 / 8][(g0 % 8) / 2] >> (16 * (g0 & 1))) & 0xFFFFu;
-                const uint32_t b1 = (bv[t][g1 / 8][(g1 % 8) / 2] >> (16 * (g1 & 1))) & 0xFFFFu;
-                const uint32_t sb = hiq ? s1 : s0, bb = hiq ? b1 : b0;
-                const float wk = bterm ? h2f((uint16_t)bb) : -h2f((uint16_t)sb);
-                corr[i & 1] = mfma16x16x4f32(xa_k, wk, corr[i & 1]);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[t][r] += corr[0][r] + corr[1][r];
-        }
-        if constexpr (KS > 1) {
-            // K-slices of a tile meet in LDS; slice 0 adds them in slice order
-            if (kh > 0)
-#pragma unroll
-                for (int t = 0; t < TPW; ++t)
-                    *((f4*)(red + ((kh - 1) * TPB + cw * TPW + t) * 1024) + lane) =
-                        (f4){acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
-            lds_barrier<0>();
-            if (kh == 0) {
-#pragma unroll
-                for (int k2 = 1; k2 < KS; ++k2)
-#pragma unroll
-                    for (int t = 0; t < TPW; ++t) {
-                        const f4 o = *((const f4*)(red + ((k2 - 1) * TPB + cw * TPW + t) * 1024) +
-                                       lane);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) acc[t][r] += o[r];
-                    }
-            }
-        }
-        if (kh != 0) return;
-        // lane (n, q) holds the outputs of activation rows 4q .. 4q+3 for weight row n
-#pragma unroll
-        for (int t = 0; t < TPW; ++t) {
-            const int g = cb * TPB + cw * TPW + t;
-            if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float gate_raw = __shfl_xor(acc[t][r], 8, MJ_WAVE);
-                    const int i = 4 * q + r;
-                    if (n < 8 && i < npass) {
-                        float up = hround(acc[t][r]);
-                        float gg = hround(gate_raw);
-                        gg = fminf(gg, 7.0f);
-                        up = fminf(fmaxf(up, -7.0f), 7.0f);
-                        const float act = hround(gg / (1.0f + expf(-gg)) * up);
-                        const int jj = g * 8 + n;
-                        a.y[(size_t)s_pair[i] * I + (jj & ~15) + perm_pos(jj & 15)] = f2h(act);
-                    }
-                }
-            } else {
-                const int col = g * 16 + n;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int i = 4 * q + r;
-                    if (i < npass) a.y[(size_t)s_pair[i] * a.N + col] = f2h(acc[t][r]);
-                }
-            }
-        }
-    };
-
-    run_pass(0, npass0, std::true_type{});
-    for (int pb = RA; pb < np; pb += RA) {
-        __syncthreads();  // the previous pass is done with LDS
-        const int npass = min(RA, np - pb);
-        stage_load(pb, npass);
-        run_pass(pb, npass, std::false_type{});
-    }
-}
-
-template <int KPL, int GS, int EPI, int KS, int TPW>
-static hipError_t launch_g7(const GatherArgs& a, int rows, int n_buckets, hipStream_t st) {
-    using S = G7Shape<KPL, GS, EPI, KS, TPW>;
-    const int ncb = a.N / (16 * S::TPB);
-    const int want = rows < 1 ? 1 : rows;
-    const int RA = want < S::R ? want : S::R;
-    launch_timed(k_gather7<KPL, GS, EPI, KS, TPW>, dim3(n_buckets * ncb), dim3(512), S::lds(RA),
-                 st, a, RA);
-    return hipGetLastError();
-}
-
-template <int KPL, int GS, int EPI, int KS, int TPW>
-static hipError_t g7_attr() {
-    return hipFuncSetAttribute((const void*)k_gather7<KPL, GS, EPI, KS, TPW>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)G7Shape<KPL, GS, EPI, KS, TPW>::lds(16));
 }
 
 // Shapes the tile kernel covers: SWIGLU / QKV / ADD at K = 2048, STORE at K = 1024 or 2048;
@@ -827,8 +502,10 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
                           hipStream_t st) {
     if (!gather3_supported(epi, a.K, a.N, a.gs)) return hipErrorInvalidValue;
     const int rows = max_rows_per_bucket;
-    // expert products over a compact routed-expert list (at most 64 experts): persistent
-    const bool per = a.ecnt && a.elist && a.ne && n_buckets <= 64;
+    // expert products over routed-expert slot records (at most 64 experts): persistent
+    const bool per = a.srec != nullptr;
+    if (per && (n_buckets > 64 || (epi != EPI_SWIGLU && epi != EPI_STORE)))
+        return hipErrorInvalidValue;
 #define MJ_G5(KPL, E, W, KS64, KS128)                                                      \
     if (per && (E == EPI_SWIGLU || E == EPI_STORE))                                         \
         return a.gs == 64 ? launch_g5<KPL, 64, E, W, KS64, true>(a, rows, n_buckets, st)    \

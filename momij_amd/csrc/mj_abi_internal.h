@@ -37,8 +37,7 @@ struct MoeScratch {
     uint16_t* down;      // [M*k][H]
     int* ecnt;           // pairs per expert [E]
     int* eplist;         // pair lists per expert [E][MJ_ROWS]
-    int* elist;          // routed experts, increasing id [E]
-    int* ne;             // number of routed experts
+    int* srec;           // routed-expert slot records [64][64] (E <= 64)
 };
 
 // Optional per-kernel-class event timing of eager passes (classes of mj_model_kernel_ms).

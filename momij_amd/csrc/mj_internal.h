@@ -109,8 +109,10 @@ struct GatherArgs {
     const Buckets* bk;      // fallback kernel: rows grouped by expert (nullptr: dense)
     const int* ecnt;        // tile kernel: pairs per expert [E]
     const int* eplist;      // tile kernel: pair lists [E][MJ_ROWS]
-    const int* elist;       // tile kernel, persistent: routed experts [64], their count *ne
-    const int* ne;
+    const int* srec;        // tile kernel, persistent: one record per routed-expert slot
+                            // [64][64]: lane j = pair j (low 16 bits); lane 0 also holds the
+                            // expert id, lane 1 the pair count (high 16 bits); count 0 past the
+                            // last routed expert
     int dense_rows;         // dense: rows 0 .. dense_rows-1 of expert 0
     uint16_t* y;            // STORE/ADD: [pairs][N] ; SWIGLU: act qx [pairs][I]
     float2* ysum;           // SWIGLU: act sums [pairs][I/64]
@@ -223,8 +225,8 @@ struct RouteArgs {
     float* logits;           // [M][E] router logits
     int* ecnt;               // pairs per expert [E] (route lists)
     int* eplist;             // pair lists [E][MJ_ROWS] (route lists)
-    int* elist;              // routed experts in increasing id [E] (nullable)
-    int* ne;                 // number of routed experts [1]
+    int* srec;               // slot records of the persistent gathers [64][64] (E <= 64;
+                             // nullable: then ecnt / eplist, when set, are written instead)
     int M, E, k;
     float eps;
     const int* abort;

@@ -409,8 +409,7 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         ms.down = (uint16_t*)a.take((size_t)R * c.top_k * H * 2);
         ms.ecnt = (int*)a.take((size_t)c.E * 4);
         ms.eplist = (int*)a.take((size_t)c.E * MJ_MAX_ROWS * 4);
-        ms.elist = (int*)a.take((size_t)(c.E > 64 ? c.E : 64) * 4);
-        ms.ne = (int*)a.take(4);
+        ms.srec = (int*)a.take((size_t)64 * 64 * 4);
     };
     Arena count;
     layout(count);

@@ -533,22 +533,27 @@ __device__ __forceinline__ void row_topk(const float* s_row, int E, int k, int* 
     __builtin_amdgcn_wave_barrier();
 }
 
-// inds and scores of every row, and the per-expert pair lists of the tile gathers: one
-// 1024-thread block, wave w ranks rows w, w + 16, ... (M <= 64: at most four each, all their
-// logits requested before the first is ranked).  Pairs are grouped by expert with LDS atomics
-// and the lists written out with plain stores (every count rewritten each launch, so nothing
-// needs clearing).  Order inside a list is immaterial: every pair's output is computed the
-// same way wherever it sits.
+// inds and scores of every row, and the pair lists of the tile gathers: one 1024-thread block,
+// wave w ranks rows w, w + 16, ... (M <= 64: at most four each, all their logits requested
+// before the first is ranked).  Pairs are grouped by expert with LDS atomics.  With slot records
+// (E <= 64) the routed experts are numbered in increasing id and slot s's record gets expert,
+// count and pairs (count 0 for every slot past the last); otherwise each expert's count and list
+// go to ecnt / eplist.  Every entry a reader uses is rewritten each launch, so nothing needs
+// clearing.  Order inside a list is immaterial: every pair's output is computed the same way
+// wherever it sits.
 #define RT_WAVES 16
 template <int NI>
 __global__ __launch_bounds__(64 * RT_WAVES) void k_route_topk(RouteArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, E = a.E, k = a.k, M = a.M;
+    constexpr bool SLOTS_OK = NI == 1;  // slot records: at most 64 experts
     __shared__ __align__(16) float s_row[RT_WAVES][64 * NI];
     __shared__ __align__(16) float s_gate[RT_WAVES][8];
     __shared__ int s_ind[RT_WAVES][8];
     __shared__ int s_cnt[MJ_MAX_EXPERTS];
+    __shared__ int s_pairs[SLOTS_OK ? 64 : 1][SLOTS_OK ? MJ_ROWS : 1];
     __shared__ int s_wsum[RT_WAVES];
     if (aborted(a.abort)) return;
+    const bool slots = SLOTS_OK && a.srec != nullptr;
     if (tid < E) s_cnt[tid] = 0;
     // all of the wave's rows (at most four) requested up front, every load unconditional
     // (clamped row and expert) so no branch waits on one
@@ -573,17 +578,22 @@ __global__ __launch_bounds__(64 * RT_WAVES) void k_route_topk(RouteArgs a) {
         if (lane < k) {
             a.inds[r * k + lane] = e;
             a.scores[r * k + lane] = gate;
-            if (a.ecnt) {
+            if (slots) {
+                const int pos = atomicAdd(&s_cnt[e], 1);
+                if constexpr (SLOTS_OK) s_pairs[e][pos] = r * k + lane;
+            } else if (a.ecnt) {
                 const int pos = atomicAdd(&s_cnt[e], 1);
                 a.eplist[e * MJ_ROWS + pos] = r * k + lane;
             }
         }
     }
-    if (!a.ecnt) return;
+    if (!slots && !a.ecnt) return;
     __syncthreads();
-    if (tid < E) a.ecnt[tid] = s_cnt[tid];
-    if (!a.elist) return;
-    // the routed experts in increasing id (a compact work list for the gathers) and their count
+    if (!slots) {
+        if (tid < E) a.ecnt[tid] = s_cnt[tid];
+        return;
+    }
+    // routed experts numbered in increasing id: slot = routed experts below this one
     const bool on = tid < E && s_cnt[tid] > 0;
     const uint64_t bal = __ballot(on);
     if (lane == 0) s_wsum[wv] = __popcll(bal);
@@ -594,8 +604,19 @@ __global__ __launch_bounds__(64 * RT_WAVES) void k_route_topk(RouteArgs a) {
         before += w < wv ? s_wsum[w] : 0;
         total += s_wsum[w];
     }
-    if (on) a.elist[before + __popcll(bal & ((1ull << lane) - 1))] = tid;
-    if (tid == 0) *a.ne = total;
+    if constexpr (SLOTS_OK) {
+        if (on) {
+            const int cnt = s_cnt[tid];
+            int* rec = a.srec + (before + __popcll(bal & ((1ull << lane) - 1))) * MJ_ROWS;
+            for (int j = 0; j < cnt; ++j)
+                rec[j] = s_pairs[tid][j] | (j == 0 ? tid << 16 : j == 1 ? cnt << 16 : 0);
+            if (cnt == 1) rec[1] = 1 << 16;
+        }
+        if (tid >= total && tid < 64) {
+            a.srec[tid * MJ_ROWS] = 0;
+            a.srec[tid * MJ_ROWS + 1] = 0;
+        }
+    }
 }
 
 bool route_supported(int H, int E, int k) {
@@ -613,7 +634,7 @@ hipError_t launch_route_logits(const RouteArgs& a, int H, hipStream_t st) {
 hipError_t launch_route_topk(const RouteArgs& a, hipStream_t st) {
     // one block: 16 waves with at most four rows each
     if (a.E < 1 || a.E > MJ_MAX_EXPERTS || a.k < 1 || a.k > 8 || a.k > a.E || a.M < 1 ||
-        a.M > 4 * RT_WAVES || a.M > MJ_ROWS)
+        a.M > 4 * RT_WAVES || a.M > MJ_ROWS || (a.srec && a.E > 64))
         return hipErrorInvalidValue;
     if (a.E <= 64)
         hipLaunchKernelGGL(k_route_topk<1>, dim3(1), dim3(64 * RT_WAVES), 0, st, a);

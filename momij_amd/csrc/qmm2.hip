@@ -415,7 +415,8 @@ hipError_t launch_gather(const GatherArgs& a, int epi, int max_rows_per_bucket, 
                          hipStream_t st) {
     if (gather3_supported(epi, a.K, a.N, a.gs))
         return launch_gather3(a, epi, max_rows_per_bucket, n_buckets_max, st);
-    if (a.ecnt != nullptr) return hipErrorInvalidValue;  // expert mode is the tile kernel's
+    if (a.ecnt != nullptr || a.srec != nullptr)  // expert modes are the tile kernel's
+        return hipErrorInvalidValue;
     // generic fallback (any K % 256 == 0, N % 16 == 0): K inside each wave, RG row groups
     const int rows = max_rows_per_bucket;
     const int rg = rows <= 4 ? 1 : (rows <= 8 ? 2 : 4);
