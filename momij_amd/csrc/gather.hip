@@ -53,8 +53,10 @@ struct G5Shape {
     // K-slice partials: in a wave's own tile area when every bucket is one pass, else in their
     // own region (later passes reuse the tiles)
     static constexpr int RED = (KS - 1) * TPB * 64 * 16;
-    __host__ __device__ static size_t lds(int RA, bool multi) {
-        return (size_t)WPB * WAVE_BYTES + (size_t)RA * XS * 2 + (size_t)RA * SS * 8 +
+    // dbl: two sets of staged rows (persistent mode stages the next item's while this one
+    // finishes)
+    __host__ __device__ static size_t lds(int RA, bool multi, bool dbl = false) {
+        return (size_t)WPB * WAVE_BYTES + (dbl ? 2 : 1) * ((size_t)RA * XS * 2 + (size_t)RA * SS * 8) +
                (EPI == EPI_QKV ? (size_t)R * ES * 4 : 0) + (multi ? RED : 0);
     }
 };
@@ -100,8 +102,16 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// Workgroup barrier that leaves vector-memory loads in flight: for LDS written with ds_write
+// only (the next item's weight stream keeps landing meanwhile, in LDS nobody reads here).
+__device__ __forceinline__ void lds_only_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false>
-__global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int multi) {
+// four waves per SIMD: two 8-wave blocks (or one 16-wave block) per CU
+__global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gather5(
+    GatherArgs a, int RA, int multi) {
     using S = G5Shape<KPL, GS, EPI, WPB, KS>;
     constexpr int R = S::R, K = S::K, KB = S::KB, KBW = S::KBW, TPB = S::TPB, XS = S::XS;
     constexpr int ES = S::ES, SCW = S::SCW;
@@ -159,22 +169,29 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
     char* wcode = wreg;
     uint16_t* wsc = (uint16_t*)(wreg + S::WCODE);          // [16][K/GS/KS] this K-slice
     uint16_t* wbi = (uint16_t*)(wreg + S::WCODE + S::WSB);
-    uint16_t* xs = (uint16_t*)(g5lds + (size_t)WPB * S::WAVE_BYTES);  // [RA][XS] qx rows
-    float2* xsl = (float2*)(xs + RA * XS);                 // [RA][SS] {sum x, sum base*x}
-    float* el = (float*)(xsl + RA * S::SS);                // [R][ES] QKV epilogue staging
-    char* red = (char*)el + (EPI == EPI_QKV ? R * ES * 4 : 0);  // [KS-1][TPB][64] f4 (multi)
-    __shared__ int s_pair[R];
+    // staged rows: one set, two in persistent mode (set buf serves the current item)
+    constexpr int NBUF = PER ? 2 : 1;
+    uint16_t* const xs0 = (uint16_t*)(g5lds + (size_t)WPB * S::WAVE_BYTES);  // [RA][XS] qx rows
+    float2* const xsl0 = (float2*)(xs0 + NBUF * RA * XS);  // [RA][SS] {sum x, sum base*x}
+    float* el = (float*)(xsl0 + NBUF * RA * S::SS);        // [R][ES] QKV epilogue staging
+    char* red = (char*)el + (EPI == EPI_QKV ? R * ES * 4 : 0);  // [KS-1][TPB][64] f4
+    __shared__ int s_pair[NBUF][R];
+    int buf = 0;
+    auto xs_of = [&](int b) { return xs0 + b * RA * XS; };
+    auto xsl_of = [&](int b) { return xsl0 + b * RA * S::SS; };
 
     // ---- activation rows of a pass, straight into LDS: rows < npass only (the rest feed
     // MFMA output rows that are discarded).  Wave w stages rows w, w + WPB, ...
-    auto stage_load = [&](int pb, int npass) {
-        const int myr = min(pb + (lane < R ? lane : 0), np - 1);
-        const int prl = (PER || a.ecnt) ? __shfl(lpair, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
+    auto stage_load = [&](int pb, int npass, int b, int lp, int npp) {
+        uint16_t* xs = xs_of(b);
+        float2* xsl = xsl_of(b);
+        const int myr = min(pb + (lane < R ? lane : 0), npp - 1);
+        const int prl = (PER || a.ecnt) ? __shfl(lp, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
 #pragma unroll
         for (int j = 0; j < R / WPB; ++j) {
             const int r = wv + WPB * j;
             const int pr = __builtin_amdgcn_readlane(prl, r);
-            if (lane == 0) s_pair[r] = pr;
+            if (lane == 0) s_pair[b][r] = pr;
             if (r < npass) {
                 const char* src = (const char*)(a.xperm + (size_t)(pr / a.x_div) * K);
 #pragma unroll
@@ -188,6 +205,8 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
     };
     // {sum x, sum base*x} of each (row, 64-block) from the staged rows (fixed order)
     auto own_block_sums = [&](int npass) {
+        const uint16_t* xs = xs_of(buf);
+        float2* xsl = xsl_of(buf);
         for (int idx = tid; idx < npass * KB; idx += NT) {
             const int r = idx % npass, b = idx / npass;
             const uint16_t* xr = xs + r * XS + 64 * b;
@@ -208,22 +227,18 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
         }
     };
 
-  for (;;) {
-    const int npass0 = min(RA, np);
-    stage_load(0, npass0);  // in flight ahead of the weight stream (loads return in issue order)
-
-    // ---- this wave's weight tile, coalesced into LDS
+    // ---- a wave's weight tile, coalesced into LDS: scales and biases, then the code groups
     const int I = a.N / 2;
-    auto tile_row = [&](int r) -> size_t {  // global row of tile row r
-        if constexpr (EPI == EPI_SWIGLU) {
-            const int j0 = (cb * TPB + tt) * 8;
-            return (size_t)e * a.N + (r < 8 ? j0 + r : I + j0 + r - 8);
-        } else {
-            return (size_t)e * a.N + (cb * TPB + tt) * 16 + r;
-        }
-    };
-    {
-        __builtin_amdgcn_sched_barrier(0);  // activation loads stay ahead in the vmcnt queue
+    auto issue_weights = [&](int ee, int cbb) {
+        auto tile_row = [&](int r) -> size_t {  // global row of tile row r
+            if constexpr (EPI == EPI_SWIGLU) {
+                const int j0 = (cbb * TPB + tt) * 8;
+                return (size_t)ee * a.N + (r < 8 ? j0 + r : I + j0 + r - 8);
+            } else {
+                return (size_t)ee * a.N + (cbb * TPB + tt) * 16 + r;
+            }
+        };
+        __builtin_amdgcn_sched_barrier(0);  // loads issued before stay ahead in the vmcnt queue
         const char* sg = (const char*)a.s;
         const char* bg = (const char*)a.b;
         if (lane < 16 * SCW) {
@@ -238,17 +253,28 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
             load_lds16(wg + tile_row(r) * (K / 4) + 16 * (kh * KBW + 4 * j + B4),
                        wcode + 1024 * j);
         __builtin_amdgcn_sched_barrier(0);
+    };
+    // persistent mode: from the second item on, a wave's weights were issued as soon as its
+    // MFMAs of the previous item were done (its tile is private to it), ahead of that item's
+    // reduction and epilogue; the item's rows are staged after the block is done with the old
+    // ones, so the item starts once everything it issued has landed
+    bool early = false;
+
+  for (;;) {
+    const int npass0 = min(RA, np);
+    if (!early) {
+        stage_load(0, npass0, buf, lpair, np);  // ahead of the weights (loads return in order)
+        issue_weights(e, cb);
     }
     const UnpackK uk = {opaque(0x00C000C0u), opaque(0x03000300u), opaque(0x4C004C00u),
                         opaque(0x44004400u)};
     const int xrow = min(n, RA - 1);
-    const uint16_t* xa = xs + xrow * XS + 16 * q;                 // A: activation row, quarter q
     const uint32_t* wq = (const uint32_t*)wcode + 16 * n + q;  // B: word q of row n's chunks
 
     auto run_pass = [&](int pb, int npass) {
         constexpr int G = KBW / 4;  // code column groups, issued after the two scale loads
         // every wave's staged rows visible (this wave's were issued before its weights)
-        if (pb == 0)
+        if (pb == 0 && !early)
             lds_barrier<G + 2>();
         else
             lds_barrier<0>();
@@ -277,7 +303,8 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
 #pragma unroll
         for (int c = 0; c < 4; ++c) corr[c] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
         const bool hiq = q >= 2, bterm = (q & 1) == 0;
-        const float* xcs = (const float*)(xsl + xrow * S::SS + kh * KBW + (q >> 1)) + (q & 1);
+        const float* xcs =
+            (const float*)(xsl_of(buf) + xrow * S::SS + kh * KBW + (q >> 1)) + (q & 1);
 #pragma unroll
         for (int i = 0; i < KBW / 2; ++i) {
             const float xa_k = xcs[4 * i];  // block 2i + q/2
@@ -291,8 +318,13 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
             corr[i & 3] = mfma16x16x4f32(xa_k, wk, corr[i & 3]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        const uint16_t* xak = xa + 64 * kh * KBW;  // this K-slice's activations
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // A: activation row xrow, quarter q, of this K-slice
+        const uint16_t* xak = xs_of(buf) + xrow * XS + 16 * q + 64 * kh * KBW;
+        // the correction chain's sum starts the accumulator (its four partial chains are
+        // then free)
+        float acc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = (corr[0][r] + corr[1][r]) + (corr[2][r] + corr[3][r]);
         // sum_B s_B * (sum q x)_B: per 64-block f16 MFMA sums, scaled in fp32, one column group
         // at a time as its codes arrive
 #pragma unroll
@@ -306,39 +338,64 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
             if (j == 6) wait_vmcnt<(G >= 7 ? G - 7 : 0) + PF>();
             if (j == 7) wait_vmcnt<PF>();
             __builtin_amdgcn_sched_barrier(0);
+            // LDS operands two blocks at a time (2 code words, 4 activation fragments), both
+            // blocks' requested before the first is used
 #pragma unroll
-            for (int B = 4 * j; B < 4 * j + 4; ++B) {  // block kh * KBW + B
-                // word q of chunk slot 64 (B / 4) + 4n + ((B % 4) ^ (n / 4))
-                const uint32_t word = wq[256 * (B / 4) + 4 * ((B & 3) ^ (n >> 2))];
+            for (int B2 = 4 * j; B2 < 4 * j + 4; B2 += 2) {
+                uint32_t wd[2];
+                u4v xv[2][2];
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    // word q of chunk slot 64 j + 4n + ((B % 4) ^ (n / 4)), B = B2 + b
+                    wd[b] = wq[256 * j + 4 * (((B2 + b) & 3) ^ (n >> 2))];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        xv[b][h] = *(const u4v*)(xak + 64 * (B2 + b) + 8 * h);
+                }
+#pragma unroll
+              for (int b = 0; b < 2; ++b) {  // block kh * KBW + B
+                const int B = B2 + b;
                 uint32_t v[8];
-                unpack16k(word, v, uk);
+                unpack16k(wd[b], v, uk);
                 f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    const u4v av = *(const u4v*)(xak + 64 * B + 8 * h);
                     const u4v bq = {v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
-                    d = mfma16x16x32(as_h8(av), as_h8(bq), d);
+                    d = mfma16x16x32(as_h8(xv[b][h]), as_h8(bq), d);
                 }
                 const int g = B * 64 / GS;
                 const uint32_t sw = opaque(sv[g / 8][(g % 8) / 2]);
                 const float sc = h2f((uint16_t)(sw >> (16 * (g & 1))));
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[r] += sc * d[r];
+              }
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) pin(acc[r]);
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] += (corr[0][r] + corr[1][r]) + (corr[2][r] + corr[3][r]);
+        if constexpr (PER) {
+            // last pass of the item: this wave's tile is free, start the next item's weights
+            const int nx = item + (int)gridDim.x;
+            const int np_next = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
+            if (pb + RA >= np && nx / ncb < 64 && np_next > 0) {
+                issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16, nx % ncb);
+                // and its rows, into the other set (its last reader finished an item ago)
+                stage_load(0, min(RA, np_next), buf ^ 1, rec_n & 0xFFFF, np_next);
+            }
+        }
         if constexpr (KS > 1) {
             // K-slices of a tile meet in LDS (a slice's partial goes into its own wave's tile
             // area, free once its MFMAs are done); slice 0 adds them in slice order
             auto slot = [&](int k2) -> f4* {
-                return (f4*)(multi ? red + ((k2 - 1) * TPB + tt) * 1024
-                                   : g5lds + (size_t)(k2 * TPB + tt) * S::WAVE_BYTES) + lane;
+                return (f4*)((multi || PER) ? red + ((k2 - 1) * TPB + tt) * 1024
+                                            : g5lds + (size_t)(k2 * TPB + tt) * S::WAVE_BYTES) +
+                       lane;
             };
             if (kh > 0) *slot(kh) = (f4){acc[0], acc[1], acc[2], acc[3]};
-            lds_barrier<0>();
+            if (PER)
+                lds_only_barrier();
+            else
+                lds_barrier<0>();
             if (kh == 0) {
 #pragma unroll
                 for (int k2 = 1; k2 < KS; ++k2) {
@@ -361,7 +418,7 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
                     up = fminf(fmaxf(up, -7.0f), 7.0f);
                     const float act = hround(g / (1.0f + expf(-g)) * up);
                     const int j = (cb * TPB + tt) * 8 + n;
-                    a.y[(size_t)s_pair[i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
+                    a.y[(size_t)s_pair[buf][i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
                 }
             }
         } else if constexpr (EPI == EPI_QKV) {
@@ -420,7 +477,7 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
             for (int r = 0; r < 4; ++r) {
                 const int i = 4 * q + r;
                 if (kh == 0 && i < npass) {
-                    uint16_t* yp = a.y + (size_t)s_pair[i] * a.N + col;
+                    uint16_t* yp = a.y + (size_t)s_pair[buf][i] * a.N + col;
                     if constexpr (EPI == EPI_ADD)
                         *yp = f2h(h2f(*yp) + hround(acc[r]));
                     else
@@ -434,7 +491,7 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
     for (int pb = RA; pb < np; pb += RA) {
         __syncthreads();  // the previous pass is done with LDS
         const int npass = min(RA, np - pb);
-        stage_load(pb, npass);
+        stage_load(pb, npass, buf, lpair, np);
         run_pass(pb, npass);
     }
     if constexpr (!PER) break;
@@ -442,10 +499,11 @@ __global__ __launch_bounds__(WPB * 64) void k_gather5(GatherArgs a, int RA, int 
     if (item / ncb >= 64) break;
     np = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
     if (np <= 0) break;
-    __syncthreads();  // this item is done with LDS
     e = __builtin_amdgcn_readlane(rec_n, 0) >> 16;
     cb = item % ncb;
     lpair = rec_n & 0xFFFF;
+    buf ^= 1;
+    early = true;
   }
 }
 
@@ -476,12 +534,12 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     const bool expert = a.ecnt != nullptr || a.srec != nullptr;
     const size_t limit =
         (EPI == EPI_SWIGLU || EPI == EPI_STORE) && expert ? 80 * 1024 - 256 : G5_LDS_MAX;
-    while (RA > 1 && S::lds(RA, want > RA) > limit) --RA;
+    while (RA > 1 && S::lds(RA, want > RA || PER, PER) > limit) --RA;
     const bool multi = want > RA;
     int grid = n_buckets * ncb;
     if (PER && grid > persistent_blocks()) grid = persistent_blocks();
     launch_timed(k_gather5<KPL, GS, EPI, WPB, KS, PER>, dim3(grid), dim3(WPB * 64),
-                 S::lds(RA, multi), st, a, RA, (int)multi);
+                 S::lds(RA, multi || PER, PER), st, a, RA, (int)multi);
     return hipGetLastError();
 }
 
