@@ -99,7 +99,9 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     uint16_t* Vt = Ks + AK * QSTR;               // [HD][VSTR]
     uint16_t* Ps = Vt + HD * VSTR;               // [4 waves][16][VSTR]
     int64_t* kpos = (int64_t*)(Ps + 4 * 16 * VSTR);
-    int* ktree = (int*)(kpos + AK);
+    int64_t* rlo = kpos + AK;                    // [MJ_ROWS] first key position of a row's window
+    uint64_t* ranc = (uint64_t*)(rlo + MJ_ROWS);  // [MJ_ROWS] ancestor masks
+    int* ktree = (int*)(ranc + MJ_ROWS);
     int* s_abort = ktree + AK;
 
     // Every load of the block is issued before the first wait: this thread's K/V quarter row
@@ -138,6 +140,11 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
         }
         kpos[t] = pos;
         ktree[t] = tree;
+    }
+    // the rows' window starts and ancestor masks, fetched with everything else
+    if (t < a.M) {
+        rlo[t] = a.window > 0 ? L + sd->depth[t] - a.window + 1 : INT64_MIN;
+        ranc[t] = sd->anc[t];
     }
     // Q rows of this kv group: qv = r * gqa + j  <-  head g*gqa + j of row r; four 16-byte
     // parts per thread per round
@@ -198,8 +205,8 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const int qv = qt * 16 + 4 * lq + r;
                 const int row = qv < nqv ? qv / gqa : 0;
-                const int64_t lo_r = a.window > 0 ? L + sd->depth[row] - a.window + 1 : INT64_MIN;
-                const uint64_t anc = sd->anc[row];
+                const int64_t lo_r = rlo[row];
+                const uint64_t anc = ranc[row];
 #pragma unroll
                 for (int kt = 0; kt < 4; ++kt) {
                     const int kk = 16 * kt + ln;
@@ -328,10 +335,11 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
 }
 
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
+    if (a.M < 1 || a.M > MJ_ROWS) return hipErrorInvalidValue;  // row metadata is staged per row
     const int gqa = a.nQ / a.nKV;
     const int nqt = (a.M * gqa + 15) / 16;
     const size_t lds = (size_t)(nqt * 16 * QSTR + AK * QSTR + HD * VSTR + 4 * 16 * VSTR) * 2 +
-                       AK * (8 + 4) + 16;
+                       AK * (8 + 4) + MJ_ROWS * 16 + 16;
     launch_timed(k_attn_chunk, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -302,19 +302,27 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         f4 corr[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) corr[c] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-        const bool hiq = q >= 2, bterm = (q & 1) == 0;
         const float* xcs =
             (const float*)(xsl_of(buf) + xrow * S::SS + kh * KBW + (q >> 1)) + (q & 1);
+        // this lane's B values: the biases (term 0) or the negated scales (term 1), taken from
+        // the fp16 half of block 2i + q/2's group (the sign flipped in the fp16 bits)
+        const uint32_t sgn = (q & 1) ? 0x8000u : 0u;
+        const uint32_t hsh = 16u * (uint32_t)(q >> 1);
+        u4v mv[SCW];
+#pragma unroll
+        for (int c = 0; c < SCW; ++c)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) mv[c][w] = (q & 1) ? sv[c][w] : bv[c][w];
 #pragma unroll
         for (int i = 0; i < KBW / 2; ++i) {
             const float xa_k = xcs[4 * i];  // block 2i + q/2
-            const int g0 = (2 * i) * 64 / GS, g1 = (2 * i + 1) * 64 / GS;
-            const uint32_t s0 = (sv[g0 / 8][(g0 % 8) / 2] >> (16 * (g0 & 1))) & 0xFFFFu;
-            const uint32_t s1 = (sv[g1 / 8][(g1 % 8) / 2] >> (16 * (g1 & 1))) & 0xFFFFu;
-            const uint32_t b0 = (bv[g0 / 8][(g0 % 8) / 2] >> (16 * (g0 & 1))) & 0xFFFFu;
-            const uint32_t b1 = (bv[g1 / 8][(g1 % 8) / 2] >> (16 * (g1 & 1))) & 0xFFFFu;
-            const uint32_t sb = hiq ? s1 : s0, bb = hiq ? b1 : b0;
-            const float wk = bterm ? h2f((uint16_t)bb) : -h2f((uint16_t)sb);
+            uint32_t h;
+            if constexpr (GS == 64) {  // group 2i + q/2: word i % 4 of chunk 2i / 8, half q/2
+                h = mv[(2 * i) / 8][i % 4] >> hsh;
+            } else {  // group i
+                h = mv[i / 8][(i % 8) / 2] >> (16 * (i & 1));
+            }
+            const float wk = h2f((uint16_t)(h ^ sgn));
             corr[i & 3] = mfma16x16x4f32(xa_k, wk, corr[i & 3]);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -407,17 +415,21 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         }
         // lane (n, q) now holds the outputs of activation rows 4q .. 4q+3 for weight row n
         if constexpr (EPI == EPI_SWIGLU) {
+            // up row n < 8 pairs with gate row n + 8: lanes n < 8 finish rows 4q, 4q + 1 and
+            // lanes n + 8 rows 4q + 2, 4q + 3, each taking the other half of its pair by a swap
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float gate_raw = __shfl_xor(acc[r], 8, MJ_WAVE);
+            for (int rr = 0; rr < 2; ++rr) {
+                const bool lo = n < 8;
+                const float recv = __shfl_xor(lo ? acc[rr + 2] : acc[rr], 8, MJ_WAVE);
+                const int r = lo ? rr : rr + 2;
                 const int i = 4 * q + r;
-                if (kh == 0 && n < 8 && i < npass) {
-                    float up = hround(acc[r]);
-                    float g = hround(gate_raw);
+                if (kh == 0 && i < npass) {
+                    float up = hround(lo ? acc[rr] : recv);
+                    float g = hround(lo ? recv : acc[rr + 2]);
                     g = fminf(g, 7.0f);
                     up = fminf(fmaxf(up, -7.0f), 7.0f);
                     const float act = hround(g / (1.0f + expf(-g)) * up);
-                    const int j = (cb * TPB + tt) * 8 + n;
+                    const int j = (cb * TPB + tt) * 8 + (n & 7);
                     a.y[(size_t)s_pair[buf][i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
                 }
             }
