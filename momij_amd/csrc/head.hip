@@ -50,26 +50,48 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
         bv[tl] = -INFINITY;
         bi[tl] = 0x7fffffff;
     }
-    for (int strip = blockIdx.x * 8 + wv; strip < nstrips; strip += TW) {
+    // The wave's strips are one stream of 8-chunk pieces (16 rows x 256 k, 8 KB): the next
+    // piece (of this strip or the next) is requested before the current one is multiplied, so
+    // a wave always has a piece in flight.
+    const int NC = K / 256;  // pieces per strip
+    auto row_ptr = [&](int strip) {
+        const int vr = strip * 16 + ln;
+        return (const u4v*)(a.w + (size_t)(vr < a.V ? vr : a.V - 1) * K) + lq;
+    };
+    int strip = blockIdx.x * 8 + wv;
+    u4v cur[8];
+    if (strip < nstrips) {
+        const u4v* wr = row_ptr(strip);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cur[u] = wr[4 * u];
+    }
+    for (; strip < nstrips; strip += TW) {
         const int v0 = strip * 16;
-        const int vr = v0 + ln;
-        const u4v* wr = (const u4v*)(a.w + (size_t)(vr < a.V ? vr : a.V - 1) * K) + lq;
         f4 acc[NT];
 #pragma unroll
         for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s0 = 0; s0 < K / 32; s0 += 8) {
-            u4v av[8];
+        for (int pc = 0; pc < NC; ++pc) {
+            // the piece after this one: pc + 1 of this strip, or piece 0 of the next strip
+            const int nstrip = pc + 1 < NC ? strip : strip + TW;
+            const int npc = pc + 1 < NC ? pc + 1 : 0;
+            u4v nxt[8];
+            if (nstrip < nstrips) {
+                const u4v* wn = row_ptr(nstrip) + 4 * 8 * npc;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) av[u] = wr[4 * (s0 + u)];
+                for (int u = 0; u < 8; ++u) nxt[u] = wn[4 * u];
+            }
+            const int s0 = 8 * pc;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
 #pragma unroll
                 for (int tl = 0; tl < NT; ++tl) {
                     const u4v xb =
                         *(const u4v*)(xs + (tl * 16 + ln) * XS + 32 * (s0 + u) + 8 * lq);
-                    acc[tl] = mfma16x16x32(as_h8(av[u]), as_h8(xb), acc[tl]);
+                    acc[tl] = mfma16x16x32(as_h8(cur[u]), as_h8(xb), acc[tl]);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
         }
         // lane holds logits for vocab v0 + 4*lq + r, row tl*16 + ln
 #pragma unroll
@@ -161,16 +183,30 @@ __global__ __launch_bounds__(64) void k_head_final(const float* pval, const int*
     }
 }
 
-int head_blocks() { return 256; }
+// two 512-thread blocks per CU (the staged rows take at most 66 KB of LDS each)
+int head_blocks() {
+    static int nb = 0;
+    if (nb == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        nb = 2 * cus;
+    }
+    return nb;
+}
 
 // Rows go through in groups of <= 32 (two 16-row MFMA tiles staged in LDS per group).
 hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, int V,
                           const int32_t* banned, int n_banned, float* logits, float* pval,
                           int* pidx, int32_t* out_idx, float* out_max, const int* abort,
                           hipStream_t st) {
-    const int nb = head_blocks();
+    if (K % 256 != 0 || M < 1) return hipErrorInvalidValue;  // 256-k pieces
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mg = M - m0 < 32 ? M - m0 : 32;
+        // two blocks per CU for one 16-row tile; a 32-row group's LDS allows one
+        const int nb = mg <= 16 ? head_blocks() : head_blocks() / 2;
         HeadArgs a{x + (size_t)m0 * K, w, mg, K, V, banned, n_banned,
                    logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
         if (mg <= 16) {
