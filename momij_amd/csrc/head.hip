@@ -42,7 +42,6 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
     __syncthreads();
     const int ln = lane & 15, lq = lane >> 4;
     const int nstrips = (a.V + 15) / 16;
-    const int TW = gridDim.x * 8;
     float bv[NT];
     int bi[NT];
 #pragma unroll
@@ -50,48 +49,78 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
         bv[tl] = -INFINITY;
         bi[tl] = 0x7fffffff;
     }
-    // The wave's strips are one stream of 8-chunk pieces (16 rows x 256 k, 8 KB): the next
-    // piece (of this strip or the next) is requested before the current one is multiplied, so
-    // a wave always has a piece in flight.
-    const int NC = K / 256;  // pieces per strip
-    auto row_ptr = [&](int strip) {
+    // Work unit: one K half of a 16-row strip.  Wave (slot, h) of a block takes half h of
+    // strips blockIdx.x * 4 + slot + round * gridDim.x * 4; the h = 1 partial meets the h = 0
+    // one in LDS (two slot sets by round parity), so twice as many units as strips keep the
+    // waves' loads even.  A wave's halves are one stream of pieces of PL 32-k chunks (16 rows x
+    // 256 k, 8 KB, when K / 2 allows): the next piece is requested before the current one is
+    // multiplied.
+    const int slot = wv & 3, h = wv >> 2;
+    const int PL = (K / 64) % 8 == 0 ? 8 : 4;  // chunks per piece (K % 256 == 0)
+    const int NH = K / 64 / PL;                // pieces per half strip
+    const int SW = gridDim.x * 4;
+    const int rounds = (nstrips - (int)blockIdx.x * 4 + SW - 1) / SW;  // of this block's slot 0
+    auto piece_ptr = [&](int strip, int pc) {
         const int vr = strip * 16 + ln;
-        return (const u4v*)(a.w + (size_t)(vr < a.V ? vr : a.V - 1) * K) + lq;
+        return (const u4v*)(a.w + (size_t)(vr < a.V ? vr : a.V - 1) * K) + lq +
+               4 * PL * (h * NH + pc);
     };
-    int strip = blockIdx.x * 8 + wv;
+    // h = 1 partials: two sets by round parity for one tile; one set for two tiles (their rows
+    // take most of the LDS), reused after a barrier
+    constexpr int NPB = NT == 1 ? 2 : 1;
+    __shared__ f4 s_part[NPB][4][NT][64];
+    int strip = blockIdx.x * 4 + slot;
     u4v cur[8];
     if (strip < nstrips) {
-        const u4v* wr = row_ptr(strip);
+        const u4v* wr = piece_ptr(strip, 0);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) cur[u] = wr[4 * u];
+        for (int u = 0; u < 8; ++u)
+            if (u < PL) cur[u] = wr[4 * u];
     }
-    for (; strip < nstrips; strip += TW) {
+    for (int rd = 0; rd < rounds; ++rd, strip += SW) {
+        if (NPB == 1 && rd > 0) __syncthreads();  // the previous round's partials were read
+        const bool live = strip < nstrips;  // same for both halves of a strip
         const int v0 = strip * 16;
         f4 acc[NT];
 #pragma unroll
         for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-        for (int pc = 0; pc < NC; ++pc) {
-            // the piece after this one: pc + 1 of this strip, or piece 0 of the next strip
-            const int nstrip = pc + 1 < NC ? strip : strip + TW;
-            const int npc = pc + 1 < NC ? pc + 1 : 0;
-            u4v nxt[8];
-            if (nstrip < nstrips) {
-                const u4v* wn = row_ptr(nstrip) + 4 * 8 * npc;
+        if (live) {
+            for (int pc = 0; pc < NH; ++pc) {
+                // the piece after this one: pc + 1 of this half, or piece 0 of the next round's
+                const int nstrip = pc + 1 < NH ? strip : strip + SW;
+                u4v nxt[8];
+                if (nstrip < nstrips) {
+                    const u4v* wn = piece_ptr(nstrip, pc + 1 < NH ? pc + 1 : 0);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) nxt[u] = wn[4 * u];
-            }
-            const int s0 = 8 * pc;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-#pragma unroll
-                for (int tl = 0; tl < NT; ++tl) {
-                    const u4v xb =
-                        *(const u4v*)(xs + (tl * 16 + ln) * XS + 32 * (s0 + u) + 8 * lq);
-                    acc[tl] = mfma16x16x32(as_h8(cur[u]), as_h8(xb), acc[tl]);
+                    for (int u = 0; u < 8; ++u)
+                        if (u < PL) nxt[u] = wn[4 * u];
                 }
-            }
+                const int s0 = PL * (h * NH + pc);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+                for (int u = 0; u < 8; ++u) {
+                    if (u >= PL) break;
+#pragma unroll
+                    for (int tl = 0; tl < NT; ++tl) {
+                        const u4v xb =
+                            *(const u4v*)(xs + (tl * 16 + ln) * XS + 32 * (s0 + u) + 8 * lq);
+                        acc[tl] = mfma16x16x32(as_h8(cur[u]), as_h8(xb), acc[tl]);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+            }
+            if (h == 1) {
+#pragma unroll
+                for (int tl = 0; tl < NT; ++tl) s_part[rd % NPB][slot][tl][lane] = acc[tl];
+            }
+        }
+        __syncthreads();  // the h = 1 halves are in LDS
+        if (!live || h == 1) continue;
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl) {
+            const f4 o = s_part[rd % NPB][slot][tl][lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[tl][r] += o[r];
         }
         // lane holds logits for vocab v0 + 4*lq + r, row tl*16 + ln
 #pragma unroll
@@ -202,7 +231,7 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
                           const int32_t* banned, int n_banned, float* logits, float* pval,
                           int* pidx, int32_t* out_idx, float* out_max, const int* abort,
                           hipStream_t st) {
-    if (K % 256 != 0 || M < 1) return hipErrorInvalidValue;  // 256-k pieces
+    if (K % 256 != 0 || M < 1) return hipErrorInvalidValue;  // two halves of 128-k multiples
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mg = M - m0 < 32 ? M - m0 : 32;
         // two blocks per CU for one 16-row tile; a 32-row group's LDS allows one
@@ -214,6 +243,7 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
             launch_timed(k_lm_head<1>, dim3(nb), dim3(512), lds, st, a);
         } else {
             const size_t lds = (size_t)32 * (K + 8) * 2;
+            if (lds > 140 * 1024) return hipErrorInvalidValue;  // K <= 2232 for 17..32 rows
             launch_timed(k_lm_head<2>, dim3(nb), dim3(512), lds, st, a);
         }
         hipError_t e = hipGetLastError();
@@ -374,10 +404,10 @@ hipError_t set_kernel_attributes() {
     static bool done = false;
     if (done) return hipSuccess;
     hipError_t e = hipFuncSetAttribute((const void*)k_lm_head<1>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
     if (e == hipSuccess)
         e = hipFuncSetAttribute((const void*)k_lm_head<2>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
     if (e == hipSuccess) e = set_gather3_attributes();
     if (e == hipSuccess) done = true;
