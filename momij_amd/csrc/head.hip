@@ -197,13 +197,21 @@ __global__ __launch_bounds__(64) void k_head_final(const float* pval, const int*
     if (m >= M) return;
     float b = -INFINITY;
     int i = 0x7fffffff;
-    for (int k = lane; k < nblk; k += 64) {
-        const float v = pval[(size_t)k * 32 + m];
-        const int j = pidx[(size_t)k * 32 + m];
-        if (v > b || (v == b && j < i)) {
-            b = v;
-            i = j;
+    for (int k0 = 0; k0 < nblk; k0 += 8 * 64) {  // eight partials a lane requested together
+        float v[8];
+        int j[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int k = k0 + 64 * u + lane;
+            v[u] = k < nblk ? pval[(size_t)k * 32 + m] : -INFINITY;
+            j[u] = k < nblk ? pidx[(size_t)k * 32 + m] : 0x7fffffff;
         }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (v[u] > b || (v[u] == b && j[u] < i)) {
+                b = v[u];
+                i = j[u];
+            }
     }
     wave_argmax(b, i);
     if (lane == 0) {
