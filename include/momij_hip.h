@@ -151,6 +151,18 @@ mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, in
                             const int32_t* banned, int n_banned, int32_t* out_argmax,
                             float* out_max, float* out_logits);
 
+/* lm_head verify over the Maple checkpoint's 4-bit head -- maple_lm_head_argmax/reduce
+ * (SeedlessMetal.swift:3005-3111, bound by SeedlessDecodeEngine.swift:481-498 when head_bits
+ * is 4, SeedlessDecodeEngine.swift:144): logits[m][v] = sum_k (q[v][k] s[v][k/64] +
+ * b[v][k/64]) x[m][k] (fp32), argmax per row with the lowest id winning ties and banned ids
+ * skipped.  w uint32 [V][K/8] (8 codes a word, LSB first), scales/biases fp16 [V][K/64],
+ * x fp16 [M][K]; group_size must be 64 and K a multiple of 512 (K <= 4096, <= 2048 for
+ * M > 16); all four operands 16-byte aligned.  Outputs as mj_lm_head_verify. */
+mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const void* scales,
+                               const void* biases, int M, int K, int V, int group_size,
+                               const int32_t* banned, int n_banned, int32_t* out_argmax,
+                               float* out_max, float* out_logits);
+
 /* Greedy acceptance -- verifyDraftChain (SeedlessDecodeEngine.swift:1574-1603) generalised to
  * a tree: from row 0 step to the lowest-index child whose token equals the current row's
  * argmax; stop when none does.  tokens/argmax int32 [n_rows] device, parents_host as above.

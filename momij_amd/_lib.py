@@ -80,6 +80,8 @@ _SIGS = {
     "mj_attn_block": (i32, [vp, C.POINTER(AttnConfig), C.POINTER(AttnWeights), vp, vp, vp, i64,
                             vp, i32]),
     "mj_lm_head_verify": (i32, [vp, vp, vp, i32, i32, i32, vp, i32, vp, vp, vp]),
+    "mj_lm_head_verify_q4": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp,
+                                   vp]),
     "mj_accept_greedy": (i32, [vp, vp, vp, vp, i32, vp]),
     "mj_accept_sampled": (i32, [vp, vp, i32, i32, vp, f32, i32, vp, u64, u64, vp]),
     "mj_model_create": (i32, [vp, C.POINTER(ModelConfig), vp, vp, vp, vp, C.POINTER(vp)]),

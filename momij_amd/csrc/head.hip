@@ -188,6 +188,202 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// The Maple head: maple_lm_head_argmax (SeedlessMetal.swift:3005-3068) over its 4-bit affine
+// weight -- w uint32 [V][K/8] (8 codes a word, LSB first), scale / bias fp16 [V][K/64];
+// logits[m][v] = sum_k (q s + b) x[m][k].  Same partials as k_lm_head (lowest id on ties,
+// banned ids skipped), folded by k_head_final.
+//
+// One 512-thread block per CU (two for <= 16 rows); wave w takes 16-row vocab strips
+// blockIdx.x * 8 + w + i * 8 * gridDim.x.  MFMA: A = 16 hidden rows x 32 k (staged in LDS), B =
+// the strip's codes: lane (n, q) holds row n's words 8g + 2q, 8g + 2q + 1 of 64-group g, each
+// widened to fp16 16 + q by the 2-bit gather's shift-and-or (nibble pairs (j, j + 4) per
+// word), so the hidden rows are staged with each 8-block in the order 0 4 1 5 2 6 3 7.  Per
+// group: s_g times the two MFMAs' sum; the remainder sum_g (b_g - 16 s_g) X_g (X_g the group
+// sum of a hidden row) is an fp32 MFMA chain.  A strip streams as four 8-group pieces, the
+// next requested before the current one is multiplied.
+struct HeadQ4Args {
+    const uint16_t* x;   // [M][K] fp16
+    const uint32_t* w;   // [V][K/8]
+    const uint16_t* s;   // [V][K/64]
+    const uint16_t* b;
+    int M, K, V;
+    const int32_t* banned;
+    int n_banned;
+    float* logits;       // [M][V] or nullptr
+    float* pval;         // [blocks][32]
+    int* pidx;
+    const int* abort;
+};
+
+__device__ __forceinline__ void unpack8k(uint32_t w, u4v& o) {
+    // nibble pairs (j, j + 4) of the word into fp16 16 + q: shift to bits 6..9 of each half
+    const uint32_t m = 0x03C003C0u, c = 0x4C004C00u;
+    o[0] = ((w << 6) & m) | c;
+    o[1] = ((w << 2) & m) | c;
+    o[2] = ((w >> 2) & m) | c;
+    o[3] = ((w >> 6) & m) | c;
+}
+
+template <int NT>
+__global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
+    if (aborted(a.abort)) return;
+    extern __shared__ __align__(16) char q4lds[];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int K = a.K, XS = K + 8, G = K / 64, GS1 = G + 1;
+    uint16_t* xs = (uint16_t*)q4lds;                 // [NT*16][XS], 8-blocks as 0 4 1 5 2 6 3 7
+    float* xg = (float*)(xs + NT * 16 * XS);         // [NT*16][G + 1] group sums
+    for (int idx = t; idx < NT * 16 * (K / 8); idx += 512) {
+        const int m = idx / (K / 8), c = idx % (K / 8);
+        u4v v = {0u, 0u, 0u, 0u};
+        if (m < a.M) v = *(const u4v*)(a.x + (size_t)m * K + 8 * c);
+        u4v o;
+        o[0] = (v[0] & 0xFFFFu) | (v[2] << 16);
+        o[1] = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
+        o[2] = (v[1] & 0xFFFFu) | (v[3] << 16);
+        o[3] = (v[1] >> 16) | (v[3] & 0xFFFF0000u);
+        *(u4v*)(xs + m * XS + 8 * c) = o;
+    }
+    for (int idx = t; idx < NT * 16 * G; idx += 512) {
+        const int m = idx / G, g = idx % G;
+        float sum = 0.0f;
+        if (m < a.M)
+            for (int c = 0; c < 8; ++c) {
+                const u4v v = *(const u4v*)(a.x + (size_t)m * K + 64 * g + 8 * c);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sum += h2f(v[j] & 0xFFFFu) + h2f(v[j] >> 16);
+            }
+        xg[m * GS1 + g] = sum;
+    }
+    __syncthreads();
+
+    const int n = lane & 15, q = lane >> 4;
+    const int nstrips = (a.V + 15) / 16, TW = gridDim.x * 8, NP = G / 8;
+    float bv[NT][4];
+    int bi[NT][4];
+#pragma unroll
+    for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            bv[tl][r] = -INFINITY;
+            bi[tl][r] = 0x7fffffff;
+        }
+    // piece p of a strip: codes of groups 8p .. 8p+7 (words 8g + 2q, +1), their scales, biases
+    struct Piece {
+        uint32_t cw[8][2];
+        u4v sc, bs;
+    };
+    auto load_piece = [&](int strip, int p, Piece& pc) {
+        const int vr = min(strip * 16 + n, a.V - 1);
+        const uint32_t* wr = a.w + (size_t)vr * (K / 8) + 64 * p + 2 * q;
+#pragma unroll
+        for (int gg = 0; gg < 8; ++gg) {
+            const uint2 v = *(const uint2*)(wr + 8 * gg);
+            pc.cw[gg][0] = v.x;
+            pc.cw[gg][1] = v.y;
+        }
+        pc.sc = *(const u4v*)(a.s + (size_t)vr * G + 8 * p);
+        pc.bs = *(const u4v*)(a.b + (size_t)vr * G + 8 * p);
+    };
+    int strip = blockIdx.x * 8 + wv;
+    Piece cur;
+    if (strip < nstrips) load_piece(strip, 0, cur);
+    for (; strip < nstrips; strip += TW) {
+        const int v0 = strip * 16;
+        f4 acc[NT];
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int p = 0; p < NP; ++p) {
+            const int nstrip = p + 1 < NP ? strip : strip + TW;
+            Piece nxt;
+            if (nstrip < nstrips) load_piece(nstrip, p + 1 < NP ? p + 1 : 0, nxt);
+            // remainder sum_g (b_g - 16 s_g) X_g of the piece: groups 8p + 4u + q
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int gg = 4 * u + q;  // this lane's group of the chain step (per-lane half)
+                const uint32_t sw = cur.sc[gg >> 1] >> (16 * (gg & 1));
+                const uint32_t bw = cur.bs[gg >> 1] >> (16 * (gg & 1));
+                const float cg = h2f((uint16_t)bw) - 16.0f * h2f((uint16_t)sw);
+#pragma unroll
+                for (int tl = 0; tl < NT; ++tl)
+                    acc[tl] = mfma16x16x4f32(xg[(tl * 16 + n) * GS1 + 8 * p + gg], cg, acc[tl]);
+            }
+#pragma unroll
+            for (int gg = 0; gg < 8; ++gg) {
+                const int g = 8 * p + gg;
+                u4v b0, b1;
+                unpack8k(cur.cw[gg][0], b0);
+                unpack8k(cur.cw[gg][1], b1);
+                const float sg = h2f((uint16_t)(cur.sc[gg >> 1] >> (16 * (gg & 1))));
+#pragma unroll
+                for (int tl = 0; tl < NT; ++tl) {
+                    const uint16_t* xr = xs + (tl * 16 + n) * XS + 64 * g + 16 * q;
+                    f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+                    d = mfma16x16x32(as_h8(*(const u4v*)xr), as_h8(b0), d);
+                    d = mfma16x16x32(as_h8(*(const u4v*)(xr + 8)), as_h8(b1), d);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[tl][r] += sg * d[r];
+                }
+            }
+            cur = nxt;
+        }
+        // lane (n, q): hidden rows tl*16 + 4q + r, vocab row v0 + n
+        const int v = v0 + n;
+        bool keep = v < a.V;
+        for (int bb = 0; bb < a.n_banned; ++bb)
+            if (a.banned[bb] == v) keep = false;
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = tl * 16 + 4 * q + r;
+                const float val = acc[tl][r];
+                if (keep && (val > bv[tl][r] || (val == bv[tl][r] && v < bi[tl][r]))) {
+                    bv[tl][r] = val;
+                    bi[tl][r] = v;
+                }
+                if (a.logits && m < a.M && v < a.V) a.logits[(size_t)m * a.V + v] = val;
+            }
+    }
+    // across the 16 vocab lanes of a row group, then across waves
+#pragma unroll
+    for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const float ov = __shfl_xor(bv[tl][r], o, MJ_WAVE);
+                const int oi = __shfl_xor(bi[tl][r], o, MJ_WAVE);
+                if (ov > bv[tl][r] || (ov == bv[tl][r] && oi < bi[tl][r])) {
+                    bv[tl][r] = ov;
+                    bi[tl][r] = oi;
+                }
+            }
+    __shared__ float sv[8][32];
+    __shared__ int si[8][32];
+    if (n == 0) {
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sv[wv][tl * 16 + 4 * q + r] = bv[tl][r];
+                si[wv][tl * 16 + 4 * q + r] = bi[tl][r];
+            }
+    }
+    __syncthreads();
+    if (t < NT * 16 && t < a.M) {
+        float bb = sv[0][t];
+        int ii = si[0][t];
+        for (int w2 = 1; w2 < 8; ++w2)
+            if (sv[w2][t] > bb || (sv[w2][t] == bb && si[w2][t] < ii)) {
+                bb = sv[w2][t];
+                ii = si[w2][t];
+            }
+        a.pval[(size_t)blockIdx.x * 32 + t] = bb;
+        a.pidx[(size_t)blockIdx.x * 32 + t] = ii;
+    }
+}
+
 // One wave per row: fold the block partials (value, lowest id on ties).
 __global__ __launch_bounds__(64) void k_head_final(const float* pval, const int* pidx, int nblk,
                                                    int M, int32_t* out_idx, float* out_max,
@@ -408,6 +604,34 @@ hipError_t launch_hold(unsigned us, hipStream_t st) {
 hipError_t set_attn_attributes();
 hipError_t set_gather3_attributes();
 
+// Rows in groups of <= 32 as launch_lm_head; K % 512 == 0 (8-group pieces), K <= 4096.
+hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                             const uint16_t* b, int M, int K, int V, const int32_t* banned,
+                             int n_banned, float* logits, float* pval, int* pidx,
+                             int32_t* out_idx, float* out_max, const int* abort, hipStream_t st) {
+    if (K % 512 != 0 || K > 4096 || M < 1) return hipErrorInvalidValue;
+    for (int m0 = 0; m0 < M; m0 += 32) {
+        const int mg = M - m0 < 32 ? M - m0 : 32;
+        const int nt = mg <= 16 ? 1 : 2;
+        const size_t lds = (size_t)nt * 16 * (K + 8) * 2 + (size_t)nt * 16 * (K / 64 + 1) * 4;
+        if (lds > 140 * 1024) return hipErrorInvalidValue;
+        const int nb = nt == 1 ? head_blocks() : head_blocks() / 2;
+        HeadQ4Args qa{x + (size_t)m0 * K, w, s, b, mg, K, V, banned, n_banned,
+                      logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
+        if (nt == 1)
+            launch_timed(k_lm_head_q4<1>, dim3(nb), dim3(512), lds, st, qa);
+        else
+            launch_timed(k_lm_head_q4<2>, dim3(nb), dim3(512), lds, st, qa);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg,
+                           out_idx + m0, out_max ? out_max + m0 : nullptr, abort);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t set_kernel_attributes() {
     static bool done = false;
     if (done) return hipSuccess;
@@ -415,6 +639,12 @@ hipError_t set_kernel_attributes() {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
     if (e == hipSuccess)
         e = hipFuncSetAttribute((const void*)k_lm_head<2>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)k_lm_head_q4<1>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)k_lm_head_q4<2>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
     if (e == hipSuccess) e = set_gather3_attributes();

@@ -177,6 +177,10 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
                           const int32_t* banned, int n_banned, float* logits, float* pval,
                           int* pidx, int32_t* out_idx, float* out_max, const int* abort,
                           hipStream_t st);
+hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                             const uint16_t* b, int M, int K, int V, const int32_t* banned,
+                             int n_banned, float* logits, float* pval, int* pidx,
+                             int32_t* out_idx, float* out_max, const int* abort, hipStream_t st);
 int head_blocks();
 hipError_t launch_accept_greedy(const int32_t* tokens, const int32_t* parents,
                                 const int32_t* argmax, int n, StepResult* res, int32_t* out_flat,

@@ -773,6 +773,41 @@ mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, in
                                       ctx->abort_dev, ctx->stream), "lm_head");
 }
 
+mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const void* scales,
+                               const void* biases, int M, int K, int V, int group_size,
+                               const int32_t* banned, int n_banned, int32_t* out_argmax,
+                               float* out_max, float* out_logits) {
+    if (!ctx) return MJ_INVALID_ARG;
+    if (!x || !w || !scales || !biases || !out_argmax || M < 1 || M > MJ_MAX_ROWS || V < 1 ||
+        n_banned < 0 || (n_banned > 0 && !banned))
+        return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify_q4: bad argument (M must be 1..%d)",
+                       MJ_MAX_ROWS);
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)scales | (uintptr_t)biases) & 15)
+        return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify_q4: operands need 16-byte alignment");
+    const int kmax = M > 16 ? 2048 : 4096;  // staged hidden rows fit 140 KB of LDS
+    if (group_size != 64 || K % 512 != 0 || K > kmax)
+        return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
+                       "lm_head_verify_q4: K=%d gs=%d (need gs 64, K%%512==0, K<=%d)", K,
+                       group_size, kmax);
+    hipSetDevice(ctx->device);
+    mj_status s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
+    if (s != MJ_OK) return s;
+    Arena count;
+    count.take((size_t)head_blocks() * 32 * 4);
+    count.take((size_t)head_blocks() * 32 * 4);
+    s = mj_scratch_reserve(ctx, count.off);
+    if (s != MJ_OK) return s;
+    Arena real{ctx->scratch, 0};
+    float* pval = (float*)real.take((size_t)head_blocks() * 32 * 4);
+    int* pidx = (int*)real.take((size_t)head_blocks() * 32 * 4);
+    return mj_hip(ctx,
+                  launch_lm_head_q4((const uint16_t*)x, (const uint32_t*)w,
+                                    (const uint16_t*)scales, (const uint16_t*)biases, M, K, V,
+                                    banned, n_banned, out_logits, pval, pidx, out_argmax, out_max,
+                                    ctx->abort_dev, ctx->stream),
+                  "lm_head q4");
+}
+
 mj_status mj_accept_greedy(mj_ctx* ctx, const int32_t* tokens, const int32_t* parents_host,
                            const int32_t* argmax, int n_rows, int32_t* out) {
     if (!ctx) return MJ_INVALID_ARG;

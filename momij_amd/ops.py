@@ -101,6 +101,13 @@ class Context:
                                               n_banned, ptr(out_argmax), ptr(out_max),
                                               ptr(out_logits)))
 
+    def lm_head_verify_q4(self, x, w, scales, biases, M, K, V, out_argmax, out_max=None,
+                          out_logits=None, banned=None, n_banned=0, group_size=64):
+        self.check(self.lib.mj_lm_head_verify_q4(self.h, ptr(x), ptr(w), ptr(scales),
+                                                 ptr(biases), M, K, V, group_size, ptr(banned),
+                                                 n_banned, ptr(out_argmax), ptr(out_max),
+                                                 ptr(out_logits)))
+
     def accept_greedy(self, tokens, parents, argmax, n_rows, out):
         par = None
         if parents is not None:

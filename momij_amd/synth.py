@@ -47,6 +47,24 @@ def dequant(w, s, b, gs: int) -> np.ndarray:
     return sg * q + bg
 
 
+def qweight4(rng: np.random.Generator, V: int, K: int, scale=(0.001, 0.004)):
+    """Random 4-bit affine weight of the Maple head, group size 64: (w uint32 [V, K/8] with 8
+    codes a word, LSB first; s, b fp16 [V, K/64]; b = -7.5 s centres the codes)."""
+    w = rng.integers(0, 2**32, size=(V, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(scale[0], scale[1], size=(V, K // 64)).astype(np.float16)
+    b = (-7.5 * s.astype(np.float32)).astype(np.float16)
+    return w, s, b
+
+
+def dequant4(w, s, b) -> np.ndarray:
+    """float64 dense 4-bit weight [V, K] = s * q + b (group size 64)."""
+    V = w.shape[0]
+    q = ((w[..., :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15).reshape(V, -1)
+    sg = np.repeat(s.astype(np.float64), 64, axis=-1)
+    bg = np.repeat(b.astype(np.float64), 64, axis=-1)
+    return sg * q.astype(np.float64) + bg
+
+
 def normal_f16(rng: np.random.Generator, shape, std=1.0) -> np.ndarray:
     return (rng.standard_normal(shape) * std).astype(np.float16)
 

@@ -489,6 +489,42 @@ void or_lm_head_logits(const uint16_t* x, const uint16_t* w, float* logits, int 
     free(xf);
 }
 
+/* ------------------------------------------------------------------------- */
+/* a7, the Maple head: maple_lm_head_argmax's 4-bit affine weight                */
+/* (SeedlessMetal.swift:3005-3068): uint32 w[V][K/8] holds 8 codes, LSB first   */
+/* (nib j = (pack >> 4j) & 15, 3046-3053); scale / bias fp16 [V][K/64], the     */
+/* group of pack wk is wk >> 3 (3043-3044: group size 64); the weight is        */
+/* float(nib) * sc + bi in fp32 (3055-3062) times x.  Accumulated in double     */
+/* here and rounded once to float.                                             */
+/* ------------------------------------------------------------------------- */
+void or_lm_head_q4_logits(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                          const uint16_t* biases, float* logits, int M, int K, int V) {
+    float* xf = (float*)malloc(sizeof(float) * (size_t)M * K);
+    or_h2f_array(x, xf, (size_t)M * K);
+    const int packs = K / 8, groups = K / 64;
+#pragma omp parallel for schedule(static)
+    for (int v = 0; v < V; ++v) {
+        float* wf = (float*)malloc(sizeof(float) * (size_t)K);
+        for (int wk = 0; wk < packs; ++wk) {
+            const uint32_t pack = w[(size_t)v * packs + wk];
+            const float sc = or_h2f(scales[(size_t)v * groups + (wk >> 3)]);
+            const float bi = or_h2f(biases[(size_t)v * groups + (wk >> 3)]);
+            for (int j = 0; j < 8; ++j) {
+                const float q = (float)((pack >> (4 * j)) & 15u);
+                const float qs = q * sc;
+                wf[8 * wk + j] = qs + bi;
+            }
+        }
+        for (int m = 0; m < M; ++m) {
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k) acc += (double)wf[k] * (double)xf[(size_t)m * K + k];
+            logits[(size_t)m * V + v] = (float)acc;
+        }
+        free(wf);
+    }
+    free(xf);
+}
+
 void or_argmax_rows(const float* logits, int M, int V, const int32_t* banned, int n_banned,
                     int32_t* out_idx, float* out_best, float* out_second) {
     for (int m = 0; m < M; ++m) {

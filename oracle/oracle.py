@@ -73,6 +73,7 @@ def lib():
         L.or_layer_forward.argtypes = [vp, vp, vp, vp, vp, vp, C.c_int64, vp, i, vp, vp]
         L.or_attn_block.argtypes = [vp, vp, vp, vp, vp, vp, C.c_int64, vp, i]
         L.or_lm_head_logits.argtypes = [vp, vp, vp, i, i, i]
+        L.or_lm_head_q4_logits.argtypes = [vp, vp, vp, vp, vp, i, i, i]
         L.or_argmax_rows.argtypes = [vp, i, i, vp, i, vp, vp, vp]
         L.or_accept_greedy.argtypes = [vp, vp, vp, i, vp, vp]
         L.or_philox4x32_10.argtypes = [vp, vp, vp]
@@ -309,6 +310,21 @@ def lm_head_logits(x, w):
     V = w.shape[0]
     out = np.empty((M, V), np.float32)
     lib().or_lm_head_logits(x.ctypes.data, w.ctypes.data, out.ctypes.data, M, K, V)
+    return out
+
+
+def lm_head_q4_logits(x, w, scales, biases):
+    """The Maple 4-bit head (group size 64): w uint32 [V][K/8], scales / biases fp16 [V][K/64]."""
+    x = _c(x, np.float16)
+    w = _c(w, np.uint32)
+    s = _c(scales, np.float16)
+    b = _c(biases, np.float16)
+    M, K = x.shape
+    V = w.shape[0]
+    assert w.shape == (V, K // 8) and s.shape == (V, K // 64) and b.shape == (V, K // 64)
+    out = np.empty((M, V), np.float32)
+    lib().or_lm_head_q4_logits(x.ctypes.data, w.ctypes.data, s.ctypes.data, b.ctypes.data,
+                               out.ctypes.data, M, K, V)
     return out
 
 

@@ -275,6 +275,32 @@ def test_lm_head_argmax(orc):
     assert orc.argmax_rows(t, banned=np.array([4]))[0][0] == 7
 
 
+def test_lm_head_q4_closed_form(orc):
+    """The Maple 4-bit head against a float64 dequantised GEMV, plus the code order (nibble j
+    of pack wk is k = 8 wk + j) and the group of a pack (wk >> 3) pinned with one-hot inputs."""
+    rng = np.random.default_rng(13)
+    M, K, V = 3, 512, 3000
+    x = synth.normal_f16(rng, (M, K))
+    w, s, b = synth.qweight4(rng, V, K)
+    lg = orc.lm_head_q4_logits(x, w, s, b)
+    ref = x.astype(np.float64) @ synth.dequant4(w, s, b).T
+    assert np.allclose(lg, ref, rtol=1e-6, atol=1e-6)
+    assert (orc.argmax_rows(lg)[0] == ref.argmax(1)).all()
+    # one code set: pack 9 (group 1), nibble 5 = 11 -> weight at k = 77 is 11 s1 + b1
+    w1 = np.zeros((1, K // 8), np.uint32)
+    w1[0, 9] = np.uint32(11 << 20)
+    s1 = np.full((1, K // 64), 0.5, np.float16)
+    s1[0, 1] = 0.25
+    b1 = np.zeros((1, K // 64), np.float16)
+    b1[0, 1] = 1.0
+    xo = np.zeros((1, K), np.float16)
+    xo[0, 77] = 2.0
+    assert orc.lm_head_q4_logits(xo, w1, s1, b1)[0, 0] == np.float32(2.0 * (11 * 0.25 + 1.0))
+    xo[0, 77] = 0.0
+    xo[0, 64] = 1.0  # another k of group 1: code 0 -> the bias alone
+    assert orc.lm_head_q4_logits(xo, w1, s1, b1)[0, 0] == np.float32(1.0)
+
+
 # ----------------------------------------------------------------------------- greedy accept
 def test_accept_greedy_chain_kats(orc):
     """SpeculativeSamplingTests.swift:94-137 (walkDraft at temperature 0) as chain verifies."""
