@@ -157,7 +157,8 @@ mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, in
  * b[v][k/64]) x[m][k] (fp32), argmax per row with the lowest id winning ties and banned ids
  * skipped.  w uint32 [V][K/8] (8 codes a word, LSB first), scales/biases fp16 [V][K/64],
  * x fp16 [M][K]; group_size must be 64 and K a multiple of 512 (K <= 4096, <= 2048 for
- * M > 16); all four operands 16-byte aligned.  Outputs as mj_lm_head_verify. */
+ * M > 16); all four operands 16-byte aligned; n_banned <= 64 (the reference stages at most
+ * 16, SeedlessDecodeEngine.swift:470).  Outputs as mj_lm_head_verify. */
 mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const void* scales,
                                const void* biases, int M, int K, int V, int group_size,
                                const int32_t* banned, int n_banned, int32_t* out_argmax,

@@ -194,14 +194,24 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
 // logits[m][v] = sum_k (q s + b) x[m][k].  Same partials as k_lm_head (lowest id on ties,
 // banned ids skipped), folded by k_head_final.
 //
-// One 512-thread block per CU (two for <= 16 rows); wave w takes 16-row vocab strips
-// blockIdx.x * 8 + w + i * 8 * gridDim.x.  MFMA: A = 16 hidden rows x 32 k (staged in LDS), B =
-// the strip's codes: lane (n, q) holds row n's words 8g + 2q, 8g + 2q + 1 of 64-group g, each
-// widened to fp16 16 + q by the 2-bit gather's shift-and-or (nibble pairs (j, j + 4) per
-// word), so the hidden rows are staged with each 8-block in the order 0 4 1 5 2 6 3 7.  Per
-// group: s_g times the two MFMAs' sum; the remainder sum_g (b_g - 16 s_g) X_g (X_g the group
-// sum of a hidden row) is an fp32 MFMA chain.  A strip streams as four 8-group pieces, the
-// next requested before the current one is multiplied.
+// MFMA 16x16x32 f16 with A = 16 hidden rows (staged in LDS) and B = a 16-row vocab strip's
+// codes, each widened to fp16 16 + q (code q in the top four mantissa bits under exponent 16:
+// one shift and one mask-or per nibble pair (j, j + 4) of a word).  The products x (16 + q)
+// are exact in fp32; per 64-group g the MFMA sum is scaled by s_g, and the remainder
+// sum_g (b_g - 16 s_g) X_g (X_g = group sum of the hidden row, staged beside it) is a chain
+// of fp32 MFMAs.
+//
+// Loads: lane (n, q) reads 16 B -- words 16 j + 4 q of a group pair j -- so a strip row's
+// 64 B come in one request; one lane swap across the wave's halves (lanes 32..63 <-> 0..31)
+// then leaves lane q holding words (0, 1) of both groups for q = 0, (4, 5) for q = 1, (2, 3)
+// for q = 2 and (6, 7) for q = 3, so each MFMA takes one group.  The hidden rows are staged to
+// match: 8-k chunk c of a group at chunk position c with bits 1 and 2 swapped, and within a
+// chunk the order k 0 4 1 5 2 6 3 7 of the nibble pairs.
+//
+// Work unit: one K half of a strip, as k_lm_head: wave (slot, h) takes half h of strips
+// blockIdx.x * 4 + slot + round * gridDim.x * 4, the h = 1 partial meets the h = 0 one in
+// LDS.  A half streams as pieces of PL group pairs (16 rows x PL x 128 k codes plus their
+// scales and biases), the next requested before the current one is multiplied.
 struct HeadQ4Args {
     const uint16_t* x;   // [M][K] fp16
     const uint32_t* w;   // [V][K/8]
@@ -216,22 +226,19 @@ struct HeadQ4Args {
     const int* abort;
 };
 
-__device__ __forceinline__ void unpack8k(uint32_t w, u4v& o) {
-    // nibble pairs (j, j + 4) of the word into fp16 16 + q: shift to bits 6..9 of each half
-    const uint32_t m = 0x03C003C0u, c = 0x4C004C00u;
-    o[0] = ((w << 6) & m) | c;
-    o[1] = ((w << 2) & m) | c;
-    o[2] = ((w >> 2) & m) | c;
-    o[3] = ((w >> 6) & m) | c;
-}
+template <int PL>
+struct Q4Piece {
+    u4v c[PL];                          // codes: group pair j, words 16 j + 4 q .. + 3
+    uint32_t sc[PL], bs[PL];            // scales / biases of groups 2 j, 2 j + 1 (lo, hi)
+};
 
-template <int NT>
+template <int NT, int PL>
 __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
     if (aborted(a.abort)) return;
     extern __shared__ __align__(16) char q4lds[];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int K = a.K, XS = K + 8, G = K / 64, GS1 = G + 1;
-    uint16_t* xs = (uint16_t*)q4lds;                 // [NT*16][XS], 8-blocks as 0 4 1 5 2 6 3 7
+    uint16_t* xs = (uint16_t*)q4lds;                 // [NT*16][XS] hidden rows, code order
     float* xg = (float*)(xs + NT * 16 * XS);         // [NT*16][G + 1] group sums
     for (int idx = t; idx < NT * 16 * (K / 8); idx += 512) {
         const int m = idx / (K / 8), c = idx % (K / 8);
@@ -242,8 +249,11 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
         o[1] = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
         o[2] = (v[1] & 0xFFFFu) | (v[3] << 16);
         o[3] = (v[1] >> 16) | (v[3] & 0xFFFF0000u);
-        *(u4v*)(xs + m * XS + 8 * c) = o;
+        const int cp = (c & ~6) | ((c & 2) << 1) | ((c & 4) >> 1);
+        *(u4v*)(xs + m * XS + 8 * cp) = o;
     }
+    __shared__ int s_ban[MJ_HEAD_MAX_BANNED];  // banned ids (read with LDS, not vector, loads)
+    for (int idx = t; idx < a.n_banned; idx += 512) s_ban[idx] = a.banned[idx];
     for (int idx = t; idx < NT * 16 * G; idx += 512) {
         const int m = idx / G, g = idx % G;
         float sum = 0.0f;
@@ -258,7 +268,16 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
     __syncthreads();
 
     const int n = lane & 15, q = lane >> 4;
-    const int nstrips = (a.V + 15) / 16, TW = gridDim.x * 8, NP = G / 8;
+    const int nstrips = (a.V + 15) / 16;
+    const int slot = wv & 3, h = wv >> 2;
+    const int NH = G / 2 / (2 * PL);   // pieces per half strip
+    const int SW = gridDim.x * 4;
+    const int rounds = (nstrips - (int)blockIdx.x * 4 + SW - 1) / SW;
+    // the code offset 0x4C00 (fp16 16) kept in a VGPR so each nibble pair is one mask-or
+    uint32_t c16 = 0x4C004C00u;
+    asm("" : "+v"(c16));
+    const uint32_t nmask = 0x03C003C0u;
+    const int hsh = 16 * (q & 1);      // this lane's half of a scale word in the remainder chain
     float bv[NT][4];
     int bi[NT][4];
 #pragma unroll
@@ -268,53 +287,86 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
             bv[tl][r] = -INFINITY;
             bi[tl][r] = 0x7fffffff;
         }
-    // piece p of a strip: codes of groups 8p .. 8p+7 (words 8g + 2q, +1), their scales, biases
-    struct Piece {
-        uint32_t cw[8][2];
-        u4v sc, bs;
-    };
-    auto load_piece = [&](int strip, int p, Piece& pc) {
+    auto load_piece = [&](int strip, int pc, Q4Piece<PL>& pz) {
         const int vr = min(strip * 16 + n, a.V - 1);
-        const uint32_t* wr = a.w + (size_t)vr * (K / 8) + 64 * p + 2 * q;
+        const int g0 = 2 * PL * (h * NH + pc);   // first group of the piece
+        const u4v* wr = (const u4v*)(a.w + (size_t)vr * (K / 8) + 8 * g0) + q;
 #pragma unroll
-        for (int gg = 0; gg < 8; ++gg) {
-            const uint2 v = *(const uint2*)(wr + 8 * gg);
-            pc.cw[gg][0] = v.x;
-            pc.cw[gg][1] = v.y;
+        for (int j = 0; j < PL; ++j) pz.c[j] = wr[4 * j];
+        const uint16_t* sr = a.s + (size_t)vr * G + g0;
+        const uint16_t* br = a.b + (size_t)vr * G + g0;
+        if constexpr (PL == 4) {
+            const u4v sv4 = *(const u4v*)sr, bv4 = *(const u4v*)br;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pz.sc[j] = sv4[j];
+                pz.bs[j] = bv4[j];
+            }
+        } else {
+            const uint2 sv2 = *(const uint2*)sr, bv2 = *(const uint2*)br;
+            pz.sc[0] = sv2.x;
+            pz.sc[1] = sv2.y;
+            pz.bs[0] = bv2.x;
+            pz.bs[1] = bv2.y;
         }
-        pc.sc = *(const u4v*)(a.s + (size_t)vr * G + 8 * p);
-        pc.bs = *(const u4v*)(a.b + (size_t)vr * G + 8 * p);
     };
-    int strip = blockIdx.x * 8 + wv;
-    Piece cur;
-    if (strip < nstrips) load_piece(strip, 0, cur);
-    for (; strip < nstrips; strip += TW) {
-        const int v0 = strip * 16;
-        f4 acc[NT];
+    constexpr int NPB = NT == 1 ? 2 : 1;
+    __shared__ f4 s_part[NPB][4][NT][64];
+    // The wave's pieces form one stream (rounds x NH) through two register sets taken in
+    // turn: a set is refilled with the piece two ahead as soon as it has been multiplied, so
+    // one piece is always in flight behind the one in use and no set is copied.  Every load is
+    // issued -- past the stream's end at the clamped last row, a cached line -- which keeps the
+    // wait before a set's use from covering the other set's requests.
+    const int strip0 = blockIdx.x * 4 + slot, TP = rounds * NH;
+    int ld_strip = strip0, ld_pc = 0;
+    auto issue = [&](Q4Piece<PL>& pz) {
+        load_piece(ld_strip, ld_pc, pz);
+        if (++ld_pc == NH) {
+            ld_pc = 0;
+            ld_strip += SW;
+        }
+    };
+    f4 acc[NT];
 #pragma unroll
-        for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-        for (int p = 0; p < NP; ++p) {
-            const int nstrip = p + 1 < NP ? strip : strip + TW;
-            Piece nxt;
-            if (nstrip < nstrips) load_piece(nstrip, p + 1 < NP ? p + 1 : 0, nxt);
-            // remainder sum_g (b_g - 16 s_g) X_g of the piece: groups 8p + 4u + q
+    for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    int c_strip = strip0, c_pc = 0, c_rd = 0;
+    auto step = [&](Q4Piece<PL>& cur, int i) {
+        const int g0 = 2 * PL * (h * NH + c_pc);
+        // remainder: lane q's group of chain step u is 4 u + q of the piece
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int gg = 4 * u + q;  // this lane's group of the chain step (per-lane half)
-                const uint32_t sw = cur.sc[gg >> 1] >> (16 * (gg & 1));
-                const uint32_t bw = cur.bs[gg >> 1] >> (16 * (gg & 1));
-                const float cg = h2f((uint16_t)bw) - 16.0f * h2f((uint16_t)sw);
+        for (int u = 0; u < PL / 2; ++u) {
+            const uint32_t sw = (q >> 1) ? cur.sc[2 * u + 1] : cur.sc[2 * u];
+            const uint32_t bw = (q >> 1) ? cur.bs[2 * u + 1] : cur.bs[2 * u];
+            const float cg = h2f((uint16_t)(bw >> hsh)) - 16.0f * h2f((uint16_t)(sw >> hsh));
 #pragma unroll
-                for (int tl = 0; tl < NT; ++tl)
-                    acc[tl] = mfma16x16x4f32(xg[(tl * 16 + n) * GS1 + 8 * p + gg], cg, acc[tl]);
+            for (int tl = 0; tl < NT; ++tl)
+                acc[tl] = mfma16x16x4f32(xg[(tl * 16 + n) * GS1 + g0 + 4 * u + q], cg, acc[tl]);
+        }
+#pragma unroll
+        for (int j = 0; j < PL; ++j) {
+            u4v cw = cur.c[j];
+            {
+                const auto r0 = __builtin_amdgcn_permlane32_swap(cw[0], cw[2], false, false);
+                const auto r1 = __builtin_amdgcn_permlane32_swap(cw[1], cw[3], false, false);
+                cw[0] = r0[0];
+                cw[2] = r0[1];
+                cw[1] = r1[0];
+                cw[3] = r1[1];
             }
 #pragma unroll
-            for (int gg = 0; gg < 8; ++gg) {
-                const int g = 8 * p + gg;
+            for (int gi = 0; gi < 2; ++gi) {
+                const int g = g0 + 2 * j + gi;
                 u4v b0, b1;
-                unpack8k(cur.cw[gg][0], b0);
-                unpack8k(cur.cw[gg][1], b1);
-                const float sg = h2f((uint16_t)(cur.sc[gg >> 1] >> (16 * (gg & 1))));
+                const uint32_t w0 = cw[2 * gi], w1 = cw[2 * gi + 1];
+                b0[0] = ((w0 << 6) & nmask) | c16;
+                b0[1] = ((w0 << 2) & nmask) | c16;
+                b0[2] = ((w0 >> 2) & nmask) | c16;
+                b0[3] = ((w0 >> 6) & nmask) | c16;
+                b1[0] = ((w1 << 6) & nmask) | c16;
+                b1[1] = ((w1 << 2) & nmask) | c16;
+                b1[2] = ((w1 >> 2) & nmask) | c16;
+                b1[3] = ((w1 >> 6) & nmask) | c16;
+                const float sg = h2f((uint16_t)(cur.sc[j] >> (16 * gi)));
 #pragma unroll
                 for (int tl = 0; tl < NT; ++tl) {
                     const uint16_t* xr = xs + (tl * 16 + n) * XS + 64 * g + 16 * q;
@@ -325,27 +377,61 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
                     for (int r = 0; r < 4; ++r) acc[tl][r] += sg * d[r];
                 }
             }
-            cur = nxt;
         }
-        // lane (n, q): hidden rows tl*16 + 4q + r, vocab row v0 + n
-        const int v = v0 + n;
-        bool keep = v < a.V;
-        for (int bb = 0; bb < a.n_banned; ++bb)
-            if (a.banned[bb] == v) keep = false;
+        __builtin_amdgcn_sched_barrier(0);
+        issue(cur);  // the piece two ahead
+        __builtin_amdgcn_sched_barrier(0);
+        if (++c_pc < NH) return;
+        c_pc = 0;
+        if (i < TP) {  // end of a round: the same for every wave of the block
+            const bool live = c_strip < nstrips;
+            if (h == 1) {
 #pragma unroll
-        for (int tl = 0; tl < NT; ++tl)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = tl * 16 + 4 * q + r;
-                const float val = acc[tl][r];
-                if (keep && (val > bv[tl][r] || (val == bv[tl][r] && v < bi[tl][r]))) {
-                    bv[tl][r] = val;
-                    bi[tl][r] = v;
-                }
-                if (a.logits && m < a.M && v < a.V) a.logits[(size_t)m * a.V + v] = val;
+                for (int tl = 0; tl < NT; ++tl) s_part[c_rd % NPB][slot][tl][lane] = acc[tl];
             }
+            __syncthreads();  // the h = 1 halves are in LDS
+            if (live && h == 0) {
+#pragma unroll
+                for (int tl = 0; tl < NT; ++tl) {
+                    const f4 o = s_part[c_rd % NPB][slot][tl][lane];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[tl][r] += o[r];
+                }
+                // lane (n, q): vocab row v0 + n, hidden rows tl * 16 + 4 q + r
+                const int v = c_strip * 16 + n;
+                bool keep = v < a.V;
+                for (int bb = 0; bb < a.n_banned; ++bb)
+                    if (s_ban[bb] == v) keep = false;
+#pragma unroll
+                for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int m = tl * 16 + 4 * q + r;
+                        const float val = acc[tl][r];
+                        if (keep && (val > bv[tl][r] || (val == bv[tl][r] && v < bi[tl][r]))) {
+                            bv[tl][r] = val;
+                            bi[tl][r] = v;
+                        }
+                        if (a.logits && m < a.M && v < a.V) a.logits[(size_t)m * a.V + v] = val;
+                    }
+            }
+            if (NPB == 1) __syncthreads();  // the partials were read before the set is reused
+        }
+        c_strip += SW;
+        ++c_rd;
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    Q4Piece<PL> pa, pb;
+    issue(pa);
+    __builtin_amdgcn_sched_barrier(0);  // all of pa's requests before pb's
+    issue(pb);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < TP; i += 2) {
+        step(pa, i);
+        step(pb, i + 1);
     }
-    // across the 16 vocab lanes of a row group, then across waves
+    // across the 16 vocab lanes of a row group, then across the h = 0 waves
 #pragma unroll
     for (int tl = 0; tl < NT; ++tl)
 #pragma unroll
@@ -359,22 +445,22 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
                     bi[tl][r] = oi;
                 }
             }
-    __shared__ float sv[8][32];
-    __shared__ int si[8][32];
-    if (n == 0) {
+    __shared__ float sv[4][32];
+    __shared__ int si[4][32];
+    if (h == 0 && n == 0) {
 #pragma unroll
         for (int tl = 0; tl < NT; ++tl)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                sv[wv][tl * 16 + 4 * q + r] = bv[tl][r];
-                si[wv][tl * 16 + 4 * q + r] = bi[tl][r];
+                sv[slot][tl * 16 + 4 * q + r] = bv[tl][r];
+                si[slot][tl * 16 + 4 * q + r] = bi[tl][r];
             }
     }
     __syncthreads();
     if (t < NT * 16 && t < a.M) {
         float bb = sv[0][t];
         int ii = si[0][t];
-        for (int w2 = 1; w2 < 8; ++w2)
+        for (int w2 = 1; w2 < 4; ++w2)
             if (sv[w2][t] > bb || (sv[w2][t] == bb && si[w2][t] < ii)) {
                 bb = sv[w2][t];
                 ii = si[w2][t];
@@ -604,12 +690,15 @@ hipError_t launch_hold(unsigned us, hipStream_t st) {
 hipError_t set_attn_attributes();
 hipError_t set_gather3_attributes();
 
-// Rows in groups of <= 32 as launch_lm_head; K % 512 == 0 (8-group pieces), K <= 4096.
+// Rows in groups of <= 32 as launch_lm_head; K % 512 == 0 (a half strip is 4 groups or a
+// multiple of 8), K <= 4096 (<= 2048 for 17..32 rows).
 hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_t* s,
                              const uint16_t* b, int M, int K, int V, const int32_t* banned,
                              int n_banned, float* logits, float* pval, int* pidx,
                              int32_t* out_idx, float* out_max, const int* abort, hipStream_t st) {
-    if (K % 512 != 0 || K > 4096 || M < 1) return hipErrorInvalidValue;
+    if (K % 512 != 0 || K > 4096 || M < 1 || n_banned > MJ_HEAD_MAX_BANNED)
+        return hipErrorInvalidValue;
+    const bool pl4 = (K / 128) % 8 == 0;  // half strip of K / 128 groups: 8-group pieces
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mg = M - m0 < 32 ? M - m0 : 32;
         const int nt = mg <= 16 ? 1 : 2;
@@ -618,10 +707,14 @@ hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_
         const int nb = nt == 1 ? head_blocks() : head_blocks() / 2;
         HeadQ4Args qa{x + (size_t)m0 * K, w, s, b, mg, K, V, banned, n_banned,
                       logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
-        if (nt == 1)
-            launch_timed(k_lm_head_q4<1>, dim3(nb), dim3(512), lds, st, qa);
+        if (nt == 1 && pl4)
+            launch_timed(k_lm_head_q4<1, 4>, dim3(nb), dim3(512), lds, st, qa);
+        else if (nt == 1)
+            launch_timed(k_lm_head_q4<1, 2>, dim3(nb), dim3(512), lds, st, qa);
+        else if (pl4)
+            launch_timed(k_lm_head_q4<2, 4>, dim3(nb), dim3(512), lds, st, qa);
         else
-            launch_timed(k_lm_head_q4<2>, dim3(nb), dim3(512), lds, st, qa);
+            launch_timed(k_lm_head_q4<2, 2>, dim3(nb), dim3(512), lds, st, qa);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg,
@@ -640,12 +733,10 @@ hipError_t set_kernel_attributes() {
     if (e == hipSuccess)
         e = hipFuncSetAttribute((const void*)k_lm_head<2>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)k_lm_head_q4<1>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)k_lm_head_q4<2>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
+    const void* q4k[4] = {(const void*)k_lm_head_q4<1, 4>, (const void*)k_lm_head_q4<1, 2>,
+                          (const void*)k_lm_head_q4<2, 4>, (const void*)k_lm_head_q4<2, 2>};
+    for (int i = 0; i < 4 && e == hipSuccess; ++i)
+        e = hipFuncSetAttribute(q4k[i], hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
     if (e == hipSuccess) e = set_gather3_attributes();
     if (e == hipSuccess) done = true;

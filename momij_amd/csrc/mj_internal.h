@@ -177,6 +177,9 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
                           const int32_t* banned, int n_banned, float* logits, float* pval,
                           int* pidx, int32_t* out_idx, float* out_max, const int* abort,
                           hipStream_t st);
+// Banned ids the 4-bit head stages in LDS (the reference passes at most 16,
+// SeedlessDecodeEngine.swift:470, 496).
+#define MJ_HEAD_MAX_BANNED 64
 hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_t* s,
                              const uint16_t* b, int M, int K, int V, const int32_t* banned,
                              int n_banned, float* logits, float* pval, int* pidx,

@@ -782,6 +782,9 @@ mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const 
         n_banned < 0 || (n_banned > 0 && !banned))
         return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify_q4: bad argument (M must be 1..%d)",
                        MJ_MAX_ROWS);
+    if (n_banned > MJ_HEAD_MAX_BANNED)
+        return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify_q4: n_banned=%d (at most %d)",
+                       n_banned, MJ_HEAD_MAX_BANNED);
     if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)scales | (uintptr_t)biases) & 15)
         return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify_q4: operands need 16-byte alignment");
     const int kmax = M > 16 ? 2048 : 4096;  // staged hidden rows fit 140 KB of LDS
