@@ -146,7 +146,8 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
  * logits[m][v] = sum_k w[v][k] * x[m][k] (fp32), argmax per row with the lowest id winning
  * ties and banned ids skipped.  x fp16 [M][K], w fp16 [V][K]; out_argmax int32 [M];
  * out_max fp32 [M] (nullable); out_logits fp32 [M][V] (nullable; written when sampling).
- * banned int32 [n_banned] device (nullable). */
+ * banned int32 [n_banned] device (nullable), n_banned <= 64 (the reference stages at most 16,
+ * SeedlessDecodeEngine.swift:470). */
 mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, int K, int V,
                             const int32_t* banned, int n_banned, int32_t* out_argmax,
                             float* out_max, float* out_logits);

@@ -27,7 +27,7 @@ struct HeadArgs {
     const int* abort;
 };
 
-template <int NT>
+template <int NT, int PL>
 __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
     if (aborted(a.abort)) return;
     extern __shared__ uint16_t xs[];  // [NT*16][K + 8]
@@ -39,6 +39,8 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
         if (m < a.M) v = *(const u4v*)(a.x + (size_t)m * K + 8 * part);
         *(u4v*)(xs + m * XS + 8 * part) = v;
     }
+    __shared__ int s_ban[MJ_HEAD_MAX_BANNED];  // banned ids (read with LDS, not vector, loads)
+    for (int idx = t; idx < a.n_banned; idx += 512) s_ban[idx] = a.banned[idx];
     __syncthreads();
     const int ln = lane & 15, lq = lane >> 4;
     const int nstrips = (a.V + 15) / 16;
@@ -53,104 +55,116 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
     // strips blockIdx.x * 4 + slot + round * gridDim.x * 4; the h = 1 partial meets the h = 0
     // one in LDS (two slot sets by round parity), so twice as many units as strips keep the
     // waves' loads even.  A wave's halves are one stream of pieces of PL 32-k chunks (16 rows x
-    // 256 k, 8 KB, when K / 2 allows): the next piece is requested before the current one is
-    // multiplied.
+    // 256 k, 8 KB, when K / 2 allows) through two register sets taken in turn: a set is
+    // refilled with the piece two ahead as soon as it has been multiplied, so one piece is
+    // always in flight behind the one in use and no set is copied.  Every load is issued --
+    // past the stream's end at the clamped last row, a cached line -- which keeps the wait
+    // before a set's use from covering the other set's requests.
     const int slot = wv & 3, h = wv >> 2;
-    const int PL = (K / 64) % 8 == 0 ? 8 : 4;  // chunks per piece (K % 256 == 0)
     const int NH = K / 64 / PL;                // pieces per half strip
     const int SW = gridDim.x * 4;
     const int rounds = (nstrips - (int)blockIdx.x * 4 + SW - 1) / SW;  // of this block's slot 0
-    auto piece_ptr = [&](int strip, int pc) {
-        const int vr = strip * 16 + ln;
-        return (const u4v*)(a.w + (size_t)(vr < a.V ? vr : a.V - 1) * K) + lq +
-               4 * PL * (h * NH + pc);
+    const int strip0 = blockIdx.x * 4 + slot, TP = rounds * NH;
+    struct Piece {
+        u4v c[PL];
+    };
+    int ld_strip = strip0, ld_pc = 0;
+    auto issue = [&](Piece& pz) {
+        const int vr = min(ld_strip * 16 + ln, a.V - 1);
+        const u4v* wr = (const u4v*)(a.w + (size_t)vr * K) + lq + 4 * PL * (h * NH + ld_pc);
+#pragma unroll
+        for (int u = 0; u < PL; ++u) pz.c[u] = wr[4 * u];
+        if (++ld_pc == NH) {
+            ld_pc = 0;
+            ld_strip += SW;
+        }
     };
     // h = 1 partials: two sets by round parity for one tile; one set for two tiles (their rows
     // take most of the LDS), reused after a barrier
     constexpr int NPB = NT == 1 ? 2 : 1;
     __shared__ f4 s_part[NPB][4][NT][64];
-    int strip = blockIdx.x * 4 + slot;
-    u4v cur[8];
-    if (strip < nstrips) {
-        const u4v* wr = piece_ptr(strip, 0);
+    f4 acc[NT];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (u < PL) cur[u] = wr[4 * u];
-    }
-    for (int rd = 0; rd < rounds; ++rd, strip += SW) {
-        if (NPB == 1 && rd > 0) __syncthreads();  // the previous round's partials were read
-        const bool live = strip < nstrips;  // same for both halves of a strip
-        const int v0 = strip * 16;
-        f4 acc[NT];
+    for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    int c_strip = strip0, c_pc = 0, c_rd = 0;
+    auto step = [&](Piece& cur, int i) {
+        const int s0 = PL * (h * NH + c_pc);
 #pragma unroll
-        for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-        if (live) {
-            for (int pc = 0; pc < NH; ++pc) {
-                // the piece after this one: pc + 1 of this half, or piece 0 of the next round's
-                const int nstrip = pc + 1 < NH ? strip : strip + SW;
-                u4v nxt[8];
-                if (nstrip < nstrips) {
-                    const u4v* wn = piece_ptr(nstrip, pc + 1 < NH ? pc + 1 : 0);
+        for (int u = 0; u < PL; ++u) {
 #pragma unroll
-                    for (int u = 0; u < 8; ++u)
-                        if (u < PL) nxt[u] = wn[4 * u];
-                }
-                const int s0 = PL * (h * NH + pc);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    if (u >= PL) break;
-#pragma unroll
-                    for (int tl = 0; tl < NT; ++tl) {
-                        const u4v xb =
-                            *(const u4v*)(xs + (tl * 16 + ln) * XS + 32 * (s0 + u) + 8 * lq);
-                        acc[tl] = mfma16x16x32(as_h8(cur[u]), as_h8(xb), acc[tl]);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
+            for (int tl = 0; tl < NT; ++tl) {
+                const u4v xb = *(const u4v*)(xs + (tl * 16 + ln) * XS + 32 * (s0 + u) + 8 * lq);
+                acc[tl] = mfma16x16x32(as_h8(cur.c[u]), as_h8(xb), acc[tl]);
             }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(cur);  // the piece two ahead
+        __builtin_amdgcn_sched_barrier(0);
+        if (++c_pc < NH) return;
+        c_pc = 0;
+        if (i < TP) {  // end of a round: the same for every wave of the block
+            const bool live = c_strip < nstrips;
+            const int v0 = c_strip * 16;
             if (h == 1) {
 #pragma unroll
-                for (int tl = 0; tl < NT; ++tl) s_part[rd % NPB][slot][tl][lane] = acc[tl];
+                for (int tl = 0; tl < NT; ++tl) s_part[c_rd % NPB][slot][tl][lane] = acc[tl];
             }
-        }
-        __syncthreads();  // the h = 1 halves are in LDS
-        if (!live || h == 1) continue;
+            __syncthreads();  // the h = 1 halves are in LDS
+            if (live && h == 0) {
 #pragma unroll
-        for (int tl = 0; tl < NT; ++tl) {
-            const f4 o = s_part[rd % NPB][slot][tl][lane];
+                for (int tl = 0; tl < NT; ++tl) {
+                    const f4 o = s_part[c_rd % NPB][slot][tl][lane];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[tl][r] += o[r];
-        }
-        // lane holds logits for vocab v0 + 4*lq + r, row tl*16 + ln
+                    for (int r = 0; r < 4; ++r) acc[tl][r] += o[r];
+                }
+                // lane holds logits for vocab v0 + 4*lq + r, row tl*16 + ln
+                bool keep[4];
 #pragma unroll
-        for (int tl = 0; tl < NT; ++tl) {
-            const int m = tl * 16 + ln;
-            if (m >= a.M) continue;
-            float vals[4];
+                for (int r = 0; r < 4; ++r) {
+                    const int v = v0 + 4 * lq + r;
+                    keep[r] = v < a.V;
+                    for (int b = 0; b < a.n_banned; ++b)
+                        if (s_ban[b] == v) keep[r] = false;
+                }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int v = v0 + 4 * lq + r;
-                float s = acc[tl][r];
-                bool keep = v < a.V;
-                for (int b = 0; b < a.n_banned; ++b)
-                    if (a.banned[b] == v) keep = false;
-                vals[r] = s;
-                if (keep && (s > bv[tl] || (s == bv[tl] && v < bi[tl]))) {
-                    bv[tl] = s;
-                    bi[tl] = v;
+                for (int tl = 0; tl < NT; ++tl) {
+                    const int m = tl * 16 + ln;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int v = v0 + 4 * lq + r;
+                        const float sc = acc[tl][r];
+                        if (keep[r] && (sc > bv[tl] || (sc == bv[tl] && v < bi[tl]))) {
+                            bv[tl] = sc;
+                            bi[tl] = v;
+                        }
+                    }
+                    if (a.logits && m < a.M) {
+                        float* lp = a.logits + (size_t)m * a.V + v0 + 4 * lq;
+                        if (v0 + 4 * lq + 3 < a.V) {
+                            *(float4*)lp =
+                                make_float4(acc[tl][0], acc[tl][1], acc[tl][2], acc[tl][3]);
+                        } else {
+                            for (int r = 0; r < 4; ++r)
+                                if (v0 + 4 * lq + r < a.V) lp[r] = acc[tl][r];
+                        }
+                    }
                 }
             }
-            if (a.logits) {
-                float* lp = a.logits + (size_t)m * a.V + v0 + 4 * lq;
-                if (v0 + 4 * lq + 3 < a.V) {
-                    *(float4*)lp = make_float4(vals[0], vals[1], vals[2], vals[3]);
-                } else {
-                    for (int r = 0; r < 4; ++r)
-                        if (v0 + 4 * lq + r < a.V) lp[r] = vals[r];
-                }
-            }
+            if (NPB == 1) __syncthreads();  // the partials were read before the set is reused
         }
+        c_strip += SW;
+        ++c_rd;
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl) acc[tl] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    };
+    Piece pa, pb;
+    issue(pa);
+    __builtin_amdgcn_sched_barrier(0);  // all of pa's requests before pb's
+    issue(pb);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < TP; i += 2) {
+        step(pa, i);
+        step(pb, i + 1);
     }
     // reduce across lanes of the same row (lane, lane^16, lane^32, lane^48)
 #pragma unroll
@@ -521,20 +535,28 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
                           const int32_t* banned, int n_banned, float* logits, float* pval,
                           int* pidx, int32_t* out_idx, float* out_max, const int* abort,
                           hipStream_t st) {
-    if (K % 256 != 0 || M < 1) return hipErrorInvalidValue;  // two halves of 128-k multiples
+    if (K % 256 != 0 || M < 1 || n_banned > MJ_HEAD_MAX_BANNED)  // halves of 128-k multiples
+        return hipErrorInvalidValue;
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mg = M - m0 < 32 ? M - m0 : 32;
         // two blocks per CU for one 16-row tile; a 32-row group's LDS allows one
         const int nb = mg <= 16 ? head_blocks() : head_blocks() / 2;
         HeadArgs a{x + (size_t)m0 * K, w, mg, K, V, banned, n_banned,
                    logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
+        const bool pl8 = (K / 64) % 8 == 0;  // 8-chunk pieces when the half strip allows
         if (mg <= 16) {
             const size_t lds = (size_t)16 * (K + 8) * 2;
-            launch_timed(k_lm_head<1>, dim3(nb), dim3(512), lds, st, a);
+            if (pl8)
+                launch_timed(k_lm_head<1, 8>, dim3(nb), dim3(512), lds, st, a);
+            else
+                launch_timed(k_lm_head<1, 4>, dim3(nb), dim3(512), lds, st, a);
         } else {
             const size_t lds = (size_t)32 * (K + 8) * 2;
             if (lds > 140 * 1024) return hipErrorInvalidValue;  // K <= 2232 for 17..32 rows
-            launch_timed(k_lm_head<2>, dim3(nb), dim3(512), lds, st, a);
+            if (pl8)
+                launch_timed(k_lm_head<2, 8>, dim3(nb), dim3(512), lds, st, a);
+            else
+                launch_timed(k_lm_head<2, 4>, dim3(nb), dim3(512), lds, st, a);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -728,15 +750,13 @@ hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_
 hipError_t set_kernel_attributes() {
     static bool done = false;
     if (done) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute((const void*)k_lm_head<1>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)k_lm_head<2>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
-    const void* q4k[4] = {(const void*)k_lm_head_q4<1, 4>, (const void*)k_lm_head_q4<1, 2>,
-                          (const void*)k_lm_head_q4<2, 4>, (const void*)k_lm_head_q4<2, 2>};
-    for (int i = 0; i < 4 && e == hipSuccess; ++i)
-        e = hipFuncSetAttribute(q4k[i], hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
+    const void* hk[8] = {(const void*)k_lm_head<1, 8>,    (const void*)k_lm_head<1, 4>,
+                         (const void*)k_lm_head<2, 8>,    (const void*)k_lm_head<2, 4>,
+                         (const void*)k_lm_head_q4<1, 4>, (const void*)k_lm_head_q4<1, 2>,
+                         (const void*)k_lm_head_q4<2, 4>, (const void*)k_lm_head_q4<2, 2>};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 8 && e == hipSuccess; ++i)
+        e = hipFuncSetAttribute(hk[i], hipFuncAttributeMaxDynamicSharedMemorySize, 140 * 1024);
     if (e == hipSuccess) e = set_attn_attributes();
     if (e == hipSuccess) e = set_gather3_attributes();
     if (e == hipSuccess) done = true;

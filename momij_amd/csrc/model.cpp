@@ -754,6 +754,9 @@ mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, in
         (n_banned > 0 && !banned))
         return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify: bad argument (M must be 1..%d)",
                        MJ_MAX_ROWS);
+    if (n_banned > MJ_HEAD_MAX_BANNED)
+        return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify: n_banned=%d (at most %d)", n_banned,
+                       MJ_HEAD_MAX_BANNED);
     if (K % 256 != 0 || K > 4096)
         return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE, "lm_head_verify: K=%d (need K%%256==0, <=4096)",
                        K);
