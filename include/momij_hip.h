@@ -198,6 +198,18 @@ typedef struct mj_model_config {
     int64_t kv_capacity;   /* ring slots per layer (>= window + MJ_MAX_ROWS when windowed) */
     int E, top_k, I, gs;
     int vocab;
+    /* Maple's layer mix (MapleConfig.isSliding, MapleConfig.swift:145-148; SeedlessAttn.swift
+     * 81-83): host arrays [n_layers] overriding window and rope_dim per layer -- sliding layers
+     * window w with partial RoPE, full-attention layers 0 / 0 (NoPE).  NULL: every layer takes
+     * window / rope_dim.  The non-zero rope dims must all equal rope_dim. */
+    const int32_t* layer_window;
+    const int32_t* layer_rope_dim;
+    /* 4: lm_head is the 4-bit gs64 head of the checkpoint (headBits, MapleConfig.swift:141),
+     * uint32 [V][H/8] with lm_head_scales / lm_head_biases fp16 [V][H/64], decoded by
+     * mj_lm_head_verify_q4's kernel (H <= 2048).  0 or 16: fp16 [V][H]. */
+    int head_bits;
+    const void* lm_head_scales;
+    const void* lm_head_biases;
 } mj_model_config;
 
 typedef struct mj_layer_weights {

@@ -54,7 +54,8 @@ class ModelConfig(C.Structure):
     _fields_ = [("n_layers", i32), ("H", i32), ("n_heads", i32), ("n_kv_heads", i32),
                 ("head_dim", i32), ("rope_dim", i32), ("rope_base", f32), ("eps", f32),
                 ("window", i32), ("kv_capacity", i64), ("E", i32), ("top_k", i32), ("I", i32),
-                ("gs", i32), ("vocab", i32)]
+                ("gs", i32), ("vocab", i32), ("layer_window", vp), ("layer_rope_dim", vp),
+                ("head_bits", i32), ("lm_head_scales", vp), ("lm_head_biases", vp)]
 
 
 class LayerWeights(C.Structure):

@@ -9,6 +9,7 @@
 // captured once per (kind, rows) into a HIP graph and replayed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstddef>
 #include <cstring>
@@ -24,6 +25,7 @@ struct mj_model {
     mj_ctx* ctx = nullptr;
     mj_model_config cfg{};
     std::vector<mj_layer_weights> layers;
+    std::vector<int> lwin, lrope;  // per-layer sliding window (0 = full) and rope dims
     const uint16_t* embed = nullptr;
     const uint16_t* final_norm = nullptr;
     const uint16_t* lm_head = nullptr;
@@ -118,7 +120,7 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, int kind, hipStream_t 
         q.qkv.C = c.kv_capacity;
         q.qkv.nQ = nQ;
         q.qkv.nKV = nKV;
-        q.qkv.rope_dim = c.rope_dim;
+        q.qkv.rope_dim = m->lrope[l];
         q.qkv.eps = c.eps;
     }
     if (pf) pf->begin(PROF_DENSE, st);
@@ -141,8 +143,8 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, int kind, hipStream_t 
     a.M = M;
     a.nQ = nQ;
     a.nKV = nKV;
-    a.rope_dim = c.rope_dim;
-    a.window = c.window;
+    a.rope_dim = m->lrope[l];
+    a.window = m->lwin[l];
     a.max_chunks = m->max_chunks;
     a.C = c.kv_capacity;
     a.eps = c.eps;
@@ -231,8 +233,17 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
         // the last layer's expert combine wrote the final norm into xf
         float* logits = (kind == PASS_SAMPLED || m->cap_logits) ? m->logits : nullptr;
         if (m->profiling) m->prof.begin(PROF_HEAD, st);
-        s = mj_hip(ctx, launch_lm_head(m->xf, m->lm_head, M, H, c.vocab, nullptr, 0, logits,
-                                       m->pval, m->pidx, m->argmax, m->maxv, ab, st), "lm_head");
+        if (c.head_bits == 4)
+            s = mj_hip(ctx,
+                       launch_lm_head_q4(m->xf, (const uint32_t*)m->lm_head,
+                                         (const uint16_t*)c.lm_head_scales,
+                                         (const uint16_t*)c.lm_head_biases, M, H, c.vocab, nullptr,
+                                         0, logits, m->pval, m->pidx, m->argmax, m->maxv, ab, st),
+                       "lm_head q4");
+        else
+            s = mj_hip(ctx, launch_lm_head(m->xf, m->lm_head, M, H, c.vocab, nullptr, 0, logits,
+                                           m->pval, m->pidx, m->argmax, m->maxv, ab, st),
+                       "lm_head");
         if (m->profiling) m->prof.end(st);
         if (s != MJ_OK) return s;
         if (m->cap_logits) {
@@ -332,7 +343,9 @@ static mj_status check_rows(mj_model* m, int M) {
     const mj_model_config& c = m->cfg;
     if (M < 1 || M > MJ_MAX_ROWS)
         return mj_fail(m->ctx, MJ_INVALID_ARG, "rows %d outside 1..%d", M, MJ_MAX_ROWS);
-    if (c.window <= 0 && m->offset + M > c.kv_capacity)
+    bool any_full = false;
+    for (int w : m->lwin) any_full = any_full || w <= 0;
+    if (any_full && m->offset + M > c.kv_capacity)
         return mj_fail(m->ctx, MJ_CAPACITY, "kv capacity %lld exceeded at offset %lld + %d",
                        (long long)c.kv_capacity, (long long)m->offset, M);
     return MJ_OK;
@@ -354,10 +367,25 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         c.I % 1024 != 0 || c.I > 4096 || (c.gs != 64 && c.gs != 128) || c.vocab < 16 ||
         c.vocab > 196608 || c.n_layers < 1 || c.n_heads * 128 % 512 != 0)
         return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE, "model_create: unsupported configuration");
-    if (c.window > 0 && c.kv_capacity < (int64_t)c.window + MJ_MAX_ROWS)
-        return mj_fail(ctx, MJ_CAPACITY, "kv_capacity must be >= window + %d", MJ_MAX_ROWS);
-    if (c.window <= 0 && c.kv_capacity < MJ_MAX_ROWS)
-        return mj_fail(ctx, MJ_CAPACITY, "kv_capacity too small");
+    std::vector<int> lwin(c.n_layers, c.window), lrope(c.n_layers, c.rope_dim);
+    for (int l = 0; l < c.n_layers; ++l) {
+        if (c.layer_window) lwin[l] = c.layer_window[l];
+        if (c.layer_rope_dim) lrope[l] = c.layer_rope_dim[l];
+        if (lrope[l] != 0 && lrope[l] != c.rope_dim)
+            return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
+                           "model_create: layer %d rope_dim %d (0 or rope_dim %d)", l, lrope[l],
+                           c.rope_dim);
+        if (lwin[l] > 0 && c.kv_capacity < (int64_t)lwin[l] + MJ_MAX_ROWS)
+            return mj_fail(ctx, MJ_CAPACITY, "kv_capacity must be >= window + %d", MJ_MAX_ROWS);
+        if (lwin[l] <= 0 && c.kv_capacity < MJ_MAX_ROWS)
+            return mj_fail(ctx, MJ_CAPACITY, "kv_capacity too small");
+    }
+    if (c.head_bits != 0 && c.head_bits != 16 &&
+        (c.head_bits != 4 || !c.lm_head_scales || !c.lm_head_biases || c.H > 2048 ||
+         c.gs <= 0))
+        return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
+                       "model_create: head_bits %d (16, or 4 with scales and biases, H <= 2048)",
+                       c.head_bits);
     hipSetDevice(ctx->device);
     mj_status s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
     if (s != MJ_OK) return s;
@@ -365,13 +393,19 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
     m->ctx = ctx;
     m->cfg = c;
     m->layers.assign(layers, layers + c.n_layers);
+    m->lwin = lwin;
+    m->lrope = lrope;
+    // the layer arrays are the caller's: the copy keeps no pointer to them
+    m->cfg.layer_window = nullptr;
+    m->cfg.layer_rope_dim = nullptr;
     m->embed = (const uint16_t*)embed;
     m->final_norm = (const uint16_t*)final_norm_w;
     m->lm_head = (const uint16_t*)lm_head;
     const int H = c.H, nQ = c.n_heads, nKV = c.n_kv_heads, R = MJ_MAX_ROWS;
     const int qkvN = (nQ + 2 * nKV) * 128;
     m->layer_stride = 2LL * nKV * c.kv_capacity * 128;
-    m->max_chunks = attn_max_chunks(c.window, c.kv_capacity, R);
+    m->max_chunks = 0;
+    for (int w : lwin) m->max_chunks = std::max(m->max_chunks, attn_max_chunks(w, c.kv_capacity, R));
     const int gqa = nQ / nKV;
     const int nqt16 = ((R * gqa + 15) / 16) * 16;
     auto layout = [&](Arena& a) {

@@ -31,32 +31,76 @@ class MapleLikeConfig:
     I: int = 1024
     gs: int = 64
     vocab: int = 151936
+    # Maple's layer mix: per-layer sliding window (0 = full attention) and rope dims (0 = NoPE);
+    # None = every layer takes window / rope_dim
+    layer_window: list | None = None
+    layer_rope_dim: list | None = None
+    # 16: fp16 lm_head [V][H]; 4: the checkpoint's 4-bit gs64 head
+    head_bits: int = 16
 
-    def to_c(self) -> ModelConfig:
-        return ModelConfig(self.n_layers, self.H, self.n_heads, self.n_kv_heads, self.head_dim,
-                           self.rope_dim, self.rope_base, self.eps, self.window, self.kv_capacity,
-                           self.E, self.top_k, self.I, self.gs, self.vocab)
+    def to_c(self, lm_head_scales=None, lm_head_biases=None) -> ModelConfig:
+        c = ModelConfig(self.n_layers, self.H, self.n_heads, self.n_kv_heads, self.head_dim,
+                        self.rope_dim, self.rope_base, self.eps, self.window, self.kv_capacity,
+                        self.E, self.top_k, self.I, self.gs, self.vocab)
+        self._arrays = []
+        if self.layer_window is not None:
+            a = (C.c_int32 * self.n_layers)(*[int(v) for v in self.layer_window])
+            self._arrays.append(a)
+            c.layer_window = C.cast(a, C.c_void_p)
+        if self.layer_rope_dim is not None:
+            a = (C.c_int32 * self.n_layers)(*[int(v) for v in self.layer_rope_dim])
+            self._arrays.append(a)
+            c.layer_rope_dim = C.cast(a, C.c_void_p)
+        c.head_bits = self.head_bits
+        c.lm_head_scales = ptr(lm_head_scales)
+        c.lm_head_biases = ptr(lm_head_biases)
+        return c
 
-    def attn_cfg(self) -> dict:
+    def layer_window_of(self, l: int) -> int:
+        return self.window if self.layer_window is None else int(self.layer_window[l])
+
+    def layer_rope_of(self, l: int) -> int:
+        return self.rope_dim if self.layer_rope_dim is None else int(self.layer_rope_dim[l])
+
+    def attn_cfg(self, layer: int | None = None) -> dict:
+        """Attention configuration of one layer (or of the uniform stack)."""
+        win = self.window if layer is None else self.layer_window_of(layer)
+        rd = self.rope_dim if layer is None else self.layer_rope_of(layer)
         return dict(H=self.H, nQ=self.n_heads, nKV=self.n_kv_heads, D=self.head_dim,
-                    rope_dim=self.rope_dim, rope_base=self.rope_base, eps=self.eps,
-                    window=self.window, C=self.kv_capacity, gs=self.gs)
+                    rope_dim=rd, rope_base=self.rope_base, eps=self.eps, window=win,
+                    C=self.kv_capacity, gs=self.gs)
+
+    @staticmethod
+    def maple_layer_mix(n_layers: int, window: int, rope_dim: int, layer_types=None):
+        """Per-layer (windows, rope dims) of MapleConfig.isSliding (MapleConfig.swift:145-148)
+        and SeedlessAttn.swift:81-83: layer l slides (window, partial RoPE) when
+        layer_types[l] == "sliding_attention", or, without layer_types, when (l + 1) % 4 != 0;
+        the others are full attention without RoPE."""
+        wins, ropes = [], []
+        for l in range(n_layers):
+            if layer_types is not None and l < len(layer_types):
+                sliding = layer_types[l] == "sliding_attention"
+            else:
+                sliding = (l + 1) % 4 != 0
+            wins.append(window if sliding else 0)
+            ropes.append(rope_dim if sliding else 0)
+        return wins, ropes
 
 
 class VerifyEngine:
     def __init__(self, ctx: Context, cfg: MapleLikeConfig, layers: list, embed, final_norm_w,
-                 lm_head):
+                 lm_head, lm_head_scales=None, lm_head_biases=None):
         self.ctx = ctx
         self.cfg = cfg
         self.lib = ctx.lib
-        self._keep = (layers, embed, final_norm_w, lm_head)
+        self._keep = (layers, embed, final_norm_w, lm_head, lm_head_scales, lm_head_biases)
         arr = (LayerWeights * cfg.n_layers)()
         for i, lw in enumerate(layers):
             arr[i].attn = Context.attn_struct(lw["attn"])
             arr[i].moe = Context.moe_struct(lw["moe"])
         self._arr = arr
         h = C.c_void_p()
-        c = cfg.to_c()
+        c = cfg.to_c(lm_head_scales, lm_head_biases)
         ctx.check(self.lib.mj_model_create(ctx.h, C.byref(c), C.cast(arr, C.c_void_p), ptr(embed),
                                            ptr(final_norm_w), ptr(lm_head), C.byref(h)))
         self.h = h

@@ -1,0 +1,125 @@
+"""GPU parity of a Maple checkpoint end to end: the MLX safetensors layout loaded and sanitized
+by momij_amd/checkpoint.py, Maple's layer mix (sliding layers with partial RoPE, every 4th layer
+full attention without RoPE) and its 4-bit gs64 lm_head inside the resident model.
+
+A synthetic 4-layer checkpoint at the real layer shapes (hidden 2048, 16/4 heads of 128,
+16 experts top-4, intermediate 1024, gs 64, vocabulary 2048, window 48; tests/ckpt_util.py) is
+prefilled with 100 tokens and verified with an 8-token chain draft; the oracle replays the same
+passes per layer (its own window / RoPE per layer, the 4-bit head) on its own caches.  Argmax
+rows, accepted length and emitted tokens are compared bit for bit (a differing argmax must be a
+numerical near-tie).
+"""
+import numpy as np
+import pytest
+
+from tests.ckpt_util import write_maple_checkpoint
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def maple(tmp_path_factory):
+    import torch
+
+    from momij_amd.checkpoint import load_maple
+    from momij_amd.engine import VerifyEngine
+    from momij_amd.ops import Context
+
+    d = str(tmp_path_factory.mktemp("maple_gpu"))
+    write_maple_checkpoint(d, n_layers=4, E=16, top_k=4, vocab=2048, window=48, seed=11)
+    cfg, w = load_maple(d, max_context=192)
+    assert cfg.layer_window == [48, 48, 48, 0] and cfg.layer_rope_dim == [64, 64, 64, 0]
+    ctx = Context(0)
+    dev = w.device()
+    torch.cuda.synchronize()
+    eng = VerifyEngine(ctx, cfg, *dev)
+
+    def h(t):
+        a = t.detach().cpu().numpy()
+        return a.view(np.uint32) if a.dtype == np.int32 else a
+
+    host = dict(layers=[{part: {k: (h(v) if hasattr(v, "detach") else v)
+                                for k, v in lw[part].items()} for part in ("attn", "moe")}
+                        for lw in w.layers],
+                embed=h(w.embed), fnorm=h(w.final_norm), head=h(w.lm_head),
+                head_s=h(w.lm_head_scales), head_b=h(w.lm_head_biases))
+    yield dict(ctx=ctx, cfg=cfg, eng=eng, w=host)
+    eng.close()
+    ctx.close()
+
+
+class OracleMaple:
+    def __init__(self, orc, cfg, w):
+        self.orc, self.cfg, self.w = orc, cfg, w
+        C = cfg.kv_capacity
+        self.kc = [np.zeros((cfg.n_kv_heads, C, 128), np.float16) for _ in range(cfg.n_layers)]
+        self.vc = [np.zeros((cfg.n_kv_heads, C, 128), np.float16) for _ in range(cfg.n_layers)]
+        self.L = 0
+
+    def rows(self, tokens, parents):
+        h = self.w["embed"][np.asarray(tokens)]
+        for l in range(self.cfg.n_layers):
+            h, self.kc[l], self.vc[l], _, _ = self.orc.layer_forward(
+                self.cfg.attn_cfg(l), self.w["layers"][l], h, self.kc[l], self.vc[l], self.L,
+                np.asarray(parents, np.int32))
+        xf = self.orc.rms_norm(h, self.w["fnorm"], self.cfg.eps)
+        return self.orc.lm_head_q4_logits(xf, self.w["head"], self.w["head_s"], self.w["head_b"])
+
+    def prefill(self, tokens, chunk=64):
+        for i in range(0, len(tokens), chunk):
+            t = tokens[i:i + chunk]
+            self.rows(t, list(range(-1, len(t) - 1)))
+            self.L += len(t)
+
+
+def _argmax_match(orc, gpu_am, logits, what):
+    idx, best, second = orc.argmax_rows(logits)
+    for r, (g, o) in enumerate(zip(gpu_am, idx)):
+        if g != o:
+            near = (best[r] - logits[r, g]) <= 1e-3 * max(1.0, abs(best[r]))
+            assert near, (what, r, g, o, best[r], logits[r, g])
+            print(f"[{what}] row {r}: near-tie argmax {g} vs {o}", flush=True)
+    return idx
+
+
+def test_maple_checkpoint_prefill_and_verify(maple, orc):
+    eng, cfg = maple["eng"], maple["cfg"]
+    print("case: maple checkpoint, 4 layers (layer 3 full NoPE), 4-bit head", flush=True)
+    rng = np.random.default_rng(2)
+    prompt = rng.integers(0, cfg.vocab, 100).tolist()
+    eng.rewind(0)
+    y = eng.prefill(prompt, chunk=64)
+    om = OracleMaple(orc, cfg, maple["w"])
+    om.prefill(prompt[:-1])
+    lg = om.rows(prompt[-1:], [-1])
+    om.L += 1
+    assert _argmax_match(orc, [y], lg, "prefill")[0] == y
+    L0 = eng.offset
+    cont, t = [], y
+    for _ in range(8):
+        t = eng.step_chain_feeds([t])[0]
+        cont.append(t)
+    eng.rewind(L0)
+    draft = cont[:5] + [int(v) for v in rng.integers(0, cfg.vocab, 3)]
+    for i in range(5, 8):
+        if draft[i] == cont[i]:
+            draft[i] = (draft[i] + 1) % cfg.vocab
+    acc, toks = eng.verify_greedy(y, draft)
+    assert acc == 5 and toks == cont[:6], (acc, toks, cont)
+    lg = om.rows([y] + draft, list(range(-1, 8)))
+    am = _argmax_match(orc, cont[:6], lg[:6], "verify")
+    oacc, _, oemit = orc.accept_greedy([y] + draft, None, am.tolist() + [0] * 3)
+    assert oacc == acc and list(oemit) == toks
+
+
+def test_full_attention_capacity_guard(maple):
+    from momij_amd._lib import MomijError
+
+    eng, cfg = maple["eng"], maple["cfg"]
+    print("case: full-attention layer past its KV capacity", flush=True)
+    eng.rewind(0)
+    y = eng.prefill(list(range(1, cfg.kv_capacity - 3)), chunk=64)
+    # 9 more rows do not fit the full-attention layer's ring: refused before any kernel runs
+    with pytest.raises(MomijError):
+        eng.verify_greedy(y, [2, 3, 4, 5, 6, 7, 8, 9])
+    eng.rewind(0)
