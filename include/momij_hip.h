@@ -37,7 +37,8 @@ typedef enum mj_status {
     MJ_INVALID_ARG = 4,        /* null pointer, bad index, bad tree */
     MJ_ABORTED = 5,            /* abort word set (stopBuf, SeedlessMetal.swift:60, 69-70) */
     MJ_HIP_ERROR = 6,          /* HIP runtime failure */
-    MJ_CAPACITY = 7            /* KV capacity / prompt too long (SeedlessAttn.swift:279-286) */
+    MJ_CAPACITY = 7,           /* KV capacity / prompt too long (SeedlessAttn.swift:279-286) */
+    MJ_OUT_OF_MEMORY = 8       /* host allocation failed (draft indexes) */
 } mj_status;
 
 typedef struct mj_ctx mj_ctx;
@@ -289,6 +290,60 @@ float mj_model_kernel_ms(const mj_model* model, int kernel_class, int64_t* launc
 /* Hardware self-check of the MFMA operand layout the kernels rely on (16x16x32 f16):
  * D = A[16x32] * B[32x16] with A, B fp16 row-major device, D fp32 [16][16] device. */
 mj_status mj_selftest_mfma(mj_ctx* ctx, const void* A, const void* B, float* D);
+
+/* ---------------------------------------------------------- draft sources ---- */
+/* Host-only drafters that propose the rows a verify pass checks (no device work).
+ *
+ * Online suffix-tree index -- SuffixDraftIndex (SuffixDraftIndex.swift:12-156): every suffix of
+ * the inserted sequences, truncated to max_depth (>= 4), with occurrence counts.  A draft takes
+ * the longest suffix of `history` (at most max_depth) that ends at a node with children, then
+ * follows the most frequent child mj_suffix_max_spec(match, max_k, alpha) times; equal counts
+ * take the lowest token id (the reference's order there is its dictionary's).  out_tokens
+ * holds max_k ids; *out_n drafted, *out_match_len the suffix length (0: no match). */
+typedef struct mj_suffix_index mj_suffix_index;
+mj_status mj_suffix_index_create(int max_depth, mj_suffix_index** out);
+mj_status mj_suffix_index_destroy(mj_suffix_index* idx);
+mj_status mj_suffix_index_clear(mj_suffix_index* idx);
+int64_t mj_suffix_index_tokens(const mj_suffix_index* idx);
+mj_status mj_suffix_index_insert(mj_suffix_index* idx, const int32_t* tokens, int n);
+mj_status mj_suffix_index_draft(const mj_suffix_index* idx, const int32_t* history, int n,
+                                int max_k, double alpha, int32_t* out_tokens, int* out_n,
+                                int* out_match_len);
+/* MAX_SPEC = alpha * match, at least 1 with a match, at most max_k -- maxSpec (48-53). */
+int mj_suffix_max_spec(int match_len, int max_k, double alpha);
+/* bestDraft (103-121): the local then the global index (either NULL), longer match first, then
+ * the longer draft. */
+mj_status mj_suffix_best_draft(const mj_suffix_index* local, const mj_suffix_index* global,
+                               const int32_t* history, int n, int max_k, double alpha,
+                               int32_t* out_tokens, int* out_n, int* out_match_len);
+/* qAlong (123-156): the draft model's q along `draft`, child count over sibling mass from the
+ * longest matching suffix; positions past the tree stay 1.  out_q float [n_draft]. */
+mj_status mj_suffix_index_q_along(const mj_suffix_index* idx, const int32_t* history, int n,
+                                  const int32_t* draft, int n_draft, float* out_q);
+/* Prompt-lookup draft -- SuffixSpec.suffixDraft (SuffixSpec.swift:17-55): the longest pattern
+ * (<= max_ngram, reference default 16) ending the history, its latest earlier occurrence (one
+ * inside the first prompt_len tokens first, when prompt_len > 0), and up to k tokens after it. */
+mj_status mj_suffix_draft_pld(const int32_t* history, int n, int k, int max_ngram,
+                              int prompt_len, int32_t* out_tokens, int* out_n);
+/* treeDraft (SuffixDraftIndex.swift:160-178): best tree draft, else the prompt lookup. */
+mj_status mj_tree_draft(const int32_t* history, int n, int k, const mj_suffix_index* local,
+                        const mj_suffix_index* global, double alpha, int prompt_len,
+                        int32_t* out_tokens, int* out_n);
+/* adaptiveDraftK (SuffixSpec.swift:8-15): draft length from the mean accepted length. */
+int mj_adaptive_draft_k(double mean_accept, int draft_k);
+
+/* Token recycling -- TokenRecycleIndex (TokenRecycleIndex.swift:9-57): per token the top_k
+ * (>= 2) latest candidate successors, newest first; a draft follows first successors until one
+ * repeats or is missing. */
+typedef struct mj_recycle_index mj_recycle_index;
+mj_status mj_recycle_index_create(int top_k, mj_recycle_index** out);
+mj_status mj_recycle_index_destroy(mj_recycle_index* r);
+mj_status mj_recycle_index_clear(mj_recycle_index* r);
+mj_status mj_recycle_index_observe(mj_recycle_index* r, int32_t from_token,
+                                   const int32_t* candidates, int n);
+mj_status mj_recycle_index_draft(const mj_recycle_index* r, int32_t last, int max_k,
+                                 int32_t* out_tokens, int* out_n);
+int mj_recycle_index_entries(const mj_recycle_index* r);
 
 #ifdef __cplusplus
 }

@@ -83,6 +83,24 @@ _SIGS = {
     "mj_lm_head_verify": (i32, [vp, vp, vp, i32, i32, i32, vp, i32, vp, vp, vp]),
     "mj_lm_head_verify_q4": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp,
                                    vp]),
+    "mj_suffix_index_create": (i32, [i32, C.POINTER(vp)]),
+    "mj_suffix_index_destroy": (i32, [vp]),
+    "mj_suffix_index_clear": (i32, [vp]),
+    "mj_suffix_index_tokens": (i64, [vp]),
+    "mj_suffix_index_insert": (i32, [vp, vp, i32]),
+    "mj_suffix_index_draft": (i32, [vp, vp, i32, i32, C.c_double, vp, vp, vp]),
+    "mj_suffix_max_spec": (i32, [i32, i32, C.c_double]),
+    "mj_suffix_best_draft": (i32, [vp, vp, vp, i32, i32, C.c_double, vp, vp, vp]),
+    "mj_suffix_index_q_along": (i32, [vp, vp, i32, vp, i32, vp]),
+    "mj_suffix_draft_pld": (i32, [vp, i32, i32, i32, i32, vp, vp]),
+    "mj_tree_draft": (i32, [vp, i32, i32, vp, vp, C.c_double, i32, vp, vp]),
+    "mj_adaptive_draft_k": (i32, [C.c_double, i32]),
+    "mj_recycle_index_create": (i32, [i32, C.POINTER(vp)]),
+    "mj_recycle_index_destroy": (i32, [vp]),
+    "mj_recycle_index_clear": (i32, [vp]),
+    "mj_recycle_index_observe": (i32, [vp, i32, vp, i32]),
+    "mj_recycle_index_draft": (i32, [vp, i32, i32, vp, vp]),
+    "mj_recycle_index_entries": (i32, [vp]),
     "mj_accept_greedy": (i32, [vp, vp, vp, vp, i32, vp]),
     "mj_accept_sampled": (i32, [vp, vp, i32, i32, vp, f32, i32, vp, u64, u64, vp]),
     "mj_model_create": (i32, [vp, C.POINTER(ModelConfig), vp, vp, vp, vp, C.POINTER(vp)]),

@@ -84,6 +84,7 @@ const char* mj_status_str(mj_status s) {
         case MJ_ABORTED: return "aborted";
         case MJ_HIP_ERROR: return "hip error";
         case MJ_CAPACITY: return "capacity exceeded";
+        case MJ_OUT_OF_MEMORY: return "out of memory";
     }
     return "unknown";
 }
