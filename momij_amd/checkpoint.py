@@ -100,17 +100,22 @@ def sanitize(arrays: dict, n_layers: int, group_size: int) -> dict:
     return arrays
 
 
-def dequant4(w, s, b, group_size: int = 64):
-    """fp16 table of a 4-bit affine weight (8 codes a uint32 word, LSB first): q * s + b in
-    fp32, rounded once to fp16."""
+def dequant4(w, s, b, group_size: int = 64, rows_per_chunk: int = 8192):
+    """fp16 table [V][K] of a 4-bit affine weight [V][K/8] (8 codes a uint32 word, LSB first):
+    q * s + b in fp32, rounded once to fp16; done in row chunks to bound the fp32 temporaries."""
     import torch
 
     wi = w.view(torch.int32) if w.dtype != torch.int32 else w
     shifts = torch.arange(0, 32, 4, dtype=torch.int32)
-    q = ((wi.unsqueeze(-1) >> shifts) & 15).reshape(*wi.shape[:-1], -1).float()
-    sg = s.float().repeat_interleave(group_size, dim=-1)
-    bg = b.float().repeat_interleave(group_size, dim=-1)
-    return (q * sg + bg).to(torch.float16)
+    V = wi.shape[0]
+    out = torch.empty((V, wi.shape[1] * 8), dtype=torch.float16)
+    for r0 in range(0, V, rows_per_chunk):
+        r1 = min(V, r0 + rows_per_chunk)
+        q = ((wi[r0:r1].unsqueeze(-1) >> shifts) & 15).reshape(r1 - r0, -1).float()
+        sg = s[r0:r1].float().repeat_interleave(group_size, dim=-1)
+        bg = b[r0:r1].float().repeat_interleave(group_size, dim=-1)
+        out[r0:r1] = (q * sg + bg).to(torch.float16)
+    return out
 
 
 def _codes(t):
