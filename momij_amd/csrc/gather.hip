@@ -170,15 +170,17 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     uint16_t* wsc = (uint16_t*)(wreg + S::WCODE);          // [16][K/GS/KS] this K-slice
     uint16_t* wbi = (uint16_t*)(wreg + S::WCODE + S::WSB);
     // staged rows: one set, two in persistent mode (set buf serves the current item)
+    // one row set; persistent mode keeps two pair lists (the next item's rows are staged once
+    // every wave is done with the current ones, while the current epilogue still needs its pairs)
     constexpr int NBUF = PER ? 2 : 1;
     uint16_t* const xs0 = (uint16_t*)(g5lds + (size_t)WPB * S::WAVE_BYTES);  // [RA][XS] qx rows
-    float2* const xsl0 = (float2*)(xs0 + NBUF * RA * XS);  // [RA][SS] {sum x, sum base*x}
-    float* el = (float*)(xsl0 + NBUF * RA * S::SS);        // [R][ES] QKV epilogue staging
+    float2* const xsl0 = (float2*)(xs0 + RA * XS);  // [RA][SS] {sum x, sum base*x}
+    float* el = (float*)(xsl0 + RA * S::SS);        // [R][ES] QKV epilogue staging
     char* red = (char*)el + (EPI == EPI_QKV ? R * ES * 4 : 0);  // [KS-1][TPB][64] f4
     __shared__ int s_pair[NBUF][R];
     int buf = 0;
-    auto xs_of = [&](int b) { return xs0 + b * RA * XS; };
-    auto xsl_of = [&](int b) { return xsl0 + b * RA * S::SS; };
+    auto xs_of = [&](int) { return xs0; };
+    auto xsl_of = [&](int) { return xsl0; };
 
     // ---- activation rows of a pass, straight into LDS: rows < npass only (the rest feed
     // MFMA output rows that are discarded).  Wave w stages rows w, w + WPB, ...
@@ -381,15 +383,15 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
             for (int r = 0; r < 4; ++r) pin(acc[r]);
         }
+        // persistent mode, last pass of the item: this wave's tile is free, start the next
+        // item's weights; its rows follow once every wave is done with the current ones
+        bool stage_next = false;
+        int np_next = 0;
         if constexpr (PER) {
-            // last pass of the item: this wave's tile is free, start the next item's weights
             const int nx = item + (int)gridDim.x;
-            const int np_next = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
-            if (pb + RA >= np && nx / ncb < 64 && np_next > 0) {
-                issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16, nx % ncb);
-                // and its rows, into the other set (its last reader finished an item ago)
-                stage_load(0, min(RA, np_next), buf ^ 1, rec_n & 0xFFFF, np_next);
-            }
+            np_next = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
+            stage_next = pb + RA >= np && nx / ncb < 64 && np_next > 0;
+            if (stage_next) issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16, nx % ncb);
         }
         if constexpr (KS > 1) {
             // K-slices of a tile meet in LDS (a slice's partial goes into its own wave's tile
@@ -411,6 +413,13 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[r] += o[r];
                 }
+            }
+        }
+        if constexpr (PER) {
+            if (stage_next) {
+                // every wave has read its rows (the K-slice barrier, or this one)
+                if constexpr (KS == 1) lds_only_barrier();
+                stage_load(0, min(RA, np_next), buf ^ 1, rec_n & 0xFFFF, np_next);
             }
         }
         // lane (n, q) now holds the outputs of activation rows 4q .. 4q+3 for weight row n
@@ -546,12 +555,12 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     const bool expert = a.ecnt != nullptr || a.srec != nullptr;
     const size_t limit =
         (EPI == EPI_SWIGLU || EPI == EPI_STORE) && expert ? 80 * 1024 - 256 : G5_LDS_MAX;
-    while (RA > 1 && S::lds(RA, want > RA || PER, PER) > limit) --RA;
+    while (RA > 1 && S::lds(RA, want > RA || PER) > limit) --RA;
     const bool multi = want > RA;
     int grid = n_buckets * ncb;
     if (PER && grid > persistent_blocks()) grid = persistent_blocks();
     launch_timed(k_gather5<KPL, GS, EPI, WPB, KS, PER>, dim3(grid), dim3(WPB * 64),
-                 S::lds(RA, multi || PER, PER), st, a, RA, (int)multi);
+                 S::lds(RA, multi || PER), st, a, RA, (int)multi);
     return hipGetLastError();
 }
 
