@@ -1,7 +1,7 @@
 /*
  * momij_oracle.c -- CPU restatement of momij's speculative-decode verify step.
  *
- * TEST INFRASTRUCTURE ONLY (the checker and the timed CPU baseline).  The product library
+ * TEST INFRASTRUCTURE ONLY (the parity reference and the timed CPU baseline).  The product library
  * libmomij_hip.so never links, loads or calls this code.  Built by oracle/Makefile with
  * -O3 -ffp-contract=off so that every a*b+c below rounds twice unless fmaf() is written.
  *

@@ -2,7 +2,7 @@
  * momij_oracle.h -- CPU restatement of momij's speculative-decode verify step.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg may load this library, and only as the checker / the timed CPU
+ * cpu_baseline leg may load this library, and only as the parity reference / the timed CPU
  * baseline.  The product library (libmomij_hip.so) never links or calls it.
  *
  * Every function cites the reference file:line whose semantics it restates

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (libmomij_oracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg, always as the checker or the timed CPU baseline, never as the thing
+cpu_baseline leg, always as the parity reference or the timed CPU baseline, never as the thing
 measured or shipped.  The product (momij_amd / libmomij_hip.so) never imports this module.
 
 fp16 arrays are numpy float16; everything else is float32 / int32 / int64 / uint32.
