@@ -168,7 +168,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only (asked for --gpus {args.gpus}); the verify "
-              "step runs on a single GPU in this build", file=sys.stderr)
+              "step here runs on a single GPU (expert / vocabulary sharding is a design, not "
+              "built)", file=sys.stderr)
         sys.exit(2)
 
     import torch
