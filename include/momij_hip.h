@@ -96,6 +96,12 @@ typedef struct mj_moe_weights {
     const void* down_b;
     int E, top_k, H, I, gs;
     float eps;
+    /* optional row-alpha form (WeightStore.swift:47-63: scales = alpha in every group of a
+     * row, biases = -alpha): fp16 [E][2I] and [E][H], 16-byte aligned, or NULL.  When set,
+     * up_gate_s/_b and down_s/_b must hold that expansion; the batched expert kernels then
+     * read one alpha per row instead of the group scales and biases. */
+    const void* up_gate_alpha;
+    const void* down_alpha;
 } mj_moe_weights;
 
 /* MoE block -- encodeMoEBlock (SeedlessMetal.swift:576-609), MapleMoE.callAsFunction

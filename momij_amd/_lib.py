@@ -36,7 +36,8 @@ u64 = C.c_uint64
 class MoeWeights(C.Structure):
     _fields_ = [("norm_w", vp), ("router_w", vp), ("up_gate_w", vp), ("up_gate_s", vp),
                 ("up_gate_b", vp), ("down_w", vp), ("down_s", vp), ("down_b", vp),
-                ("E", i32), ("top_k", i32), ("H", i32), ("I", i32), ("gs", i32), ("eps", f32)]
+                ("E", i32), ("top_k", i32), ("H", i32), ("I", i32), ("gs", i32), ("eps", f32),
+                ("up_gate_alpha", vp), ("down_alpha", vp)]
 
 
 class AttnWeights(C.Structure):

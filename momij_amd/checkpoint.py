@@ -7,7 +7,8 @@ Follows WeightStore (WeightStore.swift:9-92) and the engine's weight lookups
     (`metalF16`, 28-30), integer code arrays are kept as they are;
   * `<p>.row_alpha` [..., N] replaces `<p>.scales` / `<p>.biases` of the 2-bit weight
     `<p>.weight` [..., N, K/16]: scales = alpha repeated over the K / group_size groups,
-    biases = -scales (47-63);
+    biases = -scales (47-63); alpha itself is kept as `<p>.alpha`, and the experts' copy goes
+    to the MoE block, whose batched kernels then fold it (one alpha a row, no group loads);
   * q_proj, k_proj, v_proj concatenate along the output rows into qkv_proj, and the experts'
     up_proj, gate_proj along their rows into up_gate_proj, up first (66-90);
   * the 4-bit gs64 word embedding is dequantised once into an fp16 table
@@ -85,6 +86,7 @@ def sanitize(arrays: dict, n_layers: int, group_size: int) -> dict:
         scales = (alpha.unsqueeze(-1) * torch.ones(n_groups, dtype=alpha.dtype)).contiguous()
         arrays[prefix + ".scales"] = scales
         arrays[prefix + ".biases"] = scales * -1
+        arrays[prefix + ".alpha"] = alpha.contiguous()
     for l in range(n_layers):
         attn = f"model.layers.{l}.self_attn"
         for sfx in ("weight", "scales", "biases"):
@@ -92,7 +94,7 @@ def sanitize(arrays: dict, n_layers: int, group_size: int) -> dict:
             if all(p in arrays for p in parts):
                 arrays[f"{attn}.qkv_proj.{sfx}"] = torch.cat([arrays.pop(p) for p in parts], 0)
         mlp = f"model.layers.{l}.mlp.switch_mlp"
-        for sfx in ("weight", "scales", "biases"):
+        for sfx in ("weight", "scales", "biases", "alpha"):
             up, gate = f"{mlp}.up_proj.{sfx}", f"{mlp}.gate_proj.{sfx}"
             if up in arrays and gate in arrays:
                 arrays[f"{mlp}.up_gate_proj.{sfx}"] = torch.cat([arrays.pop(up),
@@ -173,6 +175,8 @@ def load_maple(model_dir: str, max_context: int = 4096):
                    up_gate_b=req(f"{mo}.up_gate_proj.biases"),
                    down_w=_codes(req(f"{mo}.down_proj.weight")),
                    down_s=req(f"{mo}.down_proj.scales"), down_b=req(f"{mo}.down_proj.biases"),
+                   up_gate_alpha=a.get(f"{mo}.up_gate_proj.alpha"),
+                   down_alpha=a.get(f"{mo}.down_proj.alpha"),
                    E=cfg.E, top_k=cfg.top_k, H=cfg.H, I=cfg.I, gs=cfg.gs, eps=cfg.eps)
         layers.append(dict(attn=attn, moe=moe))
     embed = dequant4(req("model.word_embeddings.weight"), req("model.word_embeddings.scales"),

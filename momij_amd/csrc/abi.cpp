@@ -260,6 +260,8 @@ mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void
     if (!w->router_w || !w->up_gate_w || !w->up_gate_s || !w->up_gate_b || !w->down_w ||
         !w->down_s || !w->down_b || ((flags & MJ_MOE_PRENORM) && !w->norm_w))
         return mj_fail(ctx, MJ_INVALID_ARG, "moe_block: null weight pointer");
+    if (((uintptr_t)w->up_gate_alpha | (uintptr_t)w->down_alpha) % 16 != 0)
+        return mj_fail(ctx, MJ_INVALID_ARG, "moe_block: row-alpha arrays must be 16-byte aligned");
     const int H = w->H, I = w->I, E = w->E, k = w->top_k, gs = w->gs;
     if (H % 2048 != 0 || H > 4096 || I % 1024 != 0 || I > 4096 || E < k || E > MJ_MAX_EXPERTS ||
         k < 1 || k > 8 || (gs != 64 && gs != 128))
@@ -430,6 +432,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         } else {
             up.bk = ms.bk;
         }
+        up.alpha = tile ? (const uint16_t*)w->up_gate_alpha : nullptr;
         up.y = ms.act;
         up.ysum = ms.act_sum;
         up.K = H;
@@ -453,6 +456,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         dn.w = w->down_w;
         dn.s = (const uint16_t*)w->down_s;
         dn.b = (const uint16_t*)w->down_b;
+        dn.alpha = tile ? (const uint16_t*)w->down_alpha : nullptr;
         dn.y = ms.down;
         dn.ysum = nullptr;
         dn.K = I;

@@ -108,7 +108,7 @@ __device__ __forceinline__ void lds_only_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false>
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false>
 // four waves per SIMD: two 8-wave blocks (or one 16-wave block) per CU
 __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gather5(
     GatherArgs a, int RA, int multi) {
@@ -241,12 +241,18 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
             }
         };
         __builtin_amdgcn_sched_barrier(0);  // loads issued before stay ahead in the vmcnt queue
-        const char* sg = (const char*)a.s;
-        const char* bg = (const char*)a.b;
-        if (lane < 16 * SCW) {
-            const int r = lane / SCW, c = kh * SCW + lane % SCW;
-            load_lds16(sg + tile_row(r) * (K / GS) * 2 + 16 * c, wsc);
-            load_lds16(bg + tile_row(r) * (K / GS) * 2 + 16 * c, wbi);
+        if constexpr (ROWA) {
+            // row-alpha weights: one alpha per row (scale alpha, bias -alpha in every group);
+            // tile rows 0..7 and 8..15 are each 8 consecutive rows, 16 bytes
+            if (lane < 2) load_lds16((const char*)a.alpha + tile_row(8 * lane) * 2, wsc);
+        } else {
+            const char* sg = (const char*)a.s;
+            const char* bg = (const char*)a.b;
+            if (lane < 16 * SCW) {
+                const int r = lane / SCW, c = kh * SCW + lane % SCW;
+                load_lds16(sg + tile_row(r) * (K / GS) * 2 + 16 * c, wsc);
+                load_lds16(bg + tile_row(r) * (K / GS) * 2 + 16 * c, wbi);
+            }
         }
         const char* wg = (const char*)a.w;
         const int r = lane >> 2, B4 = (lane & 3) ^ (r >> 2);
@@ -274,15 +280,16 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     const uint32_t* wq = (const uint32_t*)wcode + 16 * n + q;  // B: word q of row n's chunks
 
     auto run_pass = [&](int pb, int npass) {
-        constexpr int G = KBW / 4;  // code column groups, issued after the two scale loads
+        constexpr int G = KBW / 4;  // code column groups, issued after the scale loads
+        constexpr int NSB = ROWA ? 1 : 2;  // scale / bias loads of a tile
         // every wave's staged rows visible (this wave's were issued before its weights)
         if (pb == 0 && !early)
-            lds_barrier<G + 2>();
+            lds_barrier<G + NSB>();
         else
             lds_barrier<0>();
         if (own_sums) {
             own_block_sums(npass);
-            lds_barrier<G + 2>();
+            lds_barrier<G + NSB>();
         }
         // persistent mode: the next item's record, fetched behind this item's weights (one
         // vector load younger than them: PF)
@@ -293,10 +300,15 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         }
         wait_vmcnt<G + PF>();      // scales and biases have landed
         u4v sv[SCW], bv[SCW];
+        float alpha_n = 0.0f;  // row-alpha weights: alpha of weight row n
+        if constexpr (ROWA) {
+            alpha_n = h2f(wsc[n]);
+        } else {
 #pragma unroll
-        for (int c = 0; c < SCW; ++c) {
-            sv[c] = *(const u4v*)(wsc + (n * SCW + c) * 8);
-            bv[c] = *(const u4v*)(wbi + (n * SCW + c) * 8);
+            for (int c = 0; c < SCW; ++c) {
+                sv[c] = *(const u4v*)(wsc + (n * SCW + c) * 8);
+                bv[c] = *(const u4v*)(wbi + (n * SCW + c) * 8);
+            }
         }
         // + sum_B (b_B X_B - s_B Bx_B): fp32 MFMA chains over k = (block, term) pairs, issued
         // while the codes are still arriving (scales, biases and activation sums are in);
@@ -310,22 +322,29 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         // the fp16 half of block 2i + q/2's group (the sign flipped in the fp16 bits)
         const uint32_t sgn = (q & 1) ? 0x8000u : 0u;
         const uint32_t hsh = 16u * (uint32_t)(q >> 1);
-        u4v mv[SCW];
+        if constexpr (ROWA) {
+            // bias -alpha and scale alpha: B = -alpha for both terms
 #pragma unroll
-        for (int c = 0; c < SCW; ++c)
+            for (int i = 0; i < KBW / 2; ++i)
+                corr[i & 3] = mfma16x16x4f32(xcs[4 * i], -alpha_n, corr[i & 3]);
+        } else {
+            u4v mv[SCW];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) mv[c][w] = (q & 1) ? sv[c][w] : bv[c][w];
+            for (int c = 0; c < SCW; ++c)
 #pragma unroll
-        for (int i = 0; i < KBW / 2; ++i) {
-            const float xa_k = xcs[4 * i];  // block 2i + q/2
-            uint32_t h;
-            if constexpr (GS == 64) {  // group 2i + q/2: word i % 4 of chunk 2i / 8, half q/2
-                h = mv[(2 * i) / 8][i % 4] >> hsh;
-            } else {  // group i
-                h = mv[i / 8][(i % 8) / 2] >> (16 * (i & 1));
+                for (int w = 0; w < 4; ++w) mv[c][w] = (q & 1) ? sv[c][w] : bv[c][w];
+#pragma unroll
+            for (int i = 0; i < KBW / 2; ++i) {
+                const float xa_k = xcs[4 * i];  // block 2i + q/2
+                uint32_t h;
+                if constexpr (GS == 64) {  // group 2i + q/2: word i % 4 of chunk 2i / 8, half q/2
+                    h = mv[(2 * i) / 8][i % 4] >> hsh;
+                } else {  // group i
+                    h = mv[i / 8][(i % 8) / 2] >> (16 * (i & 1));
+                }
+                const float wk = h2f((uint16_t)(h ^ sgn));
+                corr[i & 3] = mfma16x16x4f32(xa_k, wk, corr[i & 3]);
             }
-            const float wk = h2f((uint16_t)(h ^ sgn));
-            corr[i & 3] = mfma16x16x4f32(xa_k, wk, corr[i & 3]);
         }
         __builtin_amdgcn_sched_barrier(0);
         // A: activation row xrow, quarter q, of this K-slice
@@ -335,6 +354,9 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         float acc[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] = (corr[0][r] + corr[1][r]) + (corr[2][r] + corr[3][r]);
+        // row-alpha weights: every block has scale alpha, so the MFMA sums chain over the whole
+        // slice and alpha scales them once
+        f4 dacc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};  // even / odd blocks
         // sum_B s_B * (sum q x)_B: per 64-block f16 MFMA sums, scaled in fp32, one column group
         // at a time as its codes arrive
 #pragma unroll
@@ -367,21 +389,33 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
                 const int B = B2 + b;
                 uint32_t v[8];
                 unpack16k(wd[b], v, uk);
-                f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (ROWA) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const u4v bq = {v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
-                    d = mfma16x16x32(as_h8(xv[b][h]), as_h8(bq), d);
+                    for (int h = 0; h < 2; ++h) {
+                        const u4v bq = {v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                        dacc[b] = mfma16x16x32(as_h8(xv[b][h]), as_h8(bq), dacc[b]);
+                    }
+                } else {
+                    f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const u4v bq = {v[4 * h], v[4 * h + 1], v[4 * h + 2], v[4 * h + 3]};
+                        d = mfma16x16x32(as_h8(xv[b][h]), as_h8(bq), d);
+                    }
+                    const int g = B * 64 / GS;
+                    const uint32_t sw = opaque(sv[g / 8][(g % 8) / 2]);
+                    const float sc = h2f((uint16_t)(sw >> (16 * (g & 1))));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[r] += sc * d[r];
                 }
-                const int g = B * 64 / GS;
-                const uint32_t sw = opaque(sv[g / 8][(g % 8) / 2]);
-                const float sc = h2f((uint16_t)(sw >> (16 * (g & 1))));
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[r] += sc * d[r];
               }
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) pin(acc[r]);
+        }
+        if constexpr (ROWA) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += alpha_n * (dacc[0][r] + dacc[1][r]);
         }
         // persistent mode, last pass of the item: this wave's tile is free, start the next
         // item's weights; its rows follow once every wave is done with the current ones
@@ -544,7 +578,7 @@ static int persistent_blocks() {
     return 2 * cus;
 }
 
-template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false>
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false>
 static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStream_t st) {
     using S = G5Shape<KPL, GS, EPI, WPB, KS>;
     const int ncb = a.N / (16 * S::TPB);
@@ -559,7 +593,7 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     const bool multi = want > RA;
     int grid = n_buckets * ncb;
     if (PER && grid > persistent_blocks()) grid = persistent_blocks();
-    launch_timed(k_gather5<KPL, GS, EPI, WPB, KS, PER>, dim3(grid), dim3(WPB * 64),
+    launch_timed(k_gather5<KPL, GS, EPI, WPB, KS, PER, ROWA>, dim3(grid), dim3(WPB * 64),
                  S::lds(RA, multi || PER), st, a, RA, (int)multi);
     return hipGetLastError();
 }
@@ -585,6 +619,23 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
     const bool per = a.srec != nullptr;
     if (per && (n_buckets > 64 || (epi != EPI_SWIGLU && epi != EPI_STORE)))
         return hipErrorInvalidValue;
+    // row-alpha expert weights (scale alpha, bias -alpha in every group of a row): the
+    // fold kernels read one alpha per row instead of the group scales and biases
+    if (a.alpha != nullptr && (a.srec != nullptr || a.ecnt != nullptr) &&
+        (epi == EPI_SWIGLU || epi == EPI_STORE)) {
+#define MJ_G5A(KPL, E, KS64, KS128)                                                        \
+    {                                                                                      \
+        if (per)                                                                           \
+            return a.gs == 64 ? launch_g5<KPL, 64, E, 8, KS64, true, true>(a, rows, n_buckets, st) \
+                              : launch_g5<KPL, 128, E, 8, KS128, true, true>(a, rows, n_buckets, st); \
+        return a.gs == 64 ? launch_g5<KPL, 64, E, 8, KS64, false, true>(a, rows, n_buckets, st)    \
+                          : launch_g5<KPL, 128, E, 8, KS128, false, true>(a, rows, n_buckets, st); \
+    }
+        if (epi == EPI_SWIGLU) MJ_G5A(8, EPI_SWIGLU, 2, 2)
+        if (a.K == 1024) MJ_G5A(4, EPI_STORE, 1, 1)
+        MJ_G5A(8, EPI_STORE, 2, 2)
+#undef MJ_G5A
+    }
 #define MJ_G5(KPL, E, W, KS64, KS128)                                                      \
     if (per && (E == EPI_SWIGLU || E == EPI_STORE))                                         \
         return a.gs == 64 ? launch_g5<KPL, 64, E, W, KS64, true>(a, rows, n_buckets, st)    \
@@ -603,9 +654,9 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
     return hipErrorInvalidValue;
 }
 
-template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false>
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false>
 static hipError_t g5_attr() {
-    return hipFuncSetAttribute((const void*)k_gather5<KPL, GS, EPI, WPB, KS, PER>,
+    return hipFuncSetAttribute((const void*)k_gather5<KPL, GS, EPI, WPB, KS, PER, ROWA>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)std::min(G5Shape<KPL, GS, EPI, WPB, KS>::lds(16, true),
                                              G5_LDS_MAX));
@@ -621,5 +672,12 @@ hipError_t set_gather3_attributes() {
     MJ_A(8, EPI_SWIGLU, 8, 2, 2) MJ_A(8, EPI_QKV, 16, 2, 2) MJ_A(8, EPI_ADD, 8, 4, 2)
     MJ_A(4, EPI_STORE, 8, 1, 1) MJ_A(8, EPI_STORE, 8, 2, 2)
 #undef MJ_A
+#define MJ_AA(KPL, E, KS64, KS128)                                              \
+    if (e == hipSuccess) e = g5_attr<KPL, 64, E, 8, KS64, true, true>();        \
+    if (e == hipSuccess) e = g5_attr<KPL, 128, E, 8, KS128, true, true>();      \
+    if (e == hipSuccess) e = g5_attr<KPL, 64, E, 8, KS64, false, true>();       \
+    if (e == hipSuccess) e = g5_attr<KPL, 128, E, 8, KS128, false, true>();
+    MJ_AA(8, EPI_SWIGLU, 2, 2) MJ_AA(4, EPI_STORE, 1, 1) MJ_AA(8, EPI_STORE, 2, 2)
+#undef MJ_AA
     return e;
 }

@@ -114,6 +114,8 @@ struct GatherArgs {
                             // expert id, lane 1 the pair count (high 16 bits); count 0 past the
                             // last routed expert
     int dense_rows;         // dense: rows 0 .. dense_rows-1 of expert 0
+    const uint16_t* alpha;  // row-alpha weights [E][N] fp16 (scale alpha, bias -alpha in
+                            // every group): the tile expert kernels read it instead of s / b
     uint16_t* y;            // STORE/ADD: [pairs][N] ; SWIGLU: act qx [pairs][I]
     float2* ysum;           // SWIGLU: act sums [pairs][I/64]
     int K, N, gs;

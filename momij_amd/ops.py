@@ -68,7 +68,8 @@ class Context:
         return MoeWeights(ptr(mw.get("norm_w")), ptr(mw["router_w"]), ptr(mw["up_gate_w"]),
                           ptr(mw["up_gate_s"]), ptr(mw["up_gate_b"]), ptr(mw["down_w"]),
                           ptr(mw["down_s"]), ptr(mw["down_b"]), mw["E"], mw["top_k"], mw["H"],
-                          mw["I"], mw["gs"], mw["eps"])
+                          mw["I"], mw["gs"], mw["eps"], ptr(mw.get("up_gate_alpha")),
+                          ptr(mw.get("down_alpha")))
 
     def moe_block(self, mw: dict, x, y, M, flags=0, inds=None, scores=None):
         st = self.moe_struct(mw)

@@ -55,8 +55,12 @@ def write_maple_checkpoint(d: str, *, n_layers=4, H=2048, nQ=16, nKV=4, D=128, E
         arrays[f"{p}.mlp.gate.weight"] = bf16(0.02 * rng.standard_normal((E, H)))
         for name, (N, K) in (("up", (I, H)), ("gate", (I, H)), ("down", (H, I))):
             w, s, b = q2((E,), N, K)
-            arrays[f"{mo}.{name}_proj.weight"], arrays[f"{mo}.{name}_proj.scales"], \
-                arrays[f"{mo}.{name}_proj.biases"] = w, s, b
+            arrays[f"{mo}.{name}_proj.weight"] = w
+            if l == 1:  # row-alpha experts
+                arrays[f"{mo}.{name}_proj.row_alpha"] = bf16(rng.uniform(0.005, 0.02,
+                                                                         size=(E, N)))
+            else:
+                arrays[f"{mo}.{name}_proj.scales"], arrays[f"{mo}.{name}_proj.biases"] = s, b
     es = rng.uniform(*embed_scale, size=(vocab, H // 64))
     arrays["model.word_embeddings.weight"] = codes(vocab, H // 8)
     arrays["model.word_embeddings.scales"] = bf16(es)

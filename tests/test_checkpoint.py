@@ -123,3 +123,16 @@ def test_missing_weight_is_an_error(tmp_path):
         save_file(t, os.path.join(d, fn))
     with pytest.raises(KeyError):
         load_maple(d)
+
+
+def test_expert_row_alpha_kept_for_the_fold(ckpt):
+    """Row-alpha experts keep alpha (up || gate along the rows) beside the expanded scales, and
+    the loader hands it to the MoE block; other layers pass none."""
+    _, cfg, w = ckpt
+    m1, m0 = w.layers[1]["moe"], w.layers[0]["moe"]
+    a_ug, a_dn = _np(m1["up_gate_alpha"]), _np(m1["down_alpha"])
+    assert a_ug.shape == (cfg.E, 2 * cfg.I) and a_dn.shape == (cfg.E, cfg.H)
+    s_ug = _np(m1["up_gate_s"])
+    assert (s_ug == a_ug[..., None]).all() and (_np(m1["up_gate_b"]) == -s_ug).all()
+    assert (_np(m1["down_s"]) == a_dn[..., None]).all()
+    assert m0["up_gate_alpha"] is None and m0["down_alpha"] is None

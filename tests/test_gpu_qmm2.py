@@ -130,6 +130,61 @@ def test_moe_block(ctx, orc, M, flags):
     assert rel < 5e-3
 
 
+def _row_alpha(mw):
+    """Row-alpha form of the expert weights (WeightStore.swift:47-63): alpha = the row's first
+    group scale, scales = alpha in every group, biases = -alpha."""
+    for p in ("up_gate", "down"):
+        alpha = np.ascontiguousarray(mw[p + "_s"][..., 0])
+        mw[p + "_s"] = np.ascontiguousarray(np.repeat(alpha[..., None], mw[p + "_s"].shape[-1], -1))
+        mw[p + "_b"] = (-mw[p + "_s"]).astype(np.float16)
+        mw[p + "_alpha"] = alpha
+    return mw
+
+
+@pytest.mark.parametrize("E,I,gs,M", [(64, 1024, 64, 8), (16, 1024, 128, 9),
+                                      (128, 1024, 128, 17), (128, 2048, 64, 8)])
+def test_moe_block_row_alpha(ctx, orc, E, I, gs, M):
+    """Row-alpha experts: the fold kernels (one alpha per row) against the oracle on the
+    expanded scales / biases, and against the group-scale kernels on the same arrays --
+    persistent slot records (E <= 64) and per-expert lists (E = 128), both K widths of down."""
+    import torch
+
+    print(f"case: moe row-alpha E={E} I={I} gs={gs} M={M}", flush=True)
+    rng = np.random.default_rng(900 + E + I + gs + M)
+    H, k = 2048, 8
+    mw = _row_alpha(synth.moe_weights(rng, E, H, I, gs))
+    x = synth.normal_f16(rng, (M, H))
+    ref_y, ref_i, _ = orc.moe_block(mw, x, prenorm=True, residual=True)
+    dmw = _moe_dev(mw)
+    dx = dev(x)
+    outs = []
+    for use_alpha in (True, False):
+        w = dict(dmw) if use_alpha else {k2: v for k2, v in dmw.items() if not k2.endswith("_alpha")}
+        y = torch.empty_like(dx)
+        inds = torch.empty((M, k), dtype=torch.int32, device="cuda")
+        _run(ctx, lambda: ctx.moe_block(w, dx, y, M, 3, inds, None))
+        assert (host(inds) == ref_i).all()
+        outs.append(host(y))
+    rel, _ = assert_close(outs[0], ref_y, what="row-alpha fold vs oracle")
+    assert rel < 5e-3
+    rel2, _ = assert_close(outs[0], outs[1], what="row-alpha fold vs group scales")
+    assert rel2 < 2e-3
+
+
+def test_moe_block_row_alpha_alignment(ctx):
+    import torch
+
+    from momij_amd._lib import MomijError
+
+    rng = np.random.default_rng(5)
+    mw = _moe_dev(_row_alpha(synth.moe_weights(rng, 16, 2048, 1024, 64)))
+    buf = torch.empty(mw["down_alpha"].numel() + 8, dtype=torch.float16, device="cuda")
+    mw["down_alpha"] = buf[1:1 + mw["down_alpha"].numel()]  # 2-byte offset
+    dx = dev(synth.normal_f16(rng, (4, 2048)))
+    with pytest.raises(MomijError):
+        ctx.moe_block(mw, dx, torch.empty_like(dx), 4, 3)
+
+
 @pytest.mark.parametrize("M", [9, 20, 40])
 def test_moe_block_all_rows_on_each_expert(ctx, orc, M):
     """8 experts with top-8: every row picks every expert, so each expert's gather serves all M
