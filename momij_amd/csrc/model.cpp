@@ -386,6 +386,15 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
                        "model_create: head_bits %d (16, or 4 with scales and biases, H <= 2048)",
                        c.head_bits);
+    for (int l = 0; l < c.n_layers; ++l) {
+        const mj_moe_weights& mw = layers[l].moe;
+        if (!mw.router_w || !mw.up_gate_w || !mw.up_gate_s || !mw.up_gate_b || !mw.down_w ||
+            !mw.down_s || !mw.down_b || !mw.norm_w ||
+            ((uintptr_t)mw.up_gate_alpha | (uintptr_t)mw.down_alpha) % 16 != 0)
+            return mj_fail(ctx, MJ_INVALID_ARG,
+                           "model_create: layer %d expert weights: null pointer or row-alpha "
+                           "array not 16-byte aligned", l);
+    }
     hipSetDevice(ctx->device);
     mj_status s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
     if (s != MJ_OK) return s;

@@ -43,7 +43,7 @@ def maple(tmp_path_factory):
                         for lw in w.layers],
                 embed=h(w.embed), fnorm=h(w.final_norm), head=h(w.lm_head),
                 head_s=h(w.lm_head_scales), head_b=h(w.lm_head_biases))
-    yield dict(ctx=ctx, cfg=cfg, eng=eng, w=host)
+    yield dict(ctx=ctx, cfg=cfg, eng=eng, w=host, dev=dev)
     eng.close()
     ctx.close()
 
@@ -123,3 +123,22 @@ def test_full_attention_capacity_guard(maple):
     with pytest.raises(MomijError):
         eng.verify_greedy(y, [2, 3, 4, 5, 6, 7, 8, 9])
     eng.rewind(0)
+
+
+def test_row_alpha_alignment_checked_at_model_create(maple):
+    """A row-alpha array that is not 16-byte aligned is refused by mj_model_create (the expert
+    kernels load it 16 bytes at a time), before any kernel runs."""
+    import torch
+
+    from momij_amd._lib import MomijError
+    from momij_amd.engine import VerifyEngine
+
+    print("case: misaligned row-alpha array at model create", flush=True)
+    layers, *rest = maple["dev"]
+    bad = [{part: dict(lw[part]) for part in ("attn", "moe")} for lw in layers]
+    a = bad[1]["moe"]["down_alpha"]
+    assert a is not None
+    buf = torch.empty(a.numel() + 8, dtype=torch.float16, device="cuda")
+    bad[1]["moe"]["down_alpha"] = buf[1:1 + a.numel()].view_as(a)
+    with pytest.raises(MomijError):
+        VerifyEngine(maple["ctx"], maple["cfg"], bad, *rest)
