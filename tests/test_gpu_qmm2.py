@@ -142,11 +142,13 @@ def _row_alpha(mw):
 
 
 @pytest.mark.parametrize("E,I,gs,M", [(64, 1024, 64, 8), (16, 1024, 128, 9),
-                                      (128, 1024, 128, 17), (128, 2048, 64, 8)])
+                                      (128, 1024, 128, 17), (128, 2048, 64, 8),
+                                      (64, 1024, 64, 1), (64, 1024, 128, 64)])
 def test_moe_block_row_alpha(ctx, orc, E, I, gs, M):
     """Row-alpha experts: the fold kernels (one alpha per row) against the oracle on the
     expanded scales / biases, and against the group-scale kernels on the same arrays --
-    persistent slot records (E <= 64) and per-expert lists (E = 128), both K widths of down."""
+    persistent slot records (E <= 64) and per-expert lists (E = 128), both K widths of down,
+    up to 64 rows; one row takes the one-row kernels, which read the expanded arrays."""
     import torch
 
     print(f"case: moe row-alpha E={E} I={I} gs={gs} M={M}", flush=True)
