@@ -270,6 +270,23 @@ mj_status mj_verify_sampled(mj_model* model, int32_t y, const int32_t* draft, in
 mj_status mj_model_set_capture(mj_model* model, void* h_capture, int32_t* inds_capture,
                                float* logits_capture);
 
+/* The same capture with every block boundary, so each block can be re-run from the exact
+ * inputs the device used (no counterpart in the reference; its layer-by-layer checks read
+ * MTLBuffers directly).  Device pointers, any may be NULL (all NULL disables); while any is
+ * set, passes run without graphs.  R = MJ_MAX_ROWS, rows beyond the pass's M are untouched. */
+typedef struct mj_capture {
+    void* h;               /* fp16 [n_layers+1][R][H]: after the embedding and after each layer */
+    int32_t* inds;         /* int32 [n_layers][R][top_k]: each layer's routing */
+    float* logits;         /* fp32 [R][V]: lm_head logits */
+    void* attn_out;        /* fp16 [n_layers][R][H]: h after each layer's attention block */
+    void* moe_in;          /* fp16 [n_layers][R][H]: the normed MoE input (router and up gather) */
+    float* router_logits;  /* fp32 [n_layers][R][E]: router logits */
+    void* head_in;         /* fp16 [R][H]: the final-normed rows fed to the lm_head */
+    void* kv_rows;         /* fp16 [n_layers][2][n_kv_heads][R][head_dim]: the K and V rows the
+                              pass appended (row r at slot (L + r) % C), before any commit */
+} mj_capture;
+mj_status mj_model_set_capture_ex(mj_model* model, const mj_capture* cap);
+
 /* Use HIP graphs for verify passes (one graph per row count and mode, replayed with a device
  * step descriptor).  On by default. */
 mj_status mj_model_set_graphs(mj_model* model, int enable);

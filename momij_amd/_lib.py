@@ -13,7 +13,8 @@ LIB_PATH = os.path.join(HERE, "libmomij_hip.so")
 
 MJ_OK = 0
 STATUS = {0: "MJ_OK", 1: "MJ_NO_DEVICE", 2: "MJ_NOT_READY", 3: "MJ_UNSUPPORTED_SHAPE",
-          4: "MJ_INVALID_ARG", 5: "MJ_ABORTED", 6: "MJ_HIP_ERROR", 7: "MJ_CAPACITY"}
+          4: "MJ_INVALID_ARG", 5: "MJ_ABORTED", 6: "MJ_HIP_ERROR", 7: "MJ_CAPACITY",
+          8: "MJ_OUT_OF_MEMORY"}
 MJ_MAX_ROWS = 64
 MJ_EPI_STORE, MJ_EPI_ADD = 0, 1
 MJ_MOE_PRENORM, MJ_MOE_RESIDUAL = 1, 2
@@ -61,6 +62,11 @@ class ModelConfig(C.Structure):
 
 class LayerWeights(C.Structure):
     _fields_ = [("attn", AttnWeights), ("moe", MoeWeights)]
+
+
+class Capture(C.Structure):
+    _fields_ = [("h", vp), ("inds", vp), ("logits", vp), ("attn_out", vp), ("moe_in", vp),
+                ("router_logits", vp), ("head_in", vp), ("kv_rows", vp)]
 
 
 _SIGS = {
@@ -114,6 +120,7 @@ _SIGS = {
     "mj_verify_greedy": (i32, [vp, i32, vp, i32, vp, vp, vp]),
     "mj_verify_sampled": (i32, [vp, i32, vp, i32, f32, i32, vp, u64, u64, vp, vp]),
     "mj_model_set_capture": (i32, [vp, vp, vp, vp]),
+    "mj_model_set_capture_ex": (i32, [vp, C.POINTER(Capture)]),
     "mj_model_set_graphs": (i32, [vp, i32]),
     "mj_model_last_pass_ms": (f32, [vp]),
     "mj_selftest_mfma": (i32, [vp, vp, vp, vp]),

@@ -335,7 +335,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.x = x;
         ra.norm_w = (flags & MJ_MOE_PRENORM) ? (const uint16_t*)w->norm_w : nullptr;
         ra.W = (const uint16_t*)w->router_w;
-        ra.xn = (M == 1 && (flags & MJ_MOE_PRENORM)) ? ms.xn : nullptr;
+        ra.xn = ((M == 1 || ms.want_plain) && (flags & MJ_MOE_PRENORM)) ? ms.xn : nullptr;
         ra.xperm = M > 1 ? ms.xperm : nullptr;
         ra.xsum = M > 1 ? ms.xsum : nullptr;
         ra.inds = inds;

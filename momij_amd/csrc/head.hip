@@ -650,6 +650,28 @@ __global__ __launch_bounds__(256) void k_kv_commit(uint16_t* kv, int64_t layer_s
     }
 }
 
+// Debug capture: the K and V rows a pass appended, dst [n_layers][2][nKV][R][128] (R =
+// MJ_ROWS), block per (layer, K|V, kv head).
+__global__ __launch_bounds__(256) void k_kv_rows(const uint16_t* kv, int64_t layer_stride, int64_t C,
+                                                 int nKV, const StepDesc* sd, uint16_t* dst) {
+    const int layer = blockIdx.x / (2 * nKV), rest = blockIdx.x % (2 * nKV);
+    const uint16_t* base = kv + layer * layer_stride + (int64_t)rest * C * 128;
+    uint16_t* out = dst + ((size_t)layer * 2 * nKV + rest) * MJ_ROWS * 128;
+    const int64_t L = sd->L;
+    for (int idx = threadIdx.x; idx < sd->M * 16; idx += 256) {
+        const int r = idx >> 4, part = idx & 15;
+        *(u4v*)(out + (size_t)r * 128 + 8 * part) =
+            *(const u4v*)(base + ((L + r) % C) * 128 + 8 * part);
+    }
+}
+
+hipError_t launch_kv_rows(const uint16_t* kv, int64_t layer_stride, int n_layers, int64_t C,
+                          int nKV, const StepDesc* sd, uint16_t* dst, hipStream_t st) {
+    hipLaunchKernelGGL(k_kv_rows, dim3(n_layers * 2 * nKV), dim3(256), 0, st, kv, layer_stride, C,
+                       nKV, sd, dst);
+    return hipGetLastError();
+}
+
 hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, int64_t C, int nKV,
                             const StepDesc* sd, const StepResult* res, const int* abort,
                             hipStream_t st) {

@@ -38,6 +38,7 @@ struct MoeScratch {
     int* ecnt;           // pairs per expert [E]
     int* eplist;         // pair lists per expert [E][MJ_ROWS]
     int* srec;           // routed-expert slot records [64][64] (E <= 64)
+    bool want_plain = false;  // also write the normed rows plain into xn (debug capture)
 };
 
 // Optional per-kernel-class event timing of eager passes (classes of mj_model_kernel_ms).

@@ -193,6 +193,8 @@ hipError_t launch_accept_greedy(const int32_t* tokens, const int32_t* parents,
 hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, int64_t C, int nKV,
                             const StepDesc* sd, const StepResult* res, const int* abort,
                             hipStream_t st);
+hipError_t launch_kv_rows(const uint16_t* kv, int64_t layer_stride, int n_layers, int64_t C,
+                          int nKV, const StepDesc* sd, uint16_t* dst, hipStream_t st);
 hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
                         const int* abort, hipStream_t st);
 hipError_t launch_embed_norm(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,

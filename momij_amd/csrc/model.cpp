@@ -50,9 +50,7 @@ struct mj_model {
     int64_t offset = 0;
     bool graphs = true;
     std::map<int, hipGraphExec_t> graph_cache;
-    void* cap_h = nullptr;
-    int32_t* cap_inds = nullptr;
-    float* cap_logits = nullptr;
+    mj_capture cap{};  // debug capture (device pointers; all null: off)
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     float last_ms = -1.0f;
     bool profiling = false;
@@ -176,6 +174,12 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, int kind, hipStream_t 
     s = mj_hip(ctx, launch_gather(o, EPI_ADD, M, 1, st), "o proj");
     if (pf) pf->end(st);
     if (s != MJ_OK) return s;
+    const size_t rowsH = (size_t)MJ_MAX_ROWS * H;
+    if (m->cap.attn_out) {
+        s = mj_hip(ctx, hipMemcpyAsync((uint16_t*)m->cap.attn_out + l * rowsH, m->h, (size_t)M * H * 2,
+                                       hipMemcpyDeviceToDevice, st), "capture");
+        if (s != MJ_OK) return s;
+    }
     int32_t* inds = m->inds_all + (size_t)l * MJ_MAX_ROWS * c.top_k;
     float* scores = m->scores_all + (size_t)l * MJ_MAX_ROWS * c.top_k;
     NormOut next{};
@@ -185,8 +189,22 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, int kind, hipStream_t 
                        m->xsum};
     else
         next = NormOut{m->final_norm, c.eps, m->xf, nullptr, nullptr};
-    return run_moe(ctx, &w.moe, m->h, m->h, M, MJ_MOE_PRENORM | MJ_MOE_RESIDUAL, m->ms, inds,
-                   scores, st, pf, (last && kind == PASS_PREFILL) ? nullptr : &next);
+    s = run_moe(ctx, &w.moe, m->h, m->h, M, MJ_MOE_PRENORM | MJ_MOE_RESIDUAL, m->ms, inds,
+                scores, st, pf, (last && kind == PASS_PREFILL) ? nullptr : &next);
+    if (s != MJ_OK) return s;
+    // the route wrote the normed rows plain into ms.xn (want_plain) and the logits into ms.logits
+    if (m->cap.moe_in) {
+        s = mj_hip(ctx, hipMemcpyAsync((uint16_t*)m->cap.moe_in + l * rowsH, m->ms.xn,
+                                       (size_t)M * H * 2, hipMemcpyDeviceToDevice, st), "capture");
+        if (s != MJ_OK) return s;
+    }
+    if (m->cap.router_logits) {
+        s = mj_hip(ctx, hipMemcpyAsync(m->cap.router_logits + (size_t)l * MJ_MAX_ROWS * c.E,
+                                       m->ms.logits, (size_t)M * c.E * 4, hipMemcpyDeviceToDevice,
+                                       st), "capture");
+        if (s != MJ_OK) return s;
+    }
+    return MJ_OK;
 }
 
 static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
@@ -207,31 +225,42 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                               H, ab, st), "attn norm");
     }
     if (s != MJ_OK) return s;
-    if (m->cap_h) {
-        s = mj_hip(ctx, hipMemcpyAsync(m->cap_h, m->h, (size_t)M * H * 2, hipMemcpyDeviceToDevice,
+    if (m->cap.h) {
+        s = mj_hip(ctx, hipMemcpyAsync(m->cap.h, m->h, (size_t)M * H * 2, hipMemcpyDeviceToDevice,
                                        st), "capture");
         if (s != MJ_OK) return s;
     }
     for (int l = 0; l < c.n_layers; ++l) {
         s = enqueue_layer(m, l, M, kind, st);
         if (s != MJ_OK) return s;
-        if (m->cap_h) {
-            s = mj_hip(ctx, hipMemcpyAsync((uint16_t*)m->cap_h + (size_t)(l + 1) * MJ_MAX_ROWS * H,
+        if (m->cap.h) {
+            s = mj_hip(ctx, hipMemcpyAsync((uint16_t*)m->cap.h + (size_t)(l + 1) * MJ_MAX_ROWS * H,
                                            m->h, (size_t)M * H * 2, hipMemcpyDeviceToDevice, st),
                        "capture");
             if (s != MJ_OK) return s;
         }
-        if (m->cap_inds) {
-            s = mj_hip(ctx, hipMemcpyAsync(m->cap_inds + (size_t)l * MJ_MAX_ROWS * c.top_k,
+        if (m->cap.inds) {
+            s = mj_hip(ctx, hipMemcpyAsync(m->cap.inds + (size_t)l * MJ_MAX_ROWS * c.top_k,
                                            m->inds_all + (size_t)l * MJ_MAX_ROWS * c.top_k,
                                            (size_t)M * c.top_k * 4, hipMemcpyDeviceToDevice, st),
                        "capture");
             if (s != MJ_OK) return s;
         }
     }
+    if (m->cap.kv_rows) {
+        s = mj_hip(ctx, launch_kv_rows(m->kv, m->layer_stride, c.n_layers, c.kv_capacity,
+                                       c.n_kv_heads, m->sd_dev, (uint16_t*)m->cap.kv_rows, st),
+                   "capture");
+        if (s != MJ_OK) return s;
+    }
     if (kind != PASS_PREFILL) {
         // the last layer's expert combine wrote the final norm into xf
-        float* logits = (kind == PASS_SAMPLED || m->cap_logits) ? m->logits : nullptr;
+        if (m->cap.head_in) {
+            s = mj_hip(ctx, hipMemcpyAsync(m->cap.head_in, m->xf, (size_t)M * H * 2,
+                                           hipMemcpyDeviceToDevice, st), "capture");
+            if (s != MJ_OK) return s;
+        }
+        float* logits = (kind == PASS_SAMPLED || m->cap.logits) ? m->logits : nullptr;
         if (m->profiling) m->prof.begin(PROF_HEAD, st);
         if (c.head_bits == 4)
             s = mj_hip(ctx,
@@ -246,8 +275,8 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                        "lm_head");
         if (m->profiling) m->prof.end(st);
         if (s != MJ_OK) return s;
-        if (m->cap_logits) {
-            s = mj_hip(ctx, hipMemcpyAsync(m->cap_logits, m->logits, (size_t)M * c.vocab * 4,
+        if (m->cap.logits) {
+            s = mj_hip(ctx, hipMemcpyAsync(m->cap.logits, m->logits, (size_t)M * c.vocab * 4,
                                            hipMemcpyDeviceToDevice, st), "capture");
             if (s != MJ_OK) return s;
         }
@@ -282,8 +311,10 @@ static mj_status run_pass(mj_model* m, int kind, int M) {
     mj_status s = mj_hip(ctx, hipMemcpyAsync(m->sd_dev, m->sd_host, sizeof(StepDesc),
                                              hipMemcpyHostToDevice, st), "descriptor upload");
     if (s != MJ_OK) return s;
-    const bool capture_ok =
-        m->graphs && !m->cap_h && !m->cap_inds && !m->cap_logits && !m->profiling;
+    const mj_capture& cp = m->cap;
+    const bool capturing = cp.h || cp.inds || cp.logits || cp.attn_out || cp.moe_in ||
+                           cp.router_logits || cp.head_in || cp.kv_rows;
+    const bool capture_ok = m->graphs && !capturing && !m->profiling;
     m->prof.used = 0;
     // A profiled pass is queued behind a hold, so every kernel starts as soon as its
     // predecessor ends: its event pair then brackets the kernel, not the host's launch gap.
@@ -525,9 +556,18 @@ mj_status mj_model_kv(mj_model* m, int layer, void** k, void** v) {
 
 mj_status mj_model_set_capture(mj_model* m, void* h, int32_t* inds, float* logits) {
     if (!m) return MJ_INVALID_ARG;
-    m->cap_h = h;
-    m->cap_inds = inds;
-    m->cap_logits = logits;
+    m->cap = mj_capture{};
+    m->cap.h = h;
+    m->cap.inds = inds;
+    m->cap.logits = logits;
+    m->ms.want_plain = false;
+    return MJ_OK;
+}
+
+mj_status mj_model_set_capture_ex(mj_model* m, const mj_capture* cap) {
+    if (!m) return MJ_INVALID_ARG;
+    m->cap = cap ? *cap : mj_capture{};
+    m->ms.want_plain = m->cap.moe_in != nullptr;
     return MJ_OK;
 }
 

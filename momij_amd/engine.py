@@ -135,6 +135,32 @@ class VerifyEngine:
     def set_capture(self, h=None, inds=None, logits=None):
         self.ctx.check(self.lib.mj_model_set_capture(self.h, ptr(h), ptr(inds), ptr(logits)))
 
+    def set_capture_ex(self, **bufs):
+        """Capture every block boundary (mj_capture field names: h, inds, logits, attn_out,
+        moe_in, router_logits, head_in, kv_rows); no arguments switches capture off."""
+        cap = _lib.Capture(*[ptr(bufs.get(f)) for f, _ in _lib.Capture._fields_])
+        self._capture = bufs  # the device buffers outlive the capture
+        self.ctx.check(self.lib.mj_model_set_capture_ex(self.h, C.byref(cap)))
+
+    def capture_buffers(self, logits: bool = True) -> dict:
+        """Device buffers for set_capture_ex at this configuration (torch tensors; the row
+        stride is MJ_MAX_ROWS)."""
+        import torch
+
+        c, R = self.cfg, _lib.MJ_MAX_ROWS
+        f16 = dict(dtype=torch.float16, device="cuda")
+        out = dict(h=torch.zeros((c.n_layers + 1, R, c.H), **f16),
+                   inds=torch.zeros((c.n_layers, R, c.top_k), dtype=torch.int32, device="cuda"),
+                   attn_out=torch.zeros((c.n_layers, R, c.H), **f16),
+                   moe_in=torch.zeros((c.n_layers, R, c.H), **f16),
+                   router_logits=torch.zeros((c.n_layers, R, c.E), dtype=torch.float32,
+                                             device="cuda"),
+                   head_in=torch.zeros((R, c.H), **f16),
+                   kv_rows=torch.zeros((c.n_layers, 2, c.n_kv_heads, R, c.head_dim), **f16))
+        if logits:
+            out["logits"] = torch.zeros((R, c.vocab), dtype=torch.float32, device="cuda")
+        return out
+
     def last_pass_ms(self) -> float:
         return float(self.lib.mj_model_last_pass_ms(self.h))
 

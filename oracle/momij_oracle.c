@@ -467,6 +467,39 @@ void or_layer_forward(const or_cfg* cfg, const or_layer_w* w, const float* inv_f
 }
 
 /* ------------------------------------------------------------------------- */
+/* KV commit after a tree verify.  The reference's reject rollback rewinds the  */
+/* offset over append-only writes (rewindOffset / snapshotForChain,             */
+/* SeedlessAttn.swift:219-225, 319-322, 540-586); a draft tree also has to move  */
+/* the accepted path into consecutive positions so the cache reads as if the    */
+/* path had been fed as a chain: the K and V rows written at slot               */
+/* (L + path[i]) % C go to slot (L + i) % C, i = 0 .. n_path-1, every source    */
+/* read before any destination is written.  Caches [nKV][C][D].                 */
+/* ------------------------------------------------------------------------- */
+void or_kv_commit(uint16_t* kcache, uint16_t* vcache, int nKV, int64_t C, int D, int64_t L,
+                  const int32_t* path, int n_path) {
+    uint16_t* rows = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)2 * nKV * n_path * D);
+    for (int c = 0; c < 2; ++c) {
+        uint16_t* cache = c == 0 ? kcache : vcache;
+        for (int g = 0; g < nKV; ++g)
+            for (int i = 0; i < n_path; ++i) {
+                const int64_t src = (L + path[i]) % C;
+                memcpy(rows + (((size_t)c * nKV + g) * n_path + i) * D,
+                       cache + ((size_t)g * C + (size_t)src) * D, sizeof(uint16_t) * (size_t)D);
+            }
+    }
+    for (int c = 0; c < 2; ++c) {
+        uint16_t* cache = c == 0 ? kcache : vcache;
+        for (int g = 0; g < nKV; ++g)
+            for (int i = 0; i < n_path; ++i) {
+                const int64_t dst = (L + i) % C;
+                memcpy(cache + ((size_t)g * C + (size_t)dst) * D,
+                       rows + (((size_t)c * nKV + g) * n_path + i) * D, sizeof(uint16_t) * (size_t)D);
+            }
+    }
+    free(rows);
+}
+
+/* ------------------------------------------------------------------------- */
 /* a7: lm_head -- maple_lm_head_argmax semantics (SeedlessMetal.swift:3005-3111)  */
 /* with an fp16 weight: logits = sum_k w[v,k] * x[m,k].  Accumulated in double   */
 /* here (closest to the exact value) and rounded once to float.                  */

@@ -21,6 +21,12 @@
  *   or_splitmix64          published SplitMix64 vectors (seed 1234567)
  *   or_try_accept/walk     SpeculativeSamplingTests.swift:5-45, 94-137 KATs
  *   or_canon_expf          libm expf within 2 ulp on a dense grid
+ *   or_moe_block, or_attn_block, or_layer_forward, or_score_resid
+ *                          float64 numpy restatement at the reference's fp16 rounding points
+ *                          (tests/restate64.py), with planted-mistake negative controls; the
+ *                          double rounding of the residual by an exact special case
+ *   or_kv_commit           a tree verify + commit leaves the cache a chain verify of the
+ *                          accepted path leaves, bit for bit; a chain path is the identity
  */
 #ifndef MOMIJ_ORACLE_H
 #define MOMIJ_ORACLE_H
@@ -160,6 +166,10 @@ typedef struct or_layer_w {
 void or_layer_forward(const or_cfg* cfg, const or_layer_w* w, const float* inv_freq, uint16_t* h,
                       uint16_t* kcache, uint16_t* vcache, int64_t L, const int32_t* parents, int M,
                       int32_t* out_inds, float* out_scores);
+/* accepted tree path compacted into consecutive positions (SeedlessAttn.swift:219-225,
+ * 540-586): rows at slot (L + path[i]) % C move to (L + i) % C; caches [nKV][C][D] */
+void or_kv_commit(uint16_t* kcache, uint16_t* vcache, int nKV, int64_t C, int D, int64_t L,
+                  const int32_t* path, int n_path);
 
 #ifdef __cplusplus
 }

@@ -72,6 +72,7 @@ def lib():
         L.or_moe_block.argtypes = [vp, vp, vp, i, i, vp, vp]
         L.or_layer_forward.argtypes = [vp, vp, vp, vp, vp, vp, C.c_int64, vp, i, vp, vp]
         L.or_attn_block.argtypes = [vp, vp, vp, vp, vp, vp, C.c_int64, vp, i]
+        L.or_kv_commit.argtypes = [vp, vp, i, C.c_int64, i, C.c_int64, vp, i]
         L.or_lm_head_logits.argtypes = [vp, vp, vp, i, i, i]
         L.or_lm_head_q4_logits.argtypes = [vp, vp, vp, vp, vp, i, i, i]
         L.or_argmax_rows.argtypes = [vp, i, i, vp, i, vp, vp, vp]
@@ -133,6 +134,17 @@ def score_reduce(down, scores, M, ktop, H):
     y = np.empty((M, H), np.float16)
     lib().or_score_reduce(down.ctypes.data, scores.ctypes.data, y.ctypes.data, M, ktop, H)
     return y
+
+
+def score_resid(down, scores, h):
+    """h + combine of the expert rows (two fp16 roundings); down [M*k][H], scores [M][k]."""
+    scores = _c(scores, np.float32)
+    M, k = scores.shape
+    down = _c(down, np.float16)
+    out = np.array(h, dtype=np.float16, copy=True, order="C")
+    lib().or_score_resid(down.ctypes.data, scores.ctypes.data, out.ctypes.data, M, k,
+                         out.shape[1])
+    return out
 
 
 def rms_norm(x, w, eps):
@@ -301,6 +313,17 @@ def layer_forward(cfg: dict, lw: dict, h, kcache, vcache, L, parents):
                            kc.ctypes.data, vc.ctypes.data, C.c_int64(L), par.ctypes.data, M,
                            inds.ctypes.data, scores.ctypes.data)
     return h, kc, vc, inds, scores
+
+
+def kv_commit(kcache, vcache, L, path):
+    """Accepted tree path moved into consecutive positions; caches [nKV][C][D], returns copies."""
+    kc = np.array(kcache, dtype=np.float16, copy=True, order="C")
+    vc = np.array(vcache, dtype=np.float16, copy=True, order="C")
+    nKV, Cs, D = kc.shape
+    p = _c(path, np.int32)
+    lib().or_kv_commit(kc.ctypes.data, vc.ctypes.data, nKV, C.c_int64(Cs), D, C.c_int64(L),
+                       p.ctypes.data, len(p))
+    return kc, vc
 
 
 def lm_head_logits(x, w):
