@@ -19,6 +19,10 @@ from tests.teacher import capture_pass, check_head, check_layer
 
 pytestmark = pytest.mark.gpu
 
+# absolute bound of the free-running comparisons (8 fp16 ulps at magnitude 4); the
+# teacher-forced block checks keep the 1e-2 bar
+FREE_RUN_ABS = 3.2e-2
+
 
 @pytest.fixture(scope="module")
 def maple(tmp_path_factory):
@@ -97,7 +101,8 @@ def test_maple_checkpoint_prefill_and_verify(maple, orc):
     om.prefill(prompt[:-1])
     xf = om.rows(prompt[-1:], [-1])
     om.L += 1
-    assert_close(cap["head_in"][35:36], xf, what="prefill head input (free-running)")
+    assert_close(cap["head_in"][35:36], xf, abs_tol=FREE_RUN_ABS,
+                 what="prefill head input (free-running)")
     L0 = eng.offset
     cont, t = [], y
     for _ in range(8):
@@ -118,8 +123,10 @@ def test_maple_checkpoint_prefill_and_verify(maple, orc):
     am, _ = check_head(orc, cap["head_in"][:9], gpu_am, "verify", q4=q4)
     oacc, _, oemit = orc.accept_greedy([y] + draft, None, am)
     assert oacc == acc and list(oemit) == toks
+    # the free-running replay accumulates both sides' rounding over 4 layers and 109 positions:
+    # the relative bar holds, single elements of magnitude ~4 may drift by a few fp16 ulps
     xf = om.rows([y] + draft, parents)
-    assert_close(cap["head_in"][:9], xf, what="verify head input (free-running)")
+    assert_close(cap["head_in"][:9], xf, abs_tol=FREE_RUN_ABS, what="verify head input (free-running)")
 
 
 def test_full_attention_capacity_guard(maple):
