@@ -116,6 +116,19 @@ typedef struct mj_moe_weights {
 mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y, int M,
                        int flags, int32_t* out_inds, float* out_scores);
 
+/* mj_moe_block without any device allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same kernels, arguments and results as mj_moe_block, with the
+ * scratch in one statically allocated device array of MJ_MOE_NOALLOC_BYTES per GPU (held until
+ * the process ends) instead of the context's growable scratch.  A call whose scratch would
+ * exceed it (M rows x top_k x (I + H) halves dominate: H <= 2048 fits any I <= 4096 at
+ * M = 64) is refused with MJ_CAPACITY before any work is queued.  Every call on one GPU shares
+ * that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (from
+ * several contexts or streams) race. */
+#define MJ_MOE_NOALLOC_BYTES (8u << 20)
+mj_status mj_moe_block_noalloc(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y,
+                               int M, int flags, int32_t* out_inds, float* out_scores);
+
 /* Attention weights of one layer (SeedlessAttn.swift:74-92). */
 typedef struct mj_attn_weights {
     const void* norm_w;      /* fp16 [H] input_layernorm */

@@ -16,6 +16,7 @@ STATUS = {0: "MJ_OK", 1: "MJ_NO_DEVICE", 2: "MJ_NOT_READY", 3: "MJ_UNSUPPORTED_S
           4: "MJ_INVALID_ARG", 5: "MJ_ABORTED", 6: "MJ_HIP_ERROR", 7: "MJ_CAPACITY",
           8: "MJ_OUT_OF_MEMORY"}
 MJ_MAX_ROWS = 64
+MJ_MOE_NOALLOC_BYTES = 8 << 20
 MJ_EPI_STORE, MJ_EPI_ADD = 0, 1
 MJ_MOE_PRENORM, MJ_MOE_RESIDUAL = 1, 2
 MJ_Q_POINT, MJ_Q_UNIFORM = 0, 1
@@ -85,6 +86,7 @@ _SIGS = {
     "mj_d2h": (i32, [vp, vp, vp, C.c_size_t]),
     "mj_gather_qmm2": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32]),
     "mj_moe_block": (i32, [vp, C.POINTER(MoeWeights), vp, vp, i32, i32, vp, vp]),
+    "mj_moe_block_noalloc": (i32, [vp, C.POINTER(MoeWeights), vp, vp, i32, i32, vp, vp]),
     "mj_attn_block": (i32, [vp, C.POINTER(AttnConfig), C.POINTER(AttnWeights), vp, vp, vp, i64,
                             vp, i32]),
     "mj_lm_head_verify": (i32, [vp, vp, vp, i32, i32, i32, vp, i32, vp, vp, vp]),

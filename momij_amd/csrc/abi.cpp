@@ -9,11 +9,37 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/momij_hip.h"
 #include "mj_abi_internal.h"
 #include "mj_internal.h"
+
+// Scratch of mj_moe_block_noalloc: one statically allocated array per GPU, held until the
+// process ends.  Host code never uses its name as an address (that is a host-side stand-in);
+// the device address comes from hipGetSymbolAddress, once per device at mj_init.
+static __device__ __align__(256) char scratch[MJ_MOE_NOALLOC_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};       // device address of `scratch`, per device
+hipError_t g_scratch_err[kMaxDevices] = {};  // the lookup's result, per device
+bool g_scratch_done[kMaxDevices] = {};
+
+// with `device` current: look the array's address up once for this device
+void resolve_static_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_done[device]) return;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_err[device] = e;
+    g_scratch_dev[device] = e == hipSuccess ? p : nullptr;
+    g_scratch_done[device] = true;
+}
+}  // namespace
 
 TimedLaunch& timed_launch() {
     static thread_local TimedLaunch t;
@@ -99,6 +125,7 @@ mj_status mj_init(int device, mj_ctx** out) {
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return MJ_NO_DEVICE;
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return MJ_NO_DEVICE;
     if (hipSetDevice(device) != hipSuccess) return MJ_NO_DEVICE;
+    resolve_static_scratch(device);
     mj_ctx* c = new mj_ctx();
     c->device = device;
     if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
@@ -251,9 +278,9 @@ mj_status mj_gather_qmm2(mj_ctx* ctx, const void* x, const uint32_t* w, const vo
                                      ctx->stream), "gather launch");
 }
 
-mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y, int M,
-                       int flags, int32_t* out_inds, float* out_scores) {
-    if (!ctx) return MJ_INVALID_ARG;
+// Arguments and shape of an MoE block call (shared by mj_moe_block and its no-alloc variant).
+static mj_status check_moe_args(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y,
+                                int M, int flags) {
     if (!w || !x || !y || M < 1 || M > MJ_MAX_ROWS)
         return mj_fail(ctx, MJ_INVALID_ARG, "moe_block: null pointer or M outside 1..%d",
                        MJ_MAX_ROWS);
@@ -268,14 +295,57 @@ mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void
         return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
                        "moe_block: unsupported shape H=%d I=%d E=%d top_k=%d gs=%d", H, I, E, k,
                        gs);
-    hipSetDevice(ctx->device);
-    {
-        mj_status sa = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
-        if (sa != MJ_OK) return sa;
-    }
-    MoeScratch ms;
-    mj_status s = moe_scratch(ctx, H, I, E, k, M, ms);
+    return MJ_OK;
+}
+
+mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y, int M,
+                       int flags, int32_t* out_inds, float* out_scores) {
+    if (!ctx) return MJ_INVALID_ARG;
+    mj_status s = check_moe_args(ctx, w, x, y, M, flags);
     if (s != MJ_OK) return s;
+    hipSetDevice(ctx->device);
+    s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
+    if (s != MJ_OK) return s;
+    MoeScratch ms;
+    s = moe_scratch(ctx, w->H, w->I, w->E, w->top_k, M, ms);
+    if (s != MJ_OK) return s;
+    return run_moe(ctx, w, (const uint16_t*)x, (uint16_t*)y, M, flags, ms,
+                   out_inds ? out_inds : ms.inds, out_scores ? out_scores : ms.scores,
+                   ctx->stream);
+}
+
+mj_status mj_moe_block_noalloc(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y,
+                               int M, int flags, int32_t* out_inds, float* out_scores) {
+    if (!ctx) return MJ_INVALID_ARG;
+    mj_status s = check_moe_args(ctx, w, x, y, M, flags);
+    if (s != MJ_OK) return s;
+    const int dev = ctx->device;
+    void* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        if (dev >= 0 && dev < kMaxDevices && g_scratch_done[dev]) {
+            if (g_scratch_err[dev] != hipSuccess)
+                return mj_fail(ctx, MJ_HIP_ERROR, "moe_block_noalloc: static scratch address: %s",
+                               hipGetErrorString(g_scratch_err[dev]));
+            base = g_scratch_dev[dev];
+        }
+    }
+    if (!base)
+        return mj_fail(ctx, MJ_NOT_READY, "moe_block_noalloc: no static scratch on device %d",
+                       dev);
+    Arena count;
+    MoeScratch ms;
+    moe_scratch_layout(count, w->H, w->I, w->E, w->top_k, M, ms);
+    if (count.off > MJ_MOE_NOALLOC_BYTES)
+        return mj_fail(ctx, MJ_CAPACITY,
+                       "moe_block_noalloc: scratch of %zu bytes for M=%d H=%d I=%d E=%d top_k=%d "
+                       "exceeds MJ_MOE_NOALLOC_BYTES (%u)", count.off, M, w->H, w->I, w->E,
+                       w->top_k, (unsigned)MJ_MOE_NOALLOC_BYTES);
+    hipSetDevice(dev);
+    s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
+    if (s != MJ_OK) return s;
+    Arena real{base, 0};
+    moe_scratch_layout(real, w->H, w->I, w->E, w->top_k, M, ms);
     return run_moe(ctx, w, (const uint16_t*)x, (uint16_t*)y, M, flags, ms,
                    out_inds ? out_inds : ms.inds, out_scores ? out_scores : ms.scores,
                    ctx->stream);
@@ -293,28 +363,29 @@ mj_status mj_selftest_mfma(mj_ctx* ctx, const void* A, const void* B, float* D) 
 // ----------------------------------------------------------------------------------------
 // MoE block orchestration (shared with the model pass).
 // ----------------------------------------------------------------------------------------
+void moe_scratch_layout(Arena& a, int H, int I, int E, int k, int M, MoeScratch& ms) {
+    ms.xn = (uint16_t*)a.take((size_t)M * H * 2);
+    ms.xperm = (uint16_t*)a.take((size_t)M * H * 2);
+    ms.xsum = (float2*)a.take((size_t)M * (H / 64) * sizeof(float2));
+    ms.logits = (float*)a.take((size_t)M * E * 4);
+    ms.inds = (int32_t*)a.take((size_t)M * k * 4);
+    ms.scores = (float*)a.take((size_t)M * k * 4);
+    ms.bk = (Buckets*)a.take(sizeof(Buckets));
+    ms.act = (uint16_t*)a.take((size_t)M * k * I * 2);
+    ms.act_sum = (float2*)a.take((size_t)M * k * (I / 64) * sizeof(float2));
+    ms.down = (uint16_t*)a.take((size_t)M * k * H * 2);
+    ms.ecnt = (int*)a.take((size_t)E * 4);
+    ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
+    ms.srec = (int*)a.take((size_t)64 * 64 * 4);
+}
+
 mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms) {
-    Arena ar;
-    auto layout = [&](Arena& a) {
-        ms.xn = (uint16_t*)a.take((size_t)M * H * 2);
-        ms.xperm = (uint16_t*)a.take((size_t)M * H * 2);
-        ms.xsum = (float2*)a.take((size_t)M * (H / 64) * sizeof(float2));
-        ms.logits = (float*)a.take((size_t)M * E * 4);
-        ms.inds = (int32_t*)a.take((size_t)M * k * 4);
-        ms.scores = (float*)a.take((size_t)M * k * 4);
-        ms.bk = (Buckets*)a.take(sizeof(Buckets));
-        ms.act = (uint16_t*)a.take((size_t)M * k * I * 2);
-        ms.act_sum = (float2*)a.take((size_t)M * k * (I / 64) * sizeof(float2));
-        ms.down = (uint16_t*)a.take((size_t)M * k * H * 2);
-        ms.ecnt = (int*)a.take((size_t)E * 4);
-        ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
-        ms.srec = (int*)a.take((size_t)64 * 64 * 4);
-    };
-    layout(ar);
-    mj_status s = mj_scratch_reserve(ctx, ar.off);
+    Arena count;
+    moe_scratch_layout(count, H, I, E, k, M, ms);
+    mj_status s = mj_scratch_reserve(ctx, count.off);
     if (s != MJ_OK) return s;
     Arena real{ctx->scratch, 0};
-    layout(real);
+    moe_scratch_layout(real, H, I, E, k, M, ms);
     return MJ_OK;
 }
 

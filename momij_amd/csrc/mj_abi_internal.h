@@ -72,6 +72,8 @@ mj_status mj_fail(mj_ctx* ctx, mj_status st, const char* fmt, ...);
 mj_status mj_hip(mj_ctx* ctx, hipError_t e, const char* what);
 mj_status mj_scratch_reserve(mj_ctx* ctx, size_t bytes);
 mj_status mj_check_abort(mj_ctx* ctx);
+// Scratch of an MoE block call laid out over an arena (base nullptr: size counting only).
+void moe_scratch_layout(Arena& a, int H, int I, int E, int k, int M, MoeScratch& ms);
 mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms);
 // next: also normalise the block's output y into these outputs (the following RMSNorm).
 mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,

@@ -76,6 +76,12 @@ class Context:
         self.check(self.lib.mj_moe_block(self.h, C.byref(st), ptr(x), ptr(y), M, flags, ptr(inds),
                                          ptr(scores)))
 
+    def moe_block_noalloc(self, mw: dict, x, y, M, flags=0, inds=None, scores=None):
+        """mj_moe_block over the library's static per-GPU scratch (no device allocation)."""
+        st = self.moe_struct(mw)
+        self.check(self.lib.mj_moe_block_noalloc(self.h, C.byref(st), ptr(x), ptr(y), M, flags,
+                                                 ptr(inds), ptr(scores)))
+
     @staticmethod
     def attn_struct(aw: dict) -> AttnWeights:
         return AttnWeights(ptr(aw["norm_w"]), ptr(aw["qkv_w"]), ptr(aw["qkv_s"]), ptr(aw["qkv_b"]),
