@@ -94,12 +94,14 @@ typedef struct mj_moe_weights {
     const uint32_t* down_w;    /* [E][H][I/16] */
     const void* down_s;        /* fp16 [E][H][I/gs] */
     const void* down_b;
-    int E, top_k, H, I, gs;
+    int E, top_k, H, I, gs;  /* H 2048 or 4096; I a multiple of 512, <= 4096; gs 64 or 128 */
     float eps;
     /* optional row-alpha form (WeightStore.swift:47-63: scales = alpha in every group of a
      * row, biases = -alpha): fp16 [E][2I] and [E][H], 16-byte aligned, or NULL.  When set,
-     * up_gate_s/_b and down_s/_b must hold that expansion; the batched expert kernels then
-     * read one alpha per row instead of the group scales and biases. */
+     * up_gate_s/_b and down_s/_b must still hold that expansion: the batched expert kernels
+     * read one alpha per row, the one-row and general kernels read the arrays, and the two are
+     * not compared (an alpha that is not the arrays' expansion makes decode and verify
+     * disagree). */
     const void* up_gate_alpha;
     const void* down_alpha;
 } mj_moe_weights;

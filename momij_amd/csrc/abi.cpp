@@ -228,7 +228,7 @@ mj_status mj_gather_qmm2(mj_ctx* ctx, const void* x, const uint32_t* w, const vo
         if (sa != MJ_OK) return sa;
     }
     const int P = M * ktop;
-    if (P == 1 && epilogue == MJ_EPI_STORE && (K == 1024 || K == 2048 || K == 4096)) {
+    if (P == 1 && epilogue == MJ_EPI_STORE && (K == 512 || K == 1024 || K == 2048 || K == 4096)) {
         QmvArgs a{};
         a.x = (const uint16_t*)x;
         a.w = w;
@@ -290,7 +290,7 @@ static mj_status check_moe_args(mj_ctx* ctx, const mj_moe_weights* w, const void
     if (((uintptr_t)w->up_gate_alpha | (uintptr_t)w->down_alpha) % 16 != 0)
         return mj_fail(ctx, MJ_INVALID_ARG, "moe_block: row-alpha arrays must be 16-byte aligned");
     const int H = w->H, I = w->I, E = w->E, k = w->top_k, gs = w->gs;
-    if (H % 2048 != 0 || H > 4096 || I % 1024 != 0 || I > 4096 || E < k || E > MJ_MAX_EXPERTS ||
+    if (H % 2048 != 0 || H > 4096 || I % 512 != 0 || I > 4096 || E < k || E > MJ_MAX_EXPERTS ||
         k < 1 || k > 8 || (gs != 64 && gs != 128))
         return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE,
                        "moe_block: unsupported shape H=%d I=%d E=%d top_k=%d gs=%d", H, I, E, k,

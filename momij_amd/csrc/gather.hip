@@ -30,6 +30,11 @@ __device__ __forceinline__ void load_lds16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
 }
 
+// 4 bytes per lane, landing at lds + 4 * lane
+__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 4, 0, 0);
+}
+
 // Launch shape: R = 16 activation rows at most per pass (the MFMA M dimension), RA <= R rows
 // staged in LDS per pass (a bucket with more rows takes several passes; `multi` says whether
 // any can), K = 256 * KPL.  A block has WPB waves = TPB tiles of 16
@@ -43,13 +48,17 @@ struct G5Shape {
     static constexpr int TPB = WPB / KS;       // weight tiles per block
     static constexpr int XS = K + 8;           // LDS row stride of activations (halves)
     static constexpr int SCH = K / GS / 8;     // 16-byte scale chunks per weight row
-    static constexpr int SCW = SCH / KS;       // ... per K-slice
+    // K / GS == 4 (K = 512, group 128): a row's scales are 8 bytes, half a chunk; they are
+    // staged 8 bytes a row and read as chunk 0 with its upper half zero
+    static constexpr bool HSC = SCH == 0;
+    static constexpr int SCW = HSC ? 1 : SCH / KS;  // ... per K-slice
     static constexpr int ES = 129;             // QKV epilogue staging stride (floats)
     static constexpr int WCODE = 16 * KBW * 16;  // bytes of one wave's code tile
     static constexpr int WSB = 16 * SCW * 16;    // bytes of one wave's scales (and of its biases)
     static constexpr int WAVE_BYTES = WCODE + 2 * WSB;
     static constexpr int SS = KB + 2;          // LDS row stride of block sums (float2)
     static_assert(WAVE_BYTES >= 64 * 16, "a K-slice partial fits in its wave's tile area");
+    static_assert(!HSC || (K / GS == 4 && KS == 1), "half-chunk scales: one K-slice of 4 groups");
     // K-slice partials: in a wave's own tile area when every bucket is one pass, else in their
     // own region (later passes reuse the tiles)
     static constexpr int RED = (KS - 1) * TPB * 64 * 16;
@@ -245,6 +254,14 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
             // row-alpha weights: one alpha per row (scale alpha, bias -alpha in every group);
             // tile rows 0..7 and 8..15 are each 8 consecutive rows, 16 bytes
             if (lane < 2) load_lds16((const char*)a.alpha + tile_row(8 * lane) * 2, wsc);
+        } else if constexpr (S::HSC) {
+            // 8 bytes of scales (and of biases) a row: lane l brings half l % 2 of row l / 2
+            const char* sg = (const char*)a.s;
+            const char* bg = (const char*)a.b;
+            if (lane < 32) {
+                load_lds4(sg + tile_row(lane >> 1) * 8 + 4 * (lane & 1), wsc);
+                load_lds4(bg + tile_row(lane >> 1) * 8 + 4 * (lane & 1), wbi);
+            }
         } else {
             const char* sg = (const char*)a.s;
             const char* bg = (const char*)a.b;
@@ -303,6 +320,10 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         float alpha_n = 0.0f;  // row-alpha weights: alpha of weight row n
         if constexpr (ROWA) {
             alpha_n = h2f(wsc[n]);
+        } else if constexpr (S::HSC) {
+            const uint2 ts = *(const uint2*)(wsc + 4 * n), tb = *(const uint2*)(wbi + 4 * n);
+            sv[0] = (u4v){ts.x, ts.y, 0u, 0u};
+            bv[0] = (u4v){tb.x, tb.y, 0u, 0u};
         } else {
 #pragma unroll
             for (int c = 0; c < SCW; ++c) {
@@ -598,15 +619,15 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     return hipGetLastError();
 }
 
-// Shapes the tile kernel covers: SWIGLU / QKV / ADD at K = 2048, STORE at K = 1024 or 2048;
-// N a multiple of the block's rows; group size 64 or 128.
+// Shapes the tile kernel covers: SWIGLU / QKV / ADD at K = 2048, STORE at K = 512, 1024 or
+// 2048; N a multiple of the block's rows; group size 64 or 128.
 bool gather3_supported(int epi, int K, int N, int gs) {
     if (gs != 64 && gs != 128) return false;
     switch (epi) {
         case EPI_SWIGLU: return K == 2048 && N % 64 == 0;
         case EPI_QKV: return K == 2048 && N % 128 == 0;
         case EPI_ADD: return K == 2048 && N % 64 == 0;
-        case EPI_STORE: return (K == 1024 || K == 2048) && N % 64 == 0;
+        case EPI_STORE: return (K == 512 || K == 1024 || K == 2048) && N % 64 == 0;
     }
     return false;
 }
@@ -632,6 +653,7 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
                           : launch_g5<KPL, 128, E, 8, KS128, false, true>(a, rows, n_buckets, st); \
     }
         if (epi == EPI_SWIGLU) MJ_G5A(8, EPI_SWIGLU, 2, 2)
+        if (a.K == 512) MJ_G5A(2, EPI_STORE, 1, 1)
         if (a.K == 1024) MJ_G5A(4, EPI_STORE, 1, 1)
         MJ_G5A(8, EPI_STORE, 2, 2)
 #undef MJ_G5A
@@ -647,6 +669,7 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
         case EPI_QKV: MJ_G5(8, EPI_QKV, 16, 2, 2)
         case EPI_ADD: MJ_G5(8, EPI_ADD, 8, 4, 2)
         case EPI_STORE:
+            if (a.K == 512) { MJ_G5(2, EPI_STORE, 8, 1, 1) }
             if (a.K == 1024) { MJ_G5(4, EPI_STORE, 8, 1, 1) }
             MJ_G5(8, EPI_STORE, 8, 2, 2)
     }
@@ -670,14 +693,15 @@ hipError_t set_gather3_attributes() {
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, W, KS64, true>();    \
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, W, KS128, true>();
     MJ_A(8, EPI_SWIGLU, 8, 2, 2) MJ_A(8, EPI_QKV, 16, 2, 2) MJ_A(8, EPI_ADD, 8, 4, 2)
-    MJ_A(4, EPI_STORE, 8, 1, 1) MJ_A(8, EPI_STORE, 8, 2, 2)
+    MJ_A(2, EPI_STORE, 8, 1, 1) MJ_A(4, EPI_STORE, 8, 1, 1) MJ_A(8, EPI_STORE, 8, 2, 2)
 #undef MJ_A
 #define MJ_AA(KPL, E, KS64, KS128)                                              \
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, 8, KS64, true, true>();        \
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, 8, KS128, true, true>();      \
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, 8, KS64, false, true>();       \
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, 8, KS128, false, true>();
-    MJ_AA(8, EPI_SWIGLU, 2, 2) MJ_AA(4, EPI_STORE, 1, 1) MJ_AA(8, EPI_STORE, 2, 2)
+    MJ_AA(8, EPI_SWIGLU, 2, 2) MJ_AA(2, EPI_STORE, 1, 1) MJ_AA(4, EPI_STORE, 1, 1)
+    MJ_AA(8, EPI_STORE, 2, 2)
 #undef MJ_AA
     return e;
 }

@@ -395,7 +395,7 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         c.n_heads % c.n_kv_heads != 0 || c.H % 2048 != 0 || c.H > 4096 ||
         (c.rope_dim != 0 && c.rope_dim != 32 && c.rope_dim != 64 && c.rope_dim != 128) ||
         c.top_k < 1 || c.top_k > 8 || c.E < c.top_k || c.E > MJ_MAX_EXPERTS ||
-        c.I % 1024 != 0 || c.I > 4096 || (c.gs != 64 && c.gs != 128) || c.vocab < 16 ||
+        c.I % 512 != 0 || c.I > 4096 || (c.gs != 64 && c.gs != 128) || c.vocab < 16 ||
         c.vocab > 196608 || c.n_layers < 1 || c.n_heads * 128 % 512 != 0)
         return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE, "model_create: unsupported configuration");
     std::vector<int> lwin(c.n_layers, c.window), lrope(c.n_layers, c.rope_dim);
@@ -425,6 +425,18 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
             return mj_fail(ctx, MJ_INVALID_ARG,
                            "model_create: layer %d expert weights: null pointer or row-alpha "
                            "array not 16-byte aligned", l);
+        // the pass scratch is sized from the model configuration: every layer's expert shape
+        // must be that one
+        if (mw.E != c.E || mw.top_k != c.top_k || mw.H != c.H || mw.I != c.I || mw.gs != c.gs)
+            return mj_fail(ctx, MJ_INVALID_ARG,
+                           "model_create: layer %d experts E=%d top_k=%d H=%d I=%d gs=%d differ "
+                           "from the model's E=%d top_k=%d H=%d I=%d gs=%d", l, mw.E, mw.top_k,
+                           mw.H, mw.I, mw.gs, c.E, c.top_k, c.H, c.I, c.gs);
+        const mj_attn_weights& aw = layers[l].attn;
+        if (!aw.norm_w || !aw.qkv_w || !aw.qkv_s || !aw.qkv_b || !aw.q_norm_w || !aw.k_norm_w ||
+            !aw.o_w || !aw.o_s || !aw.o_b)
+            return mj_fail(ctx, MJ_INVALID_ARG, "model_create: layer %d attention weights: null "
+                           "pointer", l);
     }
     hipSetDevice(ctx->device);
     mj_status s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");

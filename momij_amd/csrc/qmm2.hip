@@ -222,10 +222,12 @@ static hipError_t launch_qmv2_t(QmvArgs a, hipStream_t st) {
 hipError_t launch_qmv2(const QmvArgs& a, int epi, hipStream_t st) {
     const int lpr = a.K / 64;
     if (epi == EPI_SWIGLU) {
+        if (lpr == 8) return launch_qmv2_t<8, EPI_SWIGLU>(a, st);
         if (lpr == 16) return launch_qmv2_t<16, EPI_SWIGLU>(a, st);
         if (lpr == 32) return launch_qmv2_t<32, EPI_SWIGLU>(a, st);
         return hipErrorInvalidValue;
     }
+    if (lpr == 8) return launch_qmv2_t<8, EPI_STORE>(a, st);
     if (lpr == 16) return launch_qmv2_t<16, EPI_STORE>(a, st);
     if (lpr == 32) return launch_qmv2_t<32, EPI_STORE>(a, st);
     if (lpr == 64) return launch_qmv2_t<64, EPI_STORE>(a, st);

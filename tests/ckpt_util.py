@@ -13,7 +13,11 @@ import numpy as np
 
 def write_maple_checkpoint(d: str, *, n_layers=4, H=2048, nQ=16, nKV=4, D=128, E=16, top_k=4,
                            I=1024, gs=64, vocab=2048, window=48, layer_types=None, seed=0,
-                           embed_scale=(0.05, 0.2)):
+                           embed_scale=(0.05, 0.2), defaults_config=False):
+    """defaults_config: write a config.json holding only the layer count and vocabulary, so
+    every other field takes MapleConfig's defaults (MapleConfig.swift:5-49: hidden 2048, 16 / 4
+    heads of 128, 256 experts top-8, intermediate 512, group size 128, window 512, rope theta
+    1e4, partial rotary 0.5, 4-bit gs64 head); the arrays must then have those shapes."""
     import torch
     from safetensors.torch import save_file
 
@@ -81,6 +85,10 @@ def write_maple_checkpoint(d: str, *, n_layers=4, H=2048, nQ=16, nKV=4, D=128, E
         wmap.update({k: fn for k in ks})
     with open(os.path.join(d, "model.safetensors.index.json"), "w") as f:
         json.dump({"metadata": {}, "weight_map": wmap}, f)
+    if defaults_config:
+        with open(os.path.join(d, "config.json"), "w") as f:
+            json.dump(dict(model_type="maple", num_hidden_layers=n_layers, vocab_size=vocab), f)
+        return arrays
     cj = dict(model_type="maple", hidden_size=H, num_hidden_layers=n_layers,
               num_attention_heads=nQ, num_key_value_heads=nKV, head_dim=D, vocab_size=vocab,
               num_experts=E, num_experts_per_tok=top_k, moe_intermediate_size=I,

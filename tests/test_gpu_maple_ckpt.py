@@ -159,3 +159,114 @@ def test_row_alpha_alignment_checked_at_model_create(maple):
     bad[1]["moe"]["down_alpha"] = buf[1:1 + a.numel()].view_as(a)
     with pytest.raises(MomijError):
         VerifyEngine(maple["ctx"], maple["cfg"], bad, *rest)
+
+
+def test_layer_expert_shape_checked_at_model_create(maple):
+    """A layer whose expert shape differs from the model configuration (the pass scratch is
+    sized from the configuration) is refused by mj_model_create before any kernel runs."""
+    from momij_amd._lib import MomijError
+    from momij_amd.engine import VerifyEngine
+
+    print("case: layer expert shape differs from the model configuration", flush=True)
+    layers, *rest = maple["dev"]
+    for field, value in (("I", 2048), ("E", 8), ("top_k", 2), ("gs", 128)):
+        bad = [{part: dict(lw[part]) for part in ("attn", "moe")} for lw in layers]
+        bad[2]["moe"][field] = value
+        with pytest.raises(MomijError) as ei:
+            VerifyEngine(maple["ctx"], maple["cfg"], bad, *rest)
+        assert ei.value.status == 4 and "layer 2" in str(ei.value), field
+
+
+@pytest.fixture(scope="module")
+def maple_real(tmp_path_factory):
+    """A 4-layer checkpoint at Maple's own shapes, loaded from a config.json that leaves every
+    architecture field at MapleConfig's defaults: 256 experts top-8, intermediate 512, group
+    size 128, window 512, rope theta 1e4 on 64 dims, the 4-bit gs64 head (vocabulary 2048)."""
+    import torch
+
+    from momij_amd.checkpoint import load_maple
+    from momij_amd.engine import VerifyEngine
+    from momij_amd.ops import Context
+
+    d = str(tmp_path_factory.mktemp("maple_real"))
+    write_maple_checkpoint(d, n_layers=4, E=256, top_k=8, I=512, gs=128, vocab=2048, window=512,
+                           seed=21, defaults_config=True)
+    cfg, w = load_maple(d, max_context=256)
+    assert (cfg.E, cfg.top_k, cfg.I, cfg.gs, cfg.window, cfg.rope_dim, cfg.head_bits) == \
+        (256, 8, 512, 128, 512, 64, 4)
+    assert cfg.rope_base == 1e4 and cfg.layer_window == [512, 512, 512, 0]
+    ctx = Context(0)
+    dev = w.device()
+    torch.cuda.synchronize()
+    eng = VerifyEngine(ctx, cfg, *dev)
+
+    def h(t):
+        a = t.detach().cpu().numpy()
+        return a.view(np.uint32) if a.dtype == np.int32 else a
+
+    host = dict(layers=[{part: {k: (h(v) if hasattr(v, "detach") else v)
+                                for k, v in lw[part].items()} for part in ("attn", "moe")}
+                        for lw in w.layers],
+                embed=h(w.embed), fnorm=h(w.final_norm), head=h(w.lm_head),
+                head_s=h(w.lm_head_scales), head_b=h(w.lm_head_biases))
+    yield dict(ctx=ctx, cfg=cfg, eng=eng, w=host)
+    eng.close()
+    ctx.close()
+
+
+def test_maple_real_shape_prefill_and_verify(maple_real, orc):
+    """Maple's own expert shape end to end: prefill, an 8-token chain verify and a 16-node tree
+    verify, each block re-run by the oracle from the device's inputs (tests/teacher.py)."""
+    eng, cfg, w = maple_real["eng"], maple_real["cfg"], maple_real["w"]
+    q4 = (w["head"], w["head_s"], w["head_b"])
+    print("case: maple defaults, E=256 top-8 I=512 gs=128 window 512, 4 layers", flush=True)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, cfg.vocab, 150).tolist()
+    eng.rewind(0)
+    y, cap = capture_pass(eng, lambda: eng.prefill(prompt, chunk=64))
+    M_last = 150 - 128
+    am, _ = check_head(orc, cap["head_in"][M_last - 1:M_last], [y], "prefill", q4=q4)
+    assert am[0] == y
+    L0 = eng.offset
+    cont, t = [], y
+    for _ in range(8):
+        t = eng.step_chain_feeds([t])[0]
+        cont.append(t)
+    eng.rewind(L0)
+    draft = cont[:5] + [int(v) for v in rng.integers(0, cfg.vocab, 3)]
+    for i in range(5, 8):
+        if draft[i] == cont[i]:
+            draft[i] = (draft[i] + 1) % cfg.vocab
+    for parents, toks, want in ((None, draft, 5),
+                                (TREE16, _tree_draft(cont, cfg.vocab, rng), 4)):
+        eng.rewind(L0)
+        M = len(toks) + 1
+        par = list(range(-1, M - 1)) if parents is None else parents
+        kv0 = [_host_kv(eng, l) for l in range(cfg.n_layers)]
+        (acc, out), cap = capture_pass(eng, lambda: eng.verify_greedy(y, toks, parents))
+        assert acc == want and out == cont[:want + 1], (acc, out, cont)
+        for l in range(cfg.n_layers):
+            check_layer(orc, cfg, l, w["layers"][l], cap, M, (kv0[l][0], kv0[l][1]), L0, par)
+        gpu_am = orc.argmax_rows(cap["logits"][:M])[0]
+        am, _ = check_head(orc, cap["head_in"][:M], gpu_am, "verify", q4=q4)
+        oacc, _, oemit = orc.accept_greedy([y] + toks, parents, am)
+        assert oacc == acc and list(oemit) == out
+    eng.rewind(L0)
+
+
+TREE16 = [-1, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 10, 11, 12, 13, 14]
+
+
+def _tree_draft(cont, vocab, rng):
+    """TREE16 tokens whose first-child path (0-1-4-10-12) carries the continuation."""
+    toks = [int(t) for t in rng.integers(0, vocab, len(TREE16) - 1)]
+    depth = [0] * len(TREE16)
+    for r in range(1, len(TREE16)):
+        depth[r] = depth[TREE16[r]] + 1
+    path = [1, 4, 10, 12]
+    for d, r in enumerate(path):
+        toks[r - 1] = cont[d]
+    for r in range(1, len(TREE16)):
+        if r not in path and toks[r - 1] == cont[depth[r] - 1]:
+            toks[r - 1] = (toks[r - 1] + 1) % vocab
+    return toks
