@@ -399,16 +399,18 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
     const bool fused = route_supported(H, E, k);
     const bool up_tile = gather3_supported(EPI_SWIGLU, H, 2 * I, w->gs);
     const bool dn_tile = gather3_supported(EPI_STORE, I, H, w->gs);
-    // tile path: the top-k launch also lists each expert's (row, slot) pairs for the gathers
-    const bool tile = fused && M > 1 && M <= MJ_MAX_ROWS && up_tile && dn_tile;
+    // tile path: the top-k launch also lists each expert's (row, slot) pairs for the gathers.
+    // One row takes it too, so a row's result does not depend on how many rows share its pass
+    // (a verify row equals the one-row decode step at its position, bit for bit).
+    const bool tile = fused && M >= 1 && M <= MJ_MAX_ROWS && up_tile && dn_tile;
     if (fused) {
         RouteArgs ra{};
         ra.x = x;
         ra.norm_w = (flags & MJ_MOE_PRENORM) ? (const uint16_t*)w->norm_w : nullptr;
         ra.W = (const uint16_t*)w->router_w;
-        ra.xn = ((M == 1 || ms.want_plain) && (flags & MJ_MOE_PRENORM)) ? ms.xn : nullptr;
-        ra.xperm = M > 1 ? ms.xperm : nullptr;
-        ra.xsum = M > 1 ? ms.xsum : nullptr;
+        ra.xn = (((M == 1 && !tile) || ms.want_plain) && (flags & MJ_MOE_PRENORM)) ? ms.xn : nullptr;
+        ra.xperm = (M > 1 || tile) ? ms.xperm : nullptr;
+        ra.xsum = (M > 1 || tile) ? ms.xsum : nullptr;
         ra.inds = inds;
         ra.scores = scores;
         ra.logits = ms.logits;
@@ -425,9 +427,9 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         if (s != MJ_OK) return s;
         s = mj_hip(ctx, launch_route_topk(ra, st), "route top-k");
         if (s != MJ_OK) return s;
-        if (M == 1 && (flags & MJ_MOE_PRENORM)) xn = ms.xn;
+        if (M == 1 && !tile && (flags & MJ_MOE_PRENORM)) xn = ms.xn;
     }
-    if (M == 1) {
+    if (M == 1 && !tile) {
         if (fused) {
         } else if (flags & MJ_MOE_PRENORM) {
             s = mj_hip(ctx, launch_rmsnorm_qx(x, (const uint16_t*)w->norm_w, w->eps, ms.xn,

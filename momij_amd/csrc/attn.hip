@@ -1,16 +1,20 @@
 // attn.hip -- sliding-window attention over the fp16 KV cache for a pass of M verify rows
 // arranged as a chain or a draft tree.
 //
-// k_qknorm_rope_kv  maple_qk_norm_rope + maple_write_kv_pair (SeedlessMetal.swift:2794-2901):
-//                   per head RMSNorm(eps) * w, non-traditional half-split RoPE on the first
-//                   rope_dim dims at the row's position L + depth(r); K and V rows appended at
-//                   slot (L + r) % C.  One wave per (row, head), two dims per lane.
-// k_attn_chunk      maple_sdpa_d128 math (2919-2997): softmax(q k^T / sqrt(128)) v in fp32, GQA.
-//                   Split-K over 64-key chunks ("flash decoding"); one 256-thread block per
-//                   (kv head, chunk) stages Q (all rows x heads of the group), K and V^T in LDS
-//                   and runs QK^T and PV on v_mfma_f32_16x16x32_f16.  Mask: committed
-//                   positions inside the row's window [P-W+1, L-1] (AttentionMasks.swift:10-27)
-//                   plus the row's ancestors and itself; a chain is the causal M-row pass.
+// k_attn_chunk      maple_sdpa_d128 math (SeedlessMetal.swift:2919-2997): softmax(q k^T /
+//                   sqrt(128)) v in fp32, GQA.  Split-K over 64-key chunks ("flash decoding");
+//                   one 256-thread block per (kv head, chunk) stages Q (all rows x heads of the
+//                   group), K and V^T in LDS and runs QK^T and PV on v_mfma_f32_16x16x32_f16.
+//                   Mask: committed positions inside the row's window [P-W+1, L-1]
+//                   (AttentionMasks.swift:10-27) plus the row's ancestors and itself; a chain is
+//                   the causal M-row pass.
+//                   The block also finishes the projection's raw q and k rows as
+//                   maple_qk_norm_rope + maple_write_kv_pair do (2794-2901): per-head RMSNorm(eps)
+//                   * w, non-traditional half-split RoPE on the first rope_dim dims at the row's
+//                   position L + depth(r) (angles from the pass's RoPE table).  Queries are
+//                   finished by every block of the group (they are small); the pass's own keys
+//                   are finished by the block whose chunk holds them, which also appends them
+//                   (K finished, V as projected) at slot (L + r) % C.
 // k_attn_combine    merges the chunk partials per (row, head) and writes the output in the qx
 //                   format consumed by the o-projection.
 #include "mj_device.h"
@@ -21,277 +25,486 @@
 #define QSTR 136  // LDS row stride (halves) of Q and K tiles
 #define VSTR 72   // LDS row stride (halves) of V^T and P tiles
 
+// Chunks of a pass.  Keys are placed by absolute position: chunk c0 + c holds positions
+// [AK (c0 + c), AK (c0 + c) + AK - 1], key lane = position % AK.  The committed window
+// [lo, L - 1] is laid out that way; so are a chain pass's own rows (row r at position L + r).
+// A tree pass's own rows (positions repeat across siblings) follow in chunks of their own, by
+// row index.  With keys placed by position, a row's chunk partials and their merge order depend
+// only on the row's position, not on the other rows of the pass: a chain verify row computes
+// bit for bit what a one-row pass at its position computes.
+struct ChunkGeom {
+    int64_t lo, hi;  // positions placed by position: [lo, hi]
+    int64_t c0;      // absolute index of the first chunk
+    int n_abs, nch;  // chunks placed by position; all chunks
+};
+
+__host__ __device__ inline ChunkGeom chunk_geom(int window, int64_t L, int M, bool chain) {
+    ChunkGeom g;
+    g.lo = window > 0 ? (L - window + 1 > 0 ? L - window + 1 : 0) : 0;
+    g.hi = chain ? L + M - 1 : L - 1;
+    g.c0 = g.lo / AK;
+    g.n_abs = g.hi >= g.lo ? (int)(g.hi / AK - g.c0 + 1) : 0;
+    g.nch = g.n_abs + (chain ? 0 : (M + AK - 1) / AK);
+    return g;
+}
+
 int attn_max_chunks(int window, int64_t L_max, int M) {
+    // position-aligned chunks: one more than the keys span, one for a tree's own rows
     const int64_t keys = (window > 0 ? (int64_t)window - 1 : L_max) + M;
-    return (int)((keys + AK - 1) / AK);
+    return (int)((keys + AK - 1) / AK) + 2;
 }
 
-__global__ __launch_bounds__(256) void k_qknorm_rope_kv(AttnArgs a) {
-    if (aborted(a.abort)) return;
-    const int lane = threadIdx.x & 63;
-    const int nh = a.nQ + a.nKV;
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int r = gw / nh, hh = gw % nh;
-    if (r >= a.M) return;
-    const int qkvN = (a.nQ + 2 * a.nKV) * HD;
-    const uint32_t xv = *(const uint32_t*)(a.qkv + (size_t)r * qkvN + hh * HD + 2 * lane);
-    const float x0 = h2f(xv & 0xFFFFu), x1 = h2f(xv >> 16);
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
-    const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
-    const uint16_t* wn = hh < a.nQ ? a.q_norm_w : a.k_norm_w;
-    const uint32_t wv = *(const uint32_t*)(wn + 2 * lane);
-    float v0 = x0 * sc * h2f(wv & 0xFFFFu);
-    float v1 = x1 * sc * h2f(wv >> 16);
-    const int rd = a.rope_dim;
-    if (rd > 0) {
-        const int half = rd / 2;
-        const float u0 = __shfl_xor(v0, half / 2, MJ_WAVE);
-        const float u1 = __shfl_xor(v1, half / 2, MJ_WAVE);
-        const float pos = (float)(a.sd->L + a.sd->depth[r]);
-        const int j0 = 2 * lane;
-        if (j0 < rd) {
-            const int p0 = j0 < half ? j0 : j0 - half;
-            const float t0 = pos * a.inv_freq[p0], t1 = pos * a.inv_freq[p0 + 1];
-            const float c0 = cosf(t0), s0 = sinf(t0), c1 = cosf(t1), s1 = sinf(t1);
-            if (j0 < half) {
-                v0 = v0 * c0 - u0 * s0;
-                v1 = v1 * c1 - u1 * s1;
-            } else {
-                v0 = v0 * c0 + u0 * s0;
-                v1 = v1 * c1 + u1 * s1;
-            }
-        }
+// DPP lane moves (no LDS round trip): quad_perm [1,0,3,2] (xor 1) 0xB1, [2,3,0,1] (xor 2)
+// 0x4E; row_half_mirror 0x141, row_mirror 0x140; row_ror:n 0x120 + n (lane i of a row of 16
+// takes lane i - n mod 16)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_xor1(float v) { return dpp<0xB1>(v); }
+__device__ __forceinline__ float quad_xor2(float v) { return dpp<0x4E>(v); }
+// sum over each row of 16 lanes, every lane of the row gets it (the same bits in every lane:
+// each step adds the same two values in either order)
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    return v;
+}
+// sum over each group of 8 lanes (the same bits in every lane of the group)
+__device__ __forceinline__ float lane8_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    return v;
+}
+// max / sum over lanes i, i ^ 16, i ^ 32, i ^ 48 (v_permlane16_swap: rows 2k + 1 of the first
+// operand trade places with rows 2k of the second; v_permlane32_swap: the upper half of the
+// first with the lower half of the second; with both operands v each returns the (lower,
+// upper) pair of values, so every lane combines them in the same order)
+__device__ __forceinline__ float xrow_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xrow_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// lane i ^ X of a row of 16, X in {2, 4, 8}
+template <int X>
+__device__ __forceinline__ float row16_xor(float v, int lane) {
+    static_assert(X == 2 || X == 4 || X == 8, "lane distance");
+    if constexpr (X == 2) return dpp<0x4E>(v);
+    if constexpr (X == 8) return dpp<0x128>(v);
+    const float up = dpp<0x12C>(v), dn = dpp<0x124>(v);  // lanes i + 4, i - 4
+    return (lane & 4) ? dn : up;
+}
+
+__device__ __forceinline__ void unpack8(const u4v v, float x[8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[2 * j] = h2f(v[j] & 0xFFFFu);
+        x[2 * j + 1] = h2f(v[j] >> 16);
     }
-    const uint32_t o = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
-    if (hh < a.nQ) {
-        *(uint32_t*)(a.qbuf + ((size_t)r * a.nQ + hh) * HD + 2 * lane) = o;
-    } else {
-        const int g = hh - a.nQ;
-        const int64_t slot = (a.sd->L + r) % a.C;
-        const size_t dst = ((size_t)g * a.C + slot) * HD + 2 * lane;
-        *(uint32_t*)(a.kc + dst) = o;
-        *(uint32_t*)(a.vc + dst) =
-            *(const uint32_t*)(a.qkv + (size_t)r * qkvN + (a.nQ + a.nKV) * HD + g * HD + 2 * lane);
+}
+__device__ __forceinline__ u4v pack8(const float x[8]) {
+    u4v o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = (uint32_t)f2h(x[2 * j]) | ((uint32_t)f2h(x[2 * j + 1]) << 16);
+    return o;
+}
+
+// RoPE of 8 dims d0 .. d0 + 7 (d0 a multiple of 8: the run lies on one side of half and of
+// 2 half): dims below half take v cos - u sin, dims in [half, 2 half) v cos + u sin (u the
+// partner dim d +/- half, angles cs[i]), later dims pass through (cos 1, sin 0).  Branch-free.
+template <int HALF>
+__device__ __forceinline__ void rope8(float v[8], const float u[8], const float2* cs, int d0) {
+    const bool rot = d0 < 2 * HALF;
+    const float sg = d0 < HALF ? -1.0f : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float2 c = cs[i];
+        const float cx = rot ? c.x : 1.0f, sy = rot ? sg * c.y : 0.0f;
+        v[i] = v[i] * cx + u[i] * sy;
     }
 }
-
-hipError_t launch_qknorm_rope_kv(const AttnArgs& a, hipStream_t st) {
-    const int waves = a.M * (a.nQ + a.nKV);
-    hipLaunchKernelGGL(k_qknorm_rope_kv, dim3((waves + 3) / 4), dim3(256), 0, st, a);
-    return hipGetLastError();
+// first angle of dims d0 .. (frequency d0 or d0 - half; 0 past 2 half, where nothing is read)
+template <int HALF>
+__device__ __forceinline__ int rope_f0(int d0) {
+    return d0 < 2 * HALF ? (d0 < HALF ? d0 : d0 - HALF) : 0;
 }
 
+// Work of one block (kv head g, chunk c), 256 threads:
+//   loads, every one issued before the first wait (all unconditional, at clamped addresses):
+//     K: key t / 4, dims 32 (t % 4) ..      (the layout the own-key norm reduces over)
+//     V: keys 4 (t % 16) .. + 3, dims 8 (t / 16) ..   (transposed in registers, 8-byte LDS rows)
+//     Q: parts of 8 dims, four per thread (one round up to 16 rows)
+//     the pass's RoPE table rows, staged in LDS once for the block's queries and own keys
+//   barrier; q and the own keys finished (RMSNorm, RoPE) into LDS, own K / V appended; barrier
+//   S^T = K Q^T on MFMA (A = 16 keys, B = 16 query vectors): lane (n, q) holds query vector n
+//   against keys 16 kt + 4 q + r, so a query's mask, max and sum stay in its lane (plus two
+//   cross-lane steps) and its probabilities are already the A operand of the PV product: that
+//   product's k-slot 8 q + u takes key 32 j + 4 q + u (u < 4) or 32 j + 16 + 4 q + u - 4.
+//   Scores are kept in log2 units (scale * log2 e), so p = exp2(s - m); the partial max is
+//   stored in the same units.
+#define LOG2E 1.44269504088896341f
+// LDS of the RoPE table: M * half angles rounded up to whole 64-lane staging rounds
+__host__ __device__ inline int tab_floats2(int M, int half) {
+    return ((M * half / 2 + 63) / 64) * 64 * 2;
+}
+template <int HALF>  // rope_dim / 2 (0: no RoPE)
 __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int g = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
     const StepDesc* sd = a.sd;
     const int64_t L = sd->L;
+    const int M = a.M;
     const int gqa = a.nQ / a.nKV;
-    const int nqv = a.M * gqa, nqt = (nqv + 15) / 16;
-    const int64_t lo_min = a.window > 0 ? (L - a.window + 1 > 0 ? L - a.window + 1 : 0) : 0;
-    const int64_t ncm = L - lo_min;
-    const int64_t nk = ncm + a.M;
-    if ((int64_t)c * AK >= nk) return;  // whole block
+    const int nqv = M * gqa, nqt = (nqv + 15) / 16;
+    const int qkvN = (a.nQ + 2 * a.nKV) * HD;
+    constexpr int half = HALF;
+    const ChunkGeom cg = chunk_geom(a.window, L, M, sd->chain != 0);
+    // ring slot of position p (p - L is within the cache: |p - L| < C)
+    const int64_t Lm = L % a.C;
+    auto slot_of = [&](int64_t p) -> int64_t {
+        int64_t sl = Lm + (p - L);
+        sl += sl < 0 ? a.C : 0;
+        sl -= sl >= a.C ? a.C : 0;
+        return sl;
+    };
+    if (c >= cg.nch) return;  // whole block
+    const bool by_pos = c < cg.n_abs;
+    const int64_t cpos = (cg.c0 + c) * AK;  // position of key lane 0 (chunks placed by position)
+    // key lane k of this chunk: -2 none, -1 committed (at position p), else own row (its
+    // index; its position is L + depth[row])
+    auto key_of = [&](int k, int64_t& p) -> int {
+        if (by_pos) {
+            p = cpos + k;
+            if (p < cg.lo || p > cg.hi) return -2;
+            return p < L ? -1 : (int)(p - L);
+        }
+        p = 0;
+        const int ar = (c - cg.n_abs) * AK + k;
+        return ar < M ? ar : -2;
+    };
+    // the pass's own rows fall in this block's chunk
+    const bool own_chunk = by_pos ? cpos + AK - 1 >= L && cpos <= cg.hi : true;
 
     extern __shared__ uint16_t lds[];
     uint16_t* Qs = lds;                          // [nqt*16][QSTR]
     uint16_t* Ks = Qs + nqt * 16 * QSTR;         // [AK][QSTR]
     uint16_t* Vt = Ks + AK * QSTR;               // [HD][VSTR]
-    uint16_t* Ps = Vt + HD * VSTR;               // [4 waves][16][VSTR]
-    int64_t* kpos = (int64_t*)(Ps + 4 * 16 * VSTR);
-    int64_t* rlo = kpos + AK;                    // [MJ_ROWS] first key position of a row's window
+    float2* tab = (float2*)(Vt + HD * VSTR);     // [M][half] RoPE angles of the pass's rows
+    int* kmeta = (int*)(tab + tab_floats2(M, half));  // [AK] key: (p - L) * 128 + (class + 2)
+    int* rlo = kmeta + AK;                       // [MJ_ROWS] window start of a row, - L
     uint64_t* ranc = (uint64_t*)(rlo + MJ_ROWS);  // [MJ_ROWS] ancestor masks
-    int* ktree = (int*)(ranc + MJ_ROWS);
-    int* s_abort = ktree + AK;
+    uint16_t* qnw_s = (uint16_t*)(ranc + MJ_ROWS);  // [HD] q norm weights
+    uint16_t* knw_s = qnw_s + HD;                  // [HD] k norm weights
+    int* s_abort = (int*)(knw_s + HD);
 
-    // Every load of the block is issued before the first wait: this thread's K/V quarter row
-    // (key kk = t / 4, dims 32 (t % 4) ..), its share of the Q rows, and the key metadata.
+    // ---- K: key kk = t / 4, dims 32 dq ..
     const int kk = t >> 2, dq = t & 3;
-    const int64_t ki = (int64_t)c * AK + kk;
-    const bool kvalid = ki < nk;
-    int64_t kslot_v = 0;
-    if (kvalid) kslot_v = (ki < ncm ? lo_min + ki : L + (ki - ncm)) % a.C;
-    u4v kv[4], vv[4];
+    int64_t kp;
+    const int kcls = key_of(kk, kp);
+    const bool kvalid = kcls != -2;
+    const bool kown = kcls >= 0;
+    const int ar = kown ? kcls : 0;  // pass row of an own key
+    u4v kv[4];
     {
-        const size_t base = ((size_t)g * a.C + kslot_v) * HD + 32 * dq;
+        const int64_t slot = kvalid && !kown ? slot_of(kp) : 0;
+        const uint16_t* ks = kown ? a.qkv + (size_t)ar * qkvN + (a.nQ + g) * HD + 32 * dq
+                                  : a.kc + ((size_t)g * a.C + slot) * HD + 32 * dq;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            kv[q] = (u4v){0u, 0u, 0u, 0u};
-            vv[q] = (u4v){0u, 0u, 0u, 0u};
-            if (kvalid) {
-                kv[q] = *(const u4v*)(a.kc + base + 8 * q);
-                vv[q] = *(const u4v*)(a.vc + base + 8 * q);
-            }
+        for (int q = 0; q < 4; ++q) kv[q] = *(const u4v*)(ks + 8 * q);
+    }
+    // ---- V: keys 4 vg .. 4 vg + 3, dims 8 vd ..
+    const int vg = t & 15, vd = t >> 4;
+    u4v vv[4];
+    int vcls[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int64_t p;
+        vcls[j] = key_of(4 * vg + j, p);
+        const int64_t slot = vcls[j] == -1 ? slot_of(p) : 0;
+        const uint16_t* vs =
+            vcls[j] >= 0 ? a.qkv + (size_t)vcls[j] * qkvN + (a.nQ + a.nKV + g) * HD + 8 * vd
+                         : a.vc + ((size_t)g * a.C + slot) * HD + 8 * vd;
+        vv[j] = *(const u4v*)vs;
+    }
+    // ---- vectors to finish (RMSNorm + RoPE): the block's queries (vector qv = r * gqa + j is
+    // head g * gqa + j of row r) and the pass's own keys in this chunk (lanes ko0 .. ko1 - 1).
+    // Job jb of a vector holds its parts pa and pa + X (8 dims each; X = half / 8 parts apart,
+    // so a rotated pair of dims sits in one thread), 8 jobs a vector in 8 consecutive threads.
+    constexpr int X = HALF >= 16 ? HALF / 8 : 8;
+    int ko0 = 0, ko1 = 0;
+    if (own_chunk) {
+        ko0 = by_pos ? (int)(L - cpos > 0 ? L - cpos : 0) : 0;
+        ko1 = by_pos ? (int)(cg.hi - cpos + 1 < AK ? cg.hi - cpos + 1 : AK)
+                     : (M - (c - cg.n_abs) * AK < AK ? M - (c - cg.n_abs) * AK : AK);
+    }
+    const int njobs = 8 * (nqv + ko1 - ko0);
+    constexpr int JR = 2;  // jobs a thread loads before the first barrier (more: in a loop)
+    u4v jxa[JR], jxb[JR];
+    auto job_src = [&](int j, int& pa) -> const uint16_t* {
+        const int vi = j >> 3, jb = j & 7;
+        pa = (jb & (X - 1)) | ((jb & ~(X - 1)) << 1);
+        if (vi < nqv)
+            return a.qkv + (size_t)(vi / gqa) * qkvN + (g * gqa + vi % gqa) * HD;
+        int64_t p;
+        const int r2 = key_of(ko0 + vi - nqv, p);
+        return a.qkv + (size_t)(r2 >= 0 ? r2 : 0) * qkvN + (a.nQ + g) * HD;
+    };
+#pragma unroll
+    for (int jj = 0; jj < JR; ++jj) {
+        const int j = t + 256 * jj;
+        int pa;
+        const uint16_t* src = job_src(j < njobs ? j : njobs - 1, pa);
+        jxa[jj] = *(const u4v*)(src + 8 * pa);
+        jxb[jj] = *(const u4v*)(src + 8 * (pa + X));
+    }
+    // the norm weights into LDS (16 lanes each of wave 0)
+    if (wv == 0 && lane < HD / 8) {
+        __builtin_amdgcn_global_load_lds(a.q_norm_w + 8 * lane,
+                                         (__attribute__((address_space(3))) void*)qnw_s, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(a.k_norm_w + 8 * lane,
+                                         (__attribute__((address_space(3))) void*)knw_s, 16, 0, 0);
+    }
+    // ---- RoPE table rows (float4 = two angles), key and row metadata
+    // the table goes straight into LDS (16 bytes a lane): pairs 2e, 2e + 1 of the [M][half]
+    // angles, wave w taking pairs 64 w + lane, 64 (w + 4) + lane, ...
+    const int ntab4 = M * half / 2, hd = half > 0 ? half : 1;
+    for (int e0 = 64 * wv; e0 < ntab4; e0 += 256) {
+        const int e = e0 + lane;
+        if (e < ntab4)
+            __builtin_amdgcn_global_load_lds(a.rope_cs + (2 * e / hd) * MJ_ROPE_F + 2 * e % hd,
+                                             (__attribute__((address_space(3))) void*)(tab + 2 * e0),
+                                             16, 0, 0);
+    }
+    int64_t mpos;
+    const int mcls = key_of(t & (AK - 1), mpos);  // -2 invalid, -1 committed, >= 0 own row
+    const int rdep = sd->depth[t < M ? t : M - 1];
+    const uint64_t ranc_t = sd->anc[t < M ? t : M - 1];
+    const int abort_v = a.abort ? *a.abort : 0;  // thread 0's copy decides for the block
+
+    // ---- LDS: K rows (own keys raw for now), V^T, the table, metadata; the padding query
+    // rows of the last tile (read by the MFMAs, masked after) are cleared
+    for (int i = nqv * 16 + t; i < nqt * 16 * 16; i += 256)
+        *(u4v*)(Qs + (i >> 4) * QSTR + 8 * (i & 15)) = (u4v){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        *(u4v*)(Ks + kk * QSTR + 32 * dq + 8 * q) = kvalid ? kv[q] : (u4v){0u, 0u, 0u, 0u};
+    {
+        u4v w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = vcls[j] != -2 ? vv[j] : (u4v){0u, 0u, 0u, 0u};
+        // dim 8 vd + i of keys 4 vg .. + 3: halves i of the four key vectors
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int sh = 16 * (i & 1);
+            const uint32_t a0 = (w[0][i >> 1] >> sh) & 0xFFFFu, a1 = (w[1][i >> 1] >> sh) & 0xFFFFu;
+            const uint32_t a2 = (w[2][i >> 1] >> sh) & 0xFFFFu, a3 = (w[3][i >> 1] >> sh) & 0xFFFFu;
+            *(uint2*)(Vt + (8 * vd + i) * VSTR + 4 * vg) = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
         }
     }
     if (t < AK) {
-        const int64_t i = (int64_t)c * AK + t;
-        int64_t pos = INT64_MIN / 2;
-        int tree = -2;  // -2 invalid, -1 committed, >=0 tree row
-        if (i < nk) {
-            if (i < ncm) {
-                pos = lo_min + i;
-                tree = -1;
-            } else {
-                const int ar = (int)(i - ncm);
-                pos = L + sd->depth[ar];
-                tree = ar;
-            }
-        }
-        kpos[t] = pos;
-        ktree[t] = tree;
+        // position - L: p - L in chunks placed by position, depth[row] for a tree's own rows
+        const int64_t rel = by_pos ? mpos - L : (int64_t)sd->depth[mcls >= 0 ? mcls : 0];
+        kmeta[t] = mcls == -2 ? (int)0x80000000 : (int)rel * 128 + (mcls + 2);
     }
-    // the rows' window starts and ancestor masks, fetched with everything else
-    if (t < a.M) {
-        rlo[t] = a.window > 0 ? L + sd->depth[t] - a.window + 1 : INT64_MIN;
-        ranc[t] = sd->anc[t];
+    if (t < M) {
+        rlo[t] = a.window > 0 ? rdep - a.window + 1 : INT32_MIN / 2;
+        ranc[t] = ranc_t;
     }
-    // Q rows of this kv group: qv = r * gqa + j  <-  head g*gqa + j of row r; four 16-byte
-    // parts per thread per round
-    for (int base = 0; base < nqt * 256; base += 1024) {
-        u4v qv4[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int idx = base + t + 256 * j;
-            const int qv = idx >> 4, part = idx & 15;
-            qv4[j] = (u4v){0u, 0u, 0u, 0u};
-            if (idx < nqt * 256 && qv < nqv) {
-                const int r = qv / gqa, jj = qv % gqa;
-                qv4[j] = *(const u4v*)(a.qbuf + ((size_t)r * a.nQ + g * gqa + jj) * HD + 8 * part);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int idx = base + t + 256 * j;
-            if (idx < nqt * 256) *(u4v*)(Qs + (idx >> 4) * QSTR + 8 * (idx & 15)) = qv4[j];
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        *(u4v*)(Ks + kk * QSTR + 32 * dq + 8 * q) = kv[q];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int d = 32 * dq + 8 * q + 2 * j;
-            Vt[d * VSTR + kk] = (uint16_t)(vv[q][j] & 0xFFFFu);
-            Vt[(d + 1) * VSTR + kk] = (uint16_t)(vv[q][j] >> 16);
-        }
-    }
-    if (t == 0) *s_abort = a.abort ? *a.abort : 0;
+    if (t == 0) *s_abort = abort_v;
     __syncthreads();
     if (*s_abort) return;  // block-uniform
 
+    // ---- finish the vectors: RMSNorm over the vector's 8 jobs, RoPE of dims d < half against
+    // d + half (maple_qk_norm_rope); queries into Qs, own keys into Ks and appended at slot
+    // (L + r) % C with their V rows (maple_write_kv_pair).  No other block of this launch
+    // reads those slots (the committed window never reaches them).
+    for (int j0 = 0; j0 < njobs; j0 += 256 * JR) {
+#pragma unroll
+        for (int jj = 0; jj < JR; ++jj) {
+            const int j = j0 + t + 256 * jj;
+            if (j0 > 0) {
+                int pa;
+                const uint16_t* src = job_src(j < njobs ? j : njobs - 1, pa);
+                jxa[jj] = *(const u4v*)(src + 8 * pa);
+                jxb[jj] = *(const u4v*)(src + 8 * (pa + X));
+            }
+            const int vi = j >> 3, jb = j & 7;
+            const int pa = (jb & (X - 1)) | ((jb & ~(X - 1)) << 1), pb = pa + X;
+            const bool isq = vi < nqv;
+            int64_t kpos2;
+            const int kl = ko0 + vi - nqv;  // own key lane
+            const int kr2 = isq ? 0 : key_of(kl & (AK - 1), kpos2);
+            const int row = isq ? (vi < nqv ? vi / gqa : 0) : (kr2 >= 0 ? kr2 : 0);
+            float xa[8], xb[8], wa[8], wb[8];
+            unpack8(jxa[jj], xa);
+            unpack8(jxb[jj], xb);
+            const uint16_t* nw = isq ? qnw_s : knw_s;
+            unpack8(*(const u4v*)(nw + 8 * pa), wa);
+            unpack8(*(const u4v*)(nw + 8 * pb), wb);
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += xa[i] * xa[i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += xb[i] * xb[i];
+            ss = lane8_sum(ss);
+            const float scl = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                xa[i] = xa[i] * scl * wa[i];
+                xb[i] = xb[i] * scl * wb[i];
+            }
+            if constexpr (HALF > 0) {
+                // dims 8 pa + i < half pair with 8 pa + i + half = 8 pb + i
+                const bool rot = 8 * pa < half;
+                const float2* cs = tab + row * half + (rot ? 8 * pa : 0);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float2 c2 = cs[i];
+                    const float cx = rot ? c2.x : 1.0f, sy = rot ? c2.y : 0.0f;
+                    const float ra = xa[i] * cx - xb[i] * sy, rb = xb[i] * cx + xa[i] * sy;
+                    xa[i] = ra;
+                    xb[i] = rb;
+                }
+            }
+            const u4v oa = pack8(xa), ob = pack8(xb);
+            if (j < njobs) {
+                if (isq) {
+                    *(u4v*)(Qs + vi * QSTR + 8 * pa) = oa;
+                    *(u4v*)(Qs + vi * QSTR + 8 * pb) = ob;
+                } else {
+                    *(u4v*)(Ks + kl * QSTR + 8 * pa) = oa;
+                    *(u4v*)(Ks + kl * QSTR + 8 * pb) = ob;
+                    const size_t dst = ((size_t)g * a.C + slot_of(L + kr2)) * HD;
+                    *(u4v*)(a.kc + dst + 8 * pa) = oa;
+                    *(u4v*)(a.kc + dst + 8 * pb) = ob;
+                }
+            }
+        }
+    }
+    if (own_chunk) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (vcls[j] >= 0)
+                *(u4v*)(a.vc + ((size_t)g * a.C + slot_of(L + vcls[j])) * HD + 8 * vd) = vv[j];
+    }
+    __syncthreads();
+
+    const float sc2 = a.scale * LOG2E;
     const int ln = lane & 15, lq = lane >> 4;
-    uint16_t* Pw = Ps + wv * 16 * VSTR;
     const int iters = (nqt + 3) / 4;
     for (int it = 0; it < iters; ++it) {
         const int qt = wv + 4 * it;
-        const bool active = qt < nqt;
-        float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (qt >= nqt) break;  // wave-uniform; no block barrier follows
+        // S^T tiles: keys 16 kt + 4 lq + r against query vector 16 qt + ln
+        u4v qb[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) qb[s4] = *(const u4v*)(Qs + (qt * 16 + ln) * QSTR + 32 * s4 + 8 * lq);
         f4 S[4];
-        if (active) {
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-                S[kt] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kt = 0; kt < 4; ++kt) {
+            S[kt] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const u4v av = *(const u4v*)(Qs + (qt * 16 + ln) * QSTR + 32 * s + 8 * lq);
-                    const u4v bv = *(const u4v*)(Ks + (16 * kt + ln) * QSTR + 32 * s + 8 * lq);
-                    S[kt] = mfma16x16x32(as_h8(av), as_h8(bv), S[kt]);
-                }
-            }
-            // mask + scale; lane holds rows qv = qt*16 + 4*lq + r, key 16*kt + ln
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qv = qt * 16 + 4 * lq + r;
-                const int row = qv < nqv ? qv / gqa : 0;
-                const int64_t lo_r = rlo[row];
-                const uint64_t anc = ranc[row];
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt) {
-                    const int kk = 16 * kt + ln;
-                    const int tr = ktree[kk];
-                    bool ok = qv < nqv && tr != -2 && kpos[kk] >= lo_r;
-                    if (tr >= 0) ok = ok && ((anc >> tr) & 1ull);
-                    const float s = ok ? S[kt][r] * a.scale : -INFINITY;
-                    S[kt][r] = s;
-                    m[r] = fmaxf(m[r], s);
-                }
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const u4v av = *(const u4v*)(Ks + (16 * kt + ln) * QSTR + 32 * s4 + 8 * lq);
+                S[kt] = mfma16x16x32(as_h8(av), as_h8(qb[s4]), S[kt]);
             }
         }
+        const int qv = qt * 16 + ln;
+        const int row = qv < nqv ? qv / gqa : 0;
+        const int lo_r = rlo[row];
+        const uint64_t anc = ranc[row];
+        float m = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            const int4 km = *(const int4*)(kmeta + 16 * kt + 4 * lq);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int e = r == 0 ? km.x : r == 1 ? km.y : r == 2 ? km.z : km.w;
+                const int cls = (e & 127) - 2;  // -2 invalid, -1 committed, >= 0 own row
+                const bool ok = (qv < nqv) & (e != (int)0x80000000) & ((e >> 7) >= lo_r) &
+                                ((cls < 0) | (((anc >> (cls & 63)) & 1ull) != 0));
+                const float sv = ok ? S[kt][r] * sc2 : -INFINITY;
+                S[kt][r] = sv;
+                m = fmaxf(m, sv);
+            }
+        }
+        m = xrow_max(m);
+        float l = 0.0f;
+        u4v pa[2];  // A operands of the two PV products (fp16 pairs)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            float p[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[r] = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(S[kt][r] - m);
+                l += p[r];
+            }
+            pa[kt >> 1][2 * (kt & 1)] = (uint32_t)f2h(p[0]) | ((uint32_t)f2h(p[1]) << 16);
+            pa[kt >> 1][2 * (kt & 1) + 1] = (uint32_t)f2h(p[2]) | ((uint32_t)f2h(p[3]) << 16);
+        }
+        l = xrow_sum(l);
+        // O = P V: B lane (d, lq) = V^T[d][32 j + 4 lq .. + 3] and [32 j + 16 + 4 lq .. + 3]
+        f4 O[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) O[dt] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const uint16_t* vr = Vt + (16 * dt + ln) * VSTR + 32 * j + 4 * lq;
+                const uint2 lo4 = *(const uint2*)vr, hi4 = *(const uint2*)(vr + 16);
+                const u4v bv = {lo4.x, lo4.y, hi4.x, hi4.y};
+                O[dt] = mfma16x16x32(as_h8(pa[j]), as_h8(bv), O[dt]);
+            }
+        }
+        // lane (d, lq) holds O of query vectors 16 qt + 4 lq + r, dim 16 dt + ln
+        const size_t pbase = ((size_t)g * a.max_chunks + c) * (size_t)(nqt * 16);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+            float* op = a.opart + (pbase + qt * 16 + 4 * lq + r) * HD;
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) m[r] = fmaxf(m[r], __shfl_xor(m[r], o, MJ_WAVE));
+            for (int dt = 0; dt < 8; ++dt) op[16 * dt + ln] = O[dt][r];
         }
-        if (active) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-#pragma unroll
-                for (int kt = 0; kt < 4; ++kt) {
-                    const float p = m[r] == -INFINITY ? 0.0f : expf(S[kt][r] - m[r]);
-                    l[r] += p;
-                    Pw[(4 * lq + r) * VSTR + 16 * kt + ln] = f2h(p);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) l[r] += __shfl_xor(l[r], o, MJ_WAVE);
-        }
-        __syncthreads();  // P tile visible to the whole wave
-        if (active) {
-            f4 O[8];
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) O[dt] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const u4v av = *(const u4v*)(Pw + ln * VSTR + 32 * ks + 8 * lq);
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) {
-                    const u4v bv = *(const u4v*)(Vt + (16 * dt + ln) * VSTR + 32 * ks + 8 * lq);
-                    O[dt] = mfma16x16x32(as_h8(av), as_h8(bv), O[dt]);
-                }
-            }
-            const size_t pbase = ((size_t)g * a.max_chunks + c) * (size_t)(nqt * 16);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qv = qt * 16 + 4 * lq + r;
-                float* op = a.opart + (pbase + qv) * HD;
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) op[16 * dt + ln] = O[dt][r];
-                if (ln == 0) a.mlpart[pbase + qv] = make_float2(m[r], l[r]);
-            }
-        }
-        __syncthreads();  // before the next tile overwrites P
+        if (lq == 0) a.mlpart[pbase + qv] = make_float2(m, l);
     }
 }
 
-// One 256-thread block per (row, query head): wave w merges chunks w, w + 4, ... (lane = two
-// dims), then the four wave sums are added in wave order and the row is written in qx order.
-// Every chunk below the row's count holds a partial (a fully masked one has max -inf, sum 0).
+// One 256-thread block per (row, query head): wave w merges, in increasing order, the chunks
+// whose absolute index is w mod 4 (lane = two dims), then the four wave sums are added in wave
+// order and the row is written in qx order.  Every chunk of the pass holds a partial (a fully
+// masked one has max -inf, sum 0, output 0 and adds exact zeros), so a row's merge depends only
+// on the chunks that hold its keys.
 __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int r = blockIdx.x / a.nQ, hq = blockIdx.x % a.nQ;
     const int gqa = a.nQ / a.nKV;
     const int g = hq / gqa, qv = r * gqa + (hq % gqa);
     const size_t nq16 = (size_t)((a.M * gqa + 15) / 16) * 16;
-    const int64_t L = a.sd->L;
-    const int64_t lo_min = a.window > 0 ? (L - a.window + 1 > 0 ? L - a.window + 1 : 0) : 0;
-    const int64_t nk = (L - lo_min) + a.M;
-    const int nch = (int)((nk + AK - 1) / AK);
+    const ChunkGeom cg = chunk_geom(a.window, a.sd->L, a.M, a.sd->chain != 0);
+    const int nch = cg.nch;
+    const int cs = (int)(((int64_t)wv - cg.c0) & 3);  // this wave's first chunk
     const float2* ml = a.mlpart + (size_t)g * a.max_chunks * nq16 + qv;
     const float* op = a.opart + ((size_t)g * a.max_chunks * nq16 + qv) * HD + 2 * lane;
     float mx = -INFINITY;
     for (int c = lane; c < nch; c += 64) mx = fmaxf(mx, ml[(size_t)c * nq16].x);
     mx = wave_max(mx);
     float o0 = 0.0f, o1 = 0.0f, ls = 0.0f;
-    for (int c0 = wv; c0 < nch; c0 += 16) {
+    for (int cb = cs; cb < nch; cb += 16) {
         float2 m4[4], p4[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int c = c0 + 4 * j;
+            const int c = cb + 4 * j;
             m4[j] = make_float2(-INFINITY, 0.0f);
             p4[j] = make_float2(0.0f, 0.0f);
             if (c < nch) {
@@ -301,7 +514,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float w = m4[j].x == -INFINITY ? 0.0f : expf(m4[j].x - mx);
+            // log2 units
+            const float w = m4[j].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m4[j].x - mx);
             ls += m4[j].y * w;
             o0 += w * p4[j].x;
             o1 += w * p4[j].y;
@@ -336,11 +550,22 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
 
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
     if (a.M < 1 || a.M > MJ_ROWS) return hipErrorInvalidValue;  // row metadata is staged per row
+    // RoPE partners are found by lane moves: half = rope_dim / 2 in {16, 32, 64}
+    if (a.rope_dim != 0 && a.rope_dim != 32 && a.rope_dim != 64 && a.rope_dim != 128)
+        return hipErrorInvalidValue;
+    // key positions relative to L are packed as (p - L) * 128 + class in an int
+    if (a.C < 1 || a.C >= ((int64_t)1 << 23)) return hipErrorInvalidValue;
     const int gqa = a.nQ / a.nKV;
     const int nqt = (a.M * gqa + 15) / 16;
-    const size_t lds = (size_t)(nqt * 16 * QSTR + AK * QSTR + HD * VSTR + 4 * 16 * VSTR) * 2 +
-                       AK * (8 + 4) + MJ_ROWS * 16 + 16;
-    launch_timed(k_attn_chunk, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a);
+    const size_t lds = (size_t)(nqt * 16 * QSTR + AK * QSTR + HD * VSTR) * 2 +
+                       (size_t)tab_floats2(a.M, a.rope_dim / 2) * 8 + AK * 4 + MJ_ROWS * (4 + 8) +
+                       2 * HD * 2 + 16;
+    switch (a.rope_dim) {
+        case 0: launch_timed(k_attn_chunk<0>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
+        case 32: launch_timed(k_attn_chunk<16>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
+        case 64: launch_timed(k_attn_chunk<32>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
+        default: launch_timed(k_attn_chunk<64>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.M * a.nQ), dim3(256), 0, st, a);
@@ -348,6 +573,11 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
 }
 
 hipError_t set_attn_attributes() {
-    return hipFuncSetAttribute((const void*)k_attn_chunk,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    hipError_t e = hipSuccess;
+    const void* ks[] = {(const void*)k_attn_chunk<0>, (const void*)k_attn_chunk<16>,
+                        (const void*)k_attn_chunk<32>, (const void*)k_attn_chunk<64>};
+    for (const void* k : ks)
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    return e;
 }

@@ -14,9 +14,7 @@
 //
 // Epilogues: STORE y = half(acc); ADD y = half(y + half(acc)) (o-proj residual,
 // gqmm2_rows_fold_add 3488-3543); SWIGLU clamped SwiGLU of the up || gate row pair
-// (maple_clamped_swiglu 2435-2450) written in qx order with its block sums; QKV one head of
-// the dense qkv projection per block, finished with per-head RMSNorm + RoPE of q and k and
-// the K/V append (maple_qk_norm_rope + maple_write_kv_pair, 2794-2901).
+// (maple_clamped_swiglu 2435-2450) written in qx order with its block sums.
 #include <algorithm>
 #include <type_traits>
 
@@ -52,7 +50,6 @@ struct G5Shape {
     // staged 8 bytes a row and read as chunk 0 with its upper half zero
     static constexpr bool HSC = SCH == 0;
     static constexpr int SCW = HSC ? 1 : SCH / KS;  // ... per K-slice
-    static constexpr int ES = 129;             // QKV epilogue staging stride (floats)
     static constexpr int WCODE = 16 * KBW * 16;  // bytes of one wave's code tile
     static constexpr int WSB = 16 * SCW * 16;    // bytes of one wave's scales (and of its biases)
     static constexpr int WAVE_BYTES = WCODE + 2 * WSB;
@@ -66,7 +63,7 @@ struct G5Shape {
     // finishes)
     __host__ __device__ static size_t lds(int RA, bool multi, bool dbl = false) {
         return (size_t)WPB * WAVE_BYTES + (dbl ? 2 : 1) * ((size_t)RA * XS * 2 + (size_t)RA * SS * 8) +
-               (EPI == EPI_QKV ? (size_t)R * ES * 4 : 0) + (multi ? RED : 0);
+               (multi ? RED : 0);
     }
 };
 
@@ -123,10 +120,9 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     GatherArgs a, int RA, int multi) {
     using S = G5Shape<KPL, GS, EPI, WPB, KS>;
     constexpr int R = S::R, K = S::K, KB = S::KB, KBW = S::KBW, TPB = S::TPB, XS = S::XS;
-    constexpr int ES = S::ES, SCW = S::SCW;
+    constexpr int SCW = S::SCW;
     constexpr int NT = WPB * 64;
     constexpr int PPR = K / 8;                 // 16-byte parts per activation row
-    static_assert(EPI != EPI_QKV || TPB == 8, "one 128-row head per block");
     static_assert(PPR % 64 == 0 && R % WPB == 0 && SCW >= 1 && SCW <= 4 && KBW % 4 == 0, "shape");
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -184,8 +180,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     constexpr int NBUF = PER ? 2 : 1;
     uint16_t* const xs0 = (uint16_t*)(g5lds + (size_t)WPB * S::WAVE_BYTES);  // [RA][XS] qx rows
     float2* const xsl0 = (float2*)(xs0 + RA * XS);  // [RA][SS] {sum x, sum base*x}
-    float* el = (float*)(xsl0 + RA * S::SS);        // [R][ES] QKV epilogue staging
-    char* red = (char*)el + (EPI == EPI_QKV ? R * ES * 4 : 0);  // [KS-1][TPB][64] f4
+    char* red = (char*)(xsl0 + RA * S::SS);  // [KS-1][TPB][64] f4
     __shared__ int s_pair[NBUF][R];
     int buf = 0;
     auto xs_of = [&](int) { return xs0; };
@@ -497,56 +492,6 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
                     a.y[(size_t)s_pair[buf][i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
                 }
             }
-        } else if constexpr (EPI == EPI_QKV) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 4 * q + r;
-                if (kh == 0 && i < npass) el[i * ES + 16 * tt + n] = hround(acc[r]);
-            }
-            __syncthreads();
-            const QkvEpi& qe = a.qkv;
-            const int hh = cb;  // head of this block: q heads, then k heads, then v heads
-            for (int i = wv; i < npass; i += WPB) {
-                const int m = pb + i;
-                float v0 = el[i * ES + 2 * lane], v1 = el[i * ES + 2 * lane + 1];
-                if (hh < qe.nQ + qe.nKV) {
-                    const float ss = wave_sum(v0 * v0 + v1 * v1);
-                    const float scl = 1.0f / sqrtf(ss / 128.0f + qe.eps);
-                    const uint16_t* wn = hh < qe.nQ ? qe.q_norm_w : qe.k_norm_w;
-                    const uint32_t wpair = *(const uint32_t*)(wn + 2 * lane);
-                    v0 = v0 * scl * h2f((uint16_t)wpair);
-                    v1 = v1 * scl * h2f((uint16_t)(wpair >> 16));
-                    const int rd = qe.rope_dim;
-                    if (rd > 0) {
-                        const int half = rd / 2;
-                        const float u0 = __shfl_xor(v0, half / 2, MJ_WAVE);
-                        const float u1 = __shfl_xor(v1, half / 2, MJ_WAVE);
-                        const float pos = (float)(qe.sd->L + qe.sd->depth[m]);
-                        const int j0 = 2 * lane;
-                        if (j0 < rd) {
-                            const int f0 = j0 < half ? j0 : j0 - half;
-                            const float t0 = pos * qe.inv_freq[f0], t1 = pos * qe.inv_freq[f0 + 1];
-                            const float c0 = cosf(t0), s0 = sinf(t0), c1 = cosf(t1), s1 = sinf(t1);
-                            if (j0 < half) {
-                                v0 = v0 * c0 - u0 * s0;
-                                v1 = v1 * c1 - u1 * s1;
-                            } else {
-                                v0 = v0 * c0 + u0 * s0;
-                                v1 = v1 * c1 + u1 * s1;
-                            }
-                        }
-                    }
-                }
-                const uint32_t o = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
-                if (hh < qe.nQ) {
-                    *(uint32_t*)(qe.qbuf + ((size_t)m * qe.nQ + hh) * 128 + 2 * lane) = o;
-                } else {
-                    const int g = hh < qe.nQ + qe.nKV ? hh - qe.nQ : hh - qe.nQ - qe.nKV;
-                    const int64_t slot = (qe.sd->L + m) % qe.C;
-                    uint16_t* dst = hh < qe.nQ + qe.nKV ? qe.kc : qe.vc;
-                    *(uint32_t*)(dst + ((size_t)g * qe.C + slot) * 128 + 2 * lane) = o;
-                }
-            }
         } else {
             const int col = (cb * TPB + tt) * 16 + n;
 #pragma unroll
@@ -619,13 +564,12 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     return hipGetLastError();
 }
 
-// Shapes the tile kernel covers: SWIGLU / QKV / ADD at K = 2048, STORE at K = 512, 1024 or
-// 2048; N a multiple of the block's rows; group size 64 or 128.
+// Shapes the tile kernel covers: SWIGLU / ADD at K = 2048, STORE at K = 512, 1024 or 2048; N
+// a multiple of the block's rows; group size 64 or 128.
 bool gather3_supported(int epi, int K, int N, int gs) {
     if (gs != 64 && gs != 128) return false;
     switch (epi) {
         case EPI_SWIGLU: return K == 2048 && N % 64 == 0;
-        case EPI_QKV: return K == 2048 && N % 128 == 0;
         case EPI_ADD: return K == 2048 && N % 64 == 0;
         case EPI_STORE: return (K == 512 || K == 1024 || K == 2048) && N % 64 == 0;
     }
@@ -664,13 +608,17 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
                           : launch_g5<KPL, 128, E, W, KS128, true>(a, rows, n_buckets, st); \
     return a.gs == 64 ? launch_g5<KPL, 64, E, W, KS64>(a, rows, n_buckets, st)              \
                       : launch_g5<KPL, 128, E, W, KS128>(a, rows, n_buckets, st);
+    // dense projections (qkv, o-proj: a few MB at most) spread over many small blocks, four
+    // waves of one 16-row tile (group 64) or two (group 128): the unpack work of a block is
+    // then short, and the launch fills the chip
+    const bool dense = a.srec == nullptr && a.ecnt == nullptr && a.bk == nullptr;
     switch (epi) {
         case EPI_SWIGLU: MJ_G5(8, EPI_SWIGLU, 8, 2, 2)
-        case EPI_QKV: MJ_G5(8, EPI_QKV, 16, 2, 2)
-        case EPI_ADD: MJ_G5(8, EPI_ADD, 8, 4, 2)
+        case EPI_ADD: MJ_G5(8, EPI_ADD, 4, 4, 2)
         case EPI_STORE:
             if (a.K == 512) { MJ_G5(2, EPI_STORE, 8, 1, 1) }
             if (a.K == 1024) { MJ_G5(4, EPI_STORE, 8, 1, 1) }
+            if (dense) { MJ_G5(8, EPI_STORE, 4, 4, 2) }
             MJ_G5(8, EPI_STORE, 8, 2, 2)
     }
 #undef MJ_G5
@@ -692,8 +640,8 @@ hipError_t set_gather3_attributes() {
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, W, KS128>();        \
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, W, KS64, true>();    \
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, W, KS128, true>();
-    MJ_A(8, EPI_SWIGLU, 8, 2, 2) MJ_A(8, EPI_QKV, 16, 2, 2) MJ_A(8, EPI_ADD, 8, 4, 2)
-    MJ_A(2, EPI_STORE, 8, 1, 1) MJ_A(4, EPI_STORE, 8, 1, 1) MJ_A(8, EPI_STORE, 8, 2, 2)
+    MJ_A(8, EPI_SWIGLU, 8, 2, 2) MJ_A(8, EPI_ADD, 4, 4, 2) MJ_A(2, EPI_STORE, 8, 1, 1)
+    MJ_A(4, EPI_STORE, 8, 1, 1) MJ_A(8, EPI_STORE, 8, 2, 2) MJ_A(8, EPI_STORE, 4, 4, 2)
 #undef MJ_A
 #define MJ_AA(KPL, E, KS64, KS128)                                              \
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, 8, KS64, true, true>();        \

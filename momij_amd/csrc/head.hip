@@ -680,28 +680,43 @@ hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, in
     return hipGetLastError();
 }
 
+// RoPE angles of pass row r (its position L + depth[r]) for frequencies t < rt.half; called by
+// the first rt.half threads of the row's block.  The same cosf / sinf of pos * inv_freq[f] as
+// maple_qk_norm_rope's angle (SeedlessMetal.swift:2832-2846), evaluated once per pass.
+__device__ __forceinline__ void rope_row(const StepDesc* sd, const RopeTab& rt, int r, int t) {
+    if (t < rt.half) {
+        const float pos = (float)(sd->L + sd->depth[r]);
+        const float th = pos * rt.inv_freq[t];
+        rt.cs[r * MJ_ROPE_F + t] = make_float2(cosf(th), sinf(th));
+    }
+}
+
 // Token embedding: h[r] = table[tokens[r]] (maple_embed_token, SeedlessMetal.swift:3114-3126).
 __global__ __launch_bounds__(256) void k_embed(const uint16_t* table, const StepDesc* sd, int M,
-                                               int H, uint16_t* h, const int* abort) {
+                                               int H, uint16_t* h, RopeTab rt, const int* abort) {
     if (aborted(abort)) return;
     const int r = blockIdx.x;
     if (r >= M) return;
+    rope_row(sd, rt, r, threadIdx.x);
     const int tok = sd->tokens[r];
     for (int i = threadIdx.x; i < H / 8; i += 256)
         *(u4v*)(h + (size_t)r * H + 8 * i) = *(const u4v*)(table + (size_t)tok * H + 8 * i);
 }
 
 hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
-                        const int* abort, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed, dim3(M), dim3(256), 0, st, table, sd, M, H, h, abort);
+                        const RopeTab& rt, const int* abort, hipStream_t st) {
+    if (rt.half > MJ_ROPE_F || M > MJ_ROWS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed, dim3(M), dim3(256), 0, st, table, sd, M, H, h, rt, abort);
     return hipGetLastError();
 }
 
 // Token embedding of a 2048-wide row followed by the first layer's input RMSNorm.
 __global__ __launch_bounds__(256) void k_embed_norm(const uint16_t* table, const StepDesc* sd,
-                                                    uint16_t* h, NormOut no, const int* abort) {
+                                                    uint16_t* h, NormOut no, RopeTab rt,
+                                                    const int* abort) {
     if (aborted(abort)) return;
     const int r = blockIdx.x, t = threadIdx.x;
+    rope_row(sd, rt, r, t);
     const int tok = sd->tokens[r];
     const u4v v = *(const u4v*)(table + (size_t)tok * 2048 + 8 * t);
     *(u4v*)(h + (size_t)r * 2048 + 8 * t) = v;
@@ -709,9 +724,21 @@ __global__ __launch_bounds__(256) void k_embed_norm(const uint16_t* table, const
 }
 
 hipError_t launch_embed_norm(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
-                             const NormOut& no, const int* abort, hipStream_t st) {
-    if (H != 2048) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_embed_norm, dim3(M), dim3(256), 0, st, table, sd, h, no, abort);
+                             const NormOut& no, const RopeTab& rt, const int* abort,
+                             hipStream_t st) {
+    if (H != 2048 || rt.half > MJ_ROPE_F || M > MJ_ROWS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed_norm, dim3(M), dim3(256), 0, st, table, sd, h, no, rt, abort);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(64) void k_rope_table(const StepDesc* sd, RopeTab rt) {
+    rope_row(sd, rt, blockIdx.x, threadIdx.x);
+}
+
+hipError_t launch_rope_table(const StepDesc* sd, int M, const RopeTab& rt, hipStream_t st) {
+    if (rt.half > MJ_ROPE_F || M > MJ_ROWS) return hipErrorInvalidValue;
+    if (rt.half == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_table, dim3(M), dim3(64), 0, st, sd, rt);
     return hipGetLastError();
 }
 

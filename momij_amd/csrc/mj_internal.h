@@ -39,7 +39,7 @@ struct Buckets {
     int pair[MJ_MAX_PAIRS];
 };
 
-enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
+enum { EPI_STORE = 0, EPI_ADD = 1, EPI_SWIGLU = 2 };
 
 // Outputs of a fused RMSNorm over 2048-element rows: out = half(x * rsqrt(mean x^2 + eps) * w)
 // written plain and / or in qx order with its per-64 block sums.
@@ -59,7 +59,7 @@ struct NormOut {
 struct StepDesc {
     int64_t L;
     int32_t M;
-    int32_t pad0;
+    int32_t chain;           // 1: parents[r] = r - 1 for every row (depth[r] = r)
     int32_t tokens[MJ_ROWS];
     int32_t parents[MJ_ROWS];
     int32_t depth[MJ_ROWS];
@@ -81,20 +81,6 @@ struct StepResult {
     int32_t argmax[MJ_ROWS];
 };
 
-// EPI_QKV: the dense qkv projection finishes each head in place -- per-head RMSNorm and RoPE
-// of q and k at the row's position, q to qbuf, k and v appended to the KV cache.
-struct QkvEpi {
-    const uint16_t* q_norm_w;  // [128]
-    const uint16_t* k_norm_w;  // [128]
-    const float* inv_freq;     // [rope_dim/2]
-    const StepDesc* sd;        // L, depth
-    uint16_t* qbuf;            // [M][nQ][128]
-    uint16_t* kc;              // [nKV][C][128]
-    uint16_t* vc;
-    int64_t C;
-    int nQ, nKV, rope_dim;
-    float eps;
-};
 
 // Row sets of a gather launch (grid = groups x column blocks):
 //   ecnt != nullptr (tile kernel): group u = expert u with ecnt[u] pairs listed, in no
@@ -121,7 +107,6 @@ struct GatherArgs {
     int K, N, gs;
     int x_div;              // x row of pair p = p / x_div
     const int* abort;
-    QkvEpi qkv;             // EPI_QKV only
 };
 
 struct QmvArgs {
@@ -150,13 +135,22 @@ bool gather3_supported(int epi, int K, int N, int gs);
 hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets,
                           hipStream_t st);
 
+// RoPE angles of a pass: rope_cs[r * MJ_ROPE_F + f] = {cos, sin} of (L + depth[r]) *
+// inv_freq[f] for row r and frequency f < rope_dim / 2, written by the pass's embedding kernel
+// (or k_rope_table) so that no layer evaluates a sine.
+#define MJ_ROPE_F 64
+struct RopeTab {
+    const float* inv_freq;  // [half]
+    float2* cs;             // [MJ_ROWS][MJ_ROPE_F]
+    int half;               // rope_dim / 2 (0: no RoPE layer in the model)
+};
+
 struct AttnArgs {
-    const uint16_t* qkv;     // [M][(nQ+2nKV)*128] projection output (plain)
+    const uint16_t* qkv;     // [M][(nQ+2nKV)*128] projection output (plain, raw q / k / v)
     const uint16_t* q_norm_w;
     const uint16_t* k_norm_w;
-    const float* inv_freq;   // [rope_dim/2]
+    const float2* rope_cs;   // RopeTab::cs of the pass
     const StepDesc* sd;
-    uint16_t* qbuf;          // [M][nQ][128] normed + rotated queries
     uint16_t* kc;            // [nKV][C][128]
     uint16_t* vc;
     float* opart;            // [nKV][max_chunks][nqt*16][128] partial outputs
@@ -170,7 +164,6 @@ struct AttnArgs {
 };
 
 // attn.hip
-hipError_t launch_qknorm_rope_kv(const AttnArgs& a, hipStream_t st);
 hipError_t launch_attn(const AttnArgs& a, hipStream_t st);
 int attn_max_chunks(int window, int64_t L_max, int M);
 
@@ -195,10 +188,13 @@ hipError_t launch_kv_commit(uint16_t* kv, int64_t layer_stride, int n_layers, in
                             hipStream_t st);
 hipError_t launch_kv_rows(const uint16_t* kv, int64_t layer_stride, int n_layers, int64_t C,
                           int nKV, const StepDesc* sd, uint16_t* dst, hipStream_t st);
+// The embedding kernels also write the pass's RoPE table (rt.half == 0: none).
 hipError_t launch_embed(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
-                        const int* abort, hipStream_t st);
+                        const RopeTab& rt, const int* abort, hipStream_t st);
 hipError_t launch_embed_norm(const uint16_t* table, const StepDesc* sd, int M, int H, uint16_t* h,
-                             const NormOut& no, const int* abort, hipStream_t st);  // H = 2048
+                             const NormOut& no, const RopeTab& rt, const int* abort,
+                             hipStream_t st);  // H = 2048
+hipError_t launch_rope_table(const StepDesc* sd, int M, const RopeTab& rt, hipStream_t st);
 // One wave that waits `us` microseconds of wall-clock time (bounded), so that the host can
 // queue the launches that follow it before the GPU reaches them.
 hipError_t launch_hold(unsigned us, hipStream_t st);

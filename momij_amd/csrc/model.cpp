@@ -35,7 +35,8 @@ struct mj_model {
     int max_chunks = 0;
     // pass scratch
     void* arena = nullptr;
-    uint16_t *h, *xperm, *qkv, *qbuf, *aperm, *xf;
+    uint16_t *h, *xperm, *qkv, *aperm, *xf;
+    float2* rope_cs;
     float2 *xsum, *asum, *mlpart;
     float *opart, *pval, *rowmax, *logits, *bsum, *maxv;
     int* pidx;
@@ -65,12 +66,14 @@ static mj_status model_fail(mj_model* m, mj_status s, const char* what) {
 
 // Depth and ancestor masks of a pass; parents == nullptr means a chain.
 static mj_status fill_tree(mj_ctx* ctx, StepDesc* sd, const int32_t* parents, int M) {
+    sd->chain = 1;
     for (int r = 0; r < M; ++r) {
         const int p = parents ? parents[r] : r - 1;
         if (r == 0 ? p != -1 : (p < 0 || p >= r))
             return mj_fail(ctx, MJ_INVALID_ARG, "bad tree: parents[%d] = %d (need parents[0] = -1,"
                            " 0 <= parents[r] < r)", r, p);
         sd->parents[r] = p;
+        if (p != r - 1) sd->chain = 0;
         sd->depth[r] = r == 0 ? 0 : sd->depth[p] + 1;
         sd->anc[r] = (r == 0 ? 0ull : sd->anc[p]) | (1ull << r);
     }
@@ -105,33 +108,17 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, int kind, hipStream_t 
     q.x_div = 1;
     q.abort = ab;
     Prof* pf = m->profiling ? &m->prof : nullptr;
-    // the qkv tile kernel finishes q/k-norm, RoPE and the KV append in its epilogue
-    const bool fused_qkv = gather3_supported(EPI_QKV, H, qkvN, c.gs);
-    if (fused_qkv) {
-        q.qkv.q_norm_w = (const uint16_t*)w.attn.q_norm_w;
-        q.qkv.k_norm_w = (const uint16_t*)w.attn.k_norm_w;
-        q.qkv.inv_freq = m->inv_freq;
-        q.qkv.sd = m->sd_dev;
-        q.qkv.qbuf = m->qbuf;
-        q.qkv.kc = m->kv + (int64_t)l * m->layer_stride;
-        q.qkv.vc = q.qkv.kc + (int64_t)nKV * c.kv_capacity * 128;
-        q.qkv.C = c.kv_capacity;
-        q.qkv.nQ = nQ;
-        q.qkv.nKV = nKV;
-        q.qkv.rope_dim = m->lrope[l];
-        q.qkv.eps = c.eps;
-    }
+    // raw q / k / v rows; the attention kernel finishes q and k and appends k and v
     if (pf) pf->begin(PROF_DENSE, st);
-    s = mj_hip(ctx, launch_gather(q, fused_qkv ? EPI_QKV : EPI_STORE, M, 1, st), "qkv");
+    s = mj_hip(ctx, launch_gather(q, EPI_STORE, M, 1, st), "qkv");
     if (pf) pf->end(st);
     if (s != MJ_OK) return s;
     AttnArgs a{};
     a.qkv = m->qkv;
     a.q_norm_w = (const uint16_t*)w.attn.q_norm_w;
     a.k_norm_w = (const uint16_t*)w.attn.k_norm_w;
-    a.inv_freq = m->inv_freq;
+    a.rope_cs = m->rope_cs;
     a.sd = m->sd_dev;
-    a.qbuf = m->qbuf;
     a.kc = m->kv + (int64_t)l * m->layer_stride;
     a.vc = a.kc + (int64_t)nKV * c.kv_capacity * 128;
     a.opart = m->opart;
@@ -148,10 +135,6 @@ static mj_status enqueue_layer(mj_model* m, int l, int M, int kind, hipStream_t 
     a.eps = c.eps;
     a.scale = (float)std::pow((double)D, -0.5);
     a.abort = ab;
-    if (!fused_qkv) {
-        s = mj_hip(ctx, launch_qknorm_rope_kv(a, st), "qk norm rope");
-        if (s != MJ_OK) return s;
-    }
     if (pf) pf->begin(PROF_ATTN, st);
     s = mj_hip(ctx, launch_attn(a, st), "attention");
     if (pf) pf->end(st);
@@ -215,11 +198,12 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
     mj_status s;
     const NormOut first{(const uint16_t*)m->layers[0].attn.norm_w, c.eps, nullptr, m->xperm,
                         m->xsum};
+    const RopeTab rt{m->inv_freq, m->rope_cs, c.rope_dim / 2};
     if (H == 2048) {
-        s = mj_hip(ctx, launch_embed_norm(m->embed, m->sd_dev, M, H, m->h, first, ab, st),
+        s = mj_hip(ctx, launch_embed_norm(m->embed, m->sd_dev, M, H, m->h, first, rt, ab, st),
                    "embed + norm");
     } else {
-        s = mj_hip(ctx, launch_embed(m->embed, m->sd_dev, M, H, m->h, ab, st), "embed");
+        s = mj_hip(ctx, launch_embed(m->embed, m->sd_dev, M, H, m->h, rt, ab, st), "embed");
         if (s == MJ_OK)
             s = mj_hip(ctx, launch_rmsnorm_qx(m->h, first.w, c.eps, nullptr, m->xperm, m->xsum, M,
                                               H, ab, st), "attn norm");
@@ -465,7 +449,7 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         m->xperm = (uint16_t*)a.take((size_t)R * H * 2);
         m->xsum = (float2*)a.take((size_t)R * (H / 64) * 8);
         m->qkv = (uint16_t*)a.take((size_t)R * qkvN * 2);
-        m->qbuf = (uint16_t*)a.take((size_t)R * nQ * 128 * 2);
+        m->rope_cs = (float2*)a.take((size_t)R * MJ_ROPE_F * sizeof(float2));
         m->opart = (float*)a.take((size_t)nKV * m->max_chunks * nqt16 * 128 * 4);
         m->mlpart = (float2*)a.take((size_t)nKV * m->max_chunks * nqt16 * 8);
         m->aperm = (uint16_t*)a.take((size_t)R * nQ * 128 * 2);
@@ -742,7 +726,7 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
         p[0] = a.take((size_t)M * H * 2);                 // xperm
         p[1] = a.take((size_t)M * (H / 64) * 8);          // xsum
         p[2] = a.take((size_t)M * qkvN * 2);              // qkv
-        p[3] = a.take((size_t)M * nQ * 128 * 2);          // qbuf
+        p[3] = a.take((size_t)M * MJ_ROPE_F * sizeof(float2));  // RoPE table
         p[4] = a.take((size_t)nKV * maxc * nqt16 * 128 * 4);
         p[5] = a.take((size_t)nKV * maxc * nqt16 * 8);
         p[6] = a.take((size_t)M * nQ * 128 * 2);          // aperm
@@ -782,30 +766,17 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
     q.gs = c.gs;
     q.x_div = 1;
     q.abort = ab;
-    const bool fused_qkv = gather3_supported(EPI_QKV, H, qkvN, c.gs);
-    if (fused_qkv) {
-        q.qkv.q_norm_w = (const uint16_t*)w->q_norm_w;
-        q.qkv.k_norm_w = (const uint16_t*)w->k_norm_w;
-        q.qkv.inv_freq = (const float*)p[9];
-        q.qkv.sd = (const StepDesc*)p[8];
-        q.qkv.qbuf = (uint16_t*)p[3];
-        q.qkv.kc = (uint16_t*)kcache;
-        q.qkv.vc = (uint16_t*)vcache;
-        q.qkv.C = c.kv_capacity;
-        q.qkv.nQ = nQ;
-        q.qkv.nKV = nKV;
-        q.qkv.rope_dim = c.rope_dim;
-        q.qkv.eps = c.eps;
-    }
-    s = mj_hip(ctx, launch_gather(q, fused_qkv ? EPI_QKV : EPI_STORE, M, 1, st), "qkv");
+    const RopeTab rt{(const float*)p[9], (float2*)p[3], c.rope_dim / 2};
+    s = mj_hip(ctx, launch_rope_table((const StepDesc*)p[8], M, rt, st), "rope table");
+    if (s != MJ_OK) return s;
+    s = mj_hip(ctx, launch_gather(q, EPI_STORE, M, 1, st), "qkv");
     if (s != MJ_OK) return s;
     AttnArgs a{};
     a.qkv = (uint16_t*)p[2];
     a.q_norm_w = (const uint16_t*)w->q_norm_w;
     a.k_norm_w = (const uint16_t*)w->k_norm_w;
-    a.inv_freq = (float*)p[9];
+    a.rope_cs = (const float2*)p[3];
     a.sd = (StepDesc*)p[8];
-    a.qbuf = (uint16_t*)p[3];
     a.kc = (uint16_t*)kcache;
     a.vc = (uint16_t*)vcache;
     a.opart = (float*)p[4];
@@ -822,8 +793,7 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
     a.eps = c.eps;
     a.scale = (float)std::pow(128.0, -0.5);
     a.abort = ab;
-    if (!fused_qkv) s = mj_hip(ctx, launch_qknorm_rope_kv(a, st), "qk norm rope");
-    if (s == MJ_OK) s = mj_hip(ctx, launch_attn(a, st), "attention");
+    s = mj_hip(ctx, launch_attn(a, st), "attention");
     if (s != MJ_OK) return s;
     GatherArgs o{};
     o.xperm = (uint16_t*)p[6];

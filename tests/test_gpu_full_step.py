@@ -104,6 +104,27 @@ def test_full_chain_k8(full, orc):
     assert oacc == acc and list(oemit) == toks
 
 
+def test_full_chain_rows_bitwise_equal_one_row_steps(full):
+    """At full size: the 9 rows of a K = 8 chain pass give bit for bit the head input and
+    logits of nine one-row steps at the same positions (chain evals == sequential,
+    RealTextParityTests.swift:96-111, here on the bits rather than the tokens)."""
+    eng, cfg, y, cont = full["eng"], full["cfg"], full["y"], full["cont"]
+    print("case: full step, chain rows == one-row steps, bitwise", flush=True)
+    L0 = eng.offset
+    feeds = [y] + cont[:4] + [int(t) for t in np.random.default_rng(13).integers(0, cfg.vocab, 4)]
+    head, logits = [], []
+    for t in feeds:
+        _, cap = capture_pass(eng, lambda: eng.step_chain_feeds([t]))
+        head.append(cap["head_in"][0].copy())
+        logits.append(cap["logits"][0].copy())
+    eng.rewind(L0)
+    _, cap = capture_pass(eng, lambda: eng.step_chain_feeds(feeds))
+    eng.rewind(L0)
+    M = len(feeds)
+    assert (cap["head_in"][:M].view(np.uint16) == np.stack(head).view(np.uint16)).all()
+    assert (cap["logits"][:M].view(np.uint32) == np.stack(logits).view(np.uint32)).all()
+
+
 def test_full_tree16_commit_and_next_pass(full, orc):
     eng, cfg, y, cont = full["eng"], full["cfg"], full["y"], full["cont"]
     print("case: full step, 16-node tree verify, commit, next chain pass", flush=True)

@@ -168,6 +168,29 @@ def test_mrow_verify_equals_sequential(model):
     assert acc == 8 and toks == cont[:9]
 
 
+def test_chain_rows_bitwise_equal_one_row_steps(model):
+    """Every row of a chain pass computes bit for bit what a one-row step at its position
+    computes: head input and head logits compared as bits over a 9-row pass and nine one-row
+    steps from the same cache.  Speculative verification is then lossless by construction
+    (the reference checks the tokens: RealTextParityTests.swift:96-111)."""
+    eng = model["eng"]
+    rng = np.random.default_rng(21)
+    eng.rewind(0)
+    y = eng.prefill(rng.integers(0, model["cfg"].vocab, 75).tolist())
+    L0 = eng.offset
+    feeds = [y] + [int(t) for t in rng.integers(0, model["cfg"].vocab, 8)]
+    head, logits = [], []
+    for t in feeds:
+        _, cap = capture_pass(eng, lambda: eng.step_chain_feeds([t]))
+        head.append(cap["head_in"][0].copy())
+        logits.append(cap["logits"][0].copy())
+    eng.rewind(L0)
+    _, cap = capture_pass(eng, lambda: eng.step_chain_feeds(feeds))
+    M = len(feeds)
+    assert (cap["head_in"][:M].view(np.uint16) == np.stack(head).view(np.uint16)).all()
+    assert (cap["logits"][:M].view(np.uint32) == np.stack(logits).view(np.uint32)).all()
+
+
 def test_tree_verify_and_compaction(model, orc):
     eng, cfg = model["eng"], model["cfg"]
     print("case: 2-layer model, 16-node tree verify + KV commit", flush=True)
