@@ -211,6 +211,33 @@ mj_status mj_accept_sampled(mj_ctx* ctx, const float* logits, int rows, int V,
                             const int32_t* draft, float temperature, int q_mode,
                             const float* q_point, uint64_t seed, uint64_t counter, int32_t* out);
 
+/* LogitsProcessor options (LogitsProcessor.swift:17-49): temperature > 1e-5; top_p (nucleus,
+ * 1 = off, clamped to [0, 1]); repetition (1 = off, > 0), presence and frequency (0 = off)
+ * penalties.  hist_tokens / hist_counts (host, n_hist <= MJ_MAX_HIST, tokens distinct): the
+ * seen set and the counts the penalties read (prepare, 91-104); drafts accepted in the walk
+ * join both before the next row (walkDraft, SpeculativeSampling.swift:86-87). */
+#define MJ_MAX_HIST 65536
+typedef struct mj_sampling {
+    float temperature;
+    float top_p;
+    float repetition_penalty;
+    float presence_penalty;
+    float frequency_penalty;
+    const int32_t* hist_tokens;
+    const int32_t* hist_counts;
+    int n_hist;
+} mj_sampling;
+
+/* mj_accept_sampled with the options: every row's logits penalised (row i with the history
+ * plus drafts 0 .. i-1; the caller's logits are not modified), the bonus and a residual of zero
+ * mass sampled through samplePrepared's nucleus (LogitsProcessor.swift:137-164): tokens ranked
+ * by e descending, the lower id first among equal e, kept up to the first ranked prefix whose
+ * blocked prefix sum reaches top_p * Z, sampled in id order at u * (kept mass). */
+mj_status mj_accept_sampled_ex(mj_ctx* ctx, const float* logits, int rows, int V,
+                               const int32_t* draft, const mj_sampling* s, int q_mode,
+                               const float* q_point, uint64_t seed, uint64_t counter,
+                               int32_t* out);
+
 /* ---------------------------------------------------------------- model ------ */
 typedef struct mj_model_config {
     int n_layers;
@@ -277,6 +304,13 @@ mj_status mj_verify_greedy(mj_model* model, int32_t y, const int32_t* draft, int
 mj_status mj_verify_sampled(mj_model* model, int32_t y, const int32_t* draft, int n_draft,
                             float temperature, int q_mode, const float* q_point, uint64_t seed,
                             uint64_t counter, int32_t* out_accepted, int32_t* out_token);
+/* mj_verify_sampled with LogitsProcessor options (mj_accept_sampled_ex's rules) --
+ * verifyDraftSampled (SeedlessDecodeEngine.swift:1541-1571) with the processor's penalties
+ * and nucleus. */
+mj_status mj_verify_sampled_ex(mj_model* model, int32_t y, const int32_t* draft, int n_draft,
+                               const mj_sampling* s, int q_mode, const float* q_point,
+                               uint64_t seed, uint64_t counter, int32_t* out_accepted,
+                               int32_t* out_token);
 
 /* Debug capture for layer-by-layer checks: when set, each pass copies h after the embedding
  * and after every layer into h_capture fp16 [n_layers+1][MJ_MAX_ROWS][H], the routing into

@@ -65,6 +65,27 @@ class LayerWeights(C.Structure):
     _fields_ = [("attn", AttnWeights), ("moe", MoeWeights)]
 
 
+class Sampling(C.Structure):
+    _fields_ = [("temperature", f32), ("top_p", f32), ("repetition_penalty", f32),
+                ("presence_penalty", f32), ("frequency_penalty", f32), ("hist_tokens", vp),
+                ("hist_counts", vp), ("n_hist", i32)]
+
+
+MJ_MAX_HIST = 65536
+
+
+def sampling(temperature, top_p=1.0, rep=1.0, pres=0.0, freq=0.0, hist=None):
+    """mj_sampling for the given options; hist: {token: count} (the seen set and counts).
+    Returns (struct, keep-alive arrays)."""
+    toks = list(hist.keys()) if hist else []
+    ht = (C.c_int32 * max(len(toks), 1))(*[int(t) for t in toks])
+    hc = (C.c_int32 * max(len(toks), 1))(*[int(hist[t]) for t in toks])
+    sp = Sampling(float(temperature), float(top_p), float(rep), float(pres), float(freq),
+                  C.cast(ht, C.c_void_p) if toks else None,
+                  C.cast(hc, C.c_void_p) if toks else None, len(toks))
+    return sp, (ht, hc)
+
+
 class Capture(C.Structure):
     _fields_ = [("h", vp), ("inds", vp), ("logits", vp), ("attn_out", vp), ("moe_in", vp),
                 ("router_logits", vp), ("head_in", vp), ("kv_rows", vp)]
@@ -112,6 +133,8 @@ _SIGS = {
     "mj_recycle_index_entries": (i32, [vp]),
     "mj_accept_greedy": (i32, [vp, vp, vp, vp, i32, vp]),
     "mj_accept_sampled": (i32, [vp, vp, i32, i32, vp, f32, i32, vp, u64, u64, vp]),
+    "mj_accept_sampled_ex": (i32, [vp, vp, i32, i32, vp, C.POINTER(Sampling), i32, vp, u64, u64,
+                                   vp]),
     "mj_model_create": (i32, [vp, C.POINTER(ModelConfig), vp, vp, vp, vp, C.POINTER(vp)]),
     "mj_model_destroy": (i32, [vp]),
     "mj_model_offset": (i64, [vp]),
@@ -121,6 +144,8 @@ _SIGS = {
     "mj_step_chain_feeds": (i32, [vp, vp, i32, vp]),
     "mj_verify_greedy": (i32, [vp, i32, vp, i32, vp, vp, vp]),
     "mj_verify_sampled": (i32, [vp, i32, vp, i32, f32, i32, vp, u64, u64, vp, vp]),
+    "mj_verify_sampled_ex": (i32, [vp, i32, vp, i32, C.POINTER(Sampling), i32, vp, u64, u64, vp,
+                                   vp]),
     "mj_model_set_capture": (i32, [vp, vp, vp, vp]),
     "mj_model_set_capture_ex": (i32, [vp, C.POINTER(Capture)]),
     "mj_model_set_graphs": (i32, [vp, i32]),

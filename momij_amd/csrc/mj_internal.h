@@ -70,6 +70,9 @@ struct StepDesc {
     int32_t q_mode;
     int32_t has_qpoint;
     float q_point[MJ_ROWS];
+    // LogitsProcessor options of a sampled pass (the history itself is in a device buffer)
+    float top_p, rep, pres, freq;
+    int32_t n_hist;
 };
 
 // Result of a verify pass (device, copied back once per step).
@@ -200,11 +203,39 @@ hipError_t launch_rope_table(const StepDesc* sd, int M, const RopeTab& rt, hipSt
 hipError_t launch_hold(unsigned us, hipStream_t st);
 
 // sample.hip
-hipError_t launch_accept_sampled(const float* logits, int rows, int V, const int32_t* draft,
+// LogitsProcessor options (LogitsProcessor.swift:17-104): the penalties change the logits in
+// place (the buffer must be writable), the nucleus needs a NucleusBuf.
+struct SampleOpts {
+    float top_p = 1.0f, rep = 1.0f, pres = 0.0f, freq = 0.0f;
+    const int32_t* hist_tok = nullptr;  // device, ascending, distinct (the seen set)
+    const int32_t* hist_cnt = nullptr;  // device, their counts
+    int n_hist = 0;
+};
+struct NucState {
+    int need, row, acc;
+    float u, Z;
+};
+// Scratch of a nucleus sample over one row of V: the row's keys (e bits) and ids, their
+// descending order, the sort's temporary storage and the deferred decision.
+struct NucleusBuf {
+    uint32_t* keys;
+    int32_t* ids;
+    uint32_t* keys_s;
+    int32_t* ids_s;
+    void* tmp;
+    size_t tmp_bytes;
+    NucState* st;
+};
+size_t nucleus_bytes(int V);
+void nucleus_layout(void* base, int V, NucleusBuf& nb);
+// Full-vocabulary sampled acceptance.  With sd the temperature, q, uniforms' seed / counter,
+// the drafts and the options' scalars come from the step descriptor (hist arrays from o).
+hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* draft,
                                  float temperature, int q_mode, const float* q_point,
-                                 uint64_t seed, uint64_t counter, float* rowmax, float* bsum,
-                                 int32_t* out, StepResult* res, const StepDesc* sd,
-                                 const int* abort, hipStream_t st);
+                                 uint64_t seed, uint64_t counter, const SampleOpts& o,
+                                 const NucleusBuf* nb, float* rowmax, float* bsum, int32_t* out,
+                                 StepResult* res, const StepDesc* sd, const int* abort,
+                                 hipStream_t st);
 int sample_nblocks(int V);
 
 // large-LDS kernels need their limit raised once per process

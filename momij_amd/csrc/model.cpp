@@ -19,7 +19,14 @@
 #include "mj_abi_internal.h"
 #include "mj_internal.h"
 
-enum PassKind { PASS_PREFILL = 0, PASS_CHAIN = 1, PASS_GREEDY = 2, PASS_SAMPLED = 3 };
+// PASS_SAMPLED_NUC: a sampled pass whose bonus (or zero-mass residual) takes a nucleus
+enum PassKind {
+    PASS_PREFILL = 0,
+    PASS_CHAIN = 1,
+    PASS_GREEDY = 2,
+    PASS_SAMPLED = 3,
+    PASS_SAMPLED_NUC = 4
+};
 
 struct mj_model {
     mj_ctx* ctx = nullptr;
@@ -41,6 +48,8 @@ struct mj_model {
     float *opart, *pval, *rowmax, *logits, *bsum, *maxv;
     int* pidx;
     int32_t* argmax;
+    int32_t *hist_tok, *hist_cnt;  // sampled passes: the seen tokens (ascending) and counts
+    NucleusBuf nuc{};
     int32_t *inds_all;
     float* scores_all;
     MoeScratch ms{};
@@ -244,7 +253,8 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                            hipMemcpyDeviceToDevice, st), "capture");
             if (s != MJ_OK) return s;
         }
-        float* logits = (kind == PASS_SAMPLED || m->cap.logits) ? m->logits : nullptr;
+        float* logits =
+            (kind == PASS_SAMPLED || kind == PASS_SAMPLED_NUC || m->cap.logits) ? m->logits : nullptr;
         if (m->profiling) m->prof.begin(PROF_HEAD, st);
         if (c.head_bits == 4)
             s = mj_hip(ctx,
@@ -264,9 +274,14 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                            hipMemcpyDeviceToDevice, st), "capture");
             if (s != MJ_OK) return s;
         }
-        if (kind == PASS_SAMPLED) {
+        if (kind == PASS_SAMPLED || kind == PASS_SAMPLED_NUC) {
+            SampleOpts o{};
+            o.hist_tok = m->hist_tok;
+            o.hist_cnt = m->hist_cnt;
             s = mj_hip(ctx, launch_accept_sampled(m->logits, M, c.vocab, nullptr, 1.0f, 0, nullptr,
-                                                  0, 0, m->rowmax, m->bsum, nullptr, m->res_dev,
+                                                  0, 0, o,
+                                                  kind == PASS_SAMPLED_NUC ? &m->nuc : nullptr,
+                                                  m->rowmax, m->bsum, nullptr, m->res_dev,
                                                   m->sd_dev, ab, st), "sampled accept");
         } else {
             const int32_t* toks = (const int32_t*)((char*)m->sd_dev + offsetof(StepDesc, tokens));
@@ -275,7 +290,7 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                                  st), "greedy accept");
         }
         if (s != MJ_OK) return s;
-        if (kind == PASS_GREEDY || kind == PASS_SAMPLED) {
+        if (kind == PASS_GREEDY || kind == PASS_SAMPLED || kind == PASS_SAMPLED_NUC) {
             s = mj_hip(ctx, launch_kv_commit(m->kv, m->layer_stride, c.n_layers, c.kv_capacity,
                                              c.n_kv_heads, m->sd_dev, m->res_dev, ab, st),
                        "kv commit");
@@ -462,6 +477,9 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         m->rowmax = (float*)a.take((size_t)R * 4);
         m->logits = (float*)a.take((size_t)R * c.vocab * 4);
         m->bsum = (float*)a.take((size_t)R * sample_nblocks(c.vocab) * 4);
+        m->hist_tok = (int32_t*)a.take((size_t)MJ_MAX_HIST * 4);
+        m->hist_cnt = (int32_t*)a.take((size_t)MJ_MAX_HIST * 4);
+        nucleus_layout(a.take(nucleus_bytes(c.vocab)), c.vocab, m->nuc);
         m->inds_all = (int32_t*)a.take((size_t)c.n_layers * R * c.top_k * 4);
         m->scores_all = (float*)a.take((size_t)c.n_layers * R * c.top_k * 4);
         m->sd_dev = (StepDesc*)a.take(sizeof(StepDesc));
@@ -662,34 +680,100 @@ mj_status mj_verify_greedy(mj_model* m, int32_t y, const int32_t* draft, int n_d
     return MJ_OK;
 }
 
-mj_status mj_verify_sampled(mj_model* m, int32_t y, const int32_t* draft, int n_draft,
-                            float temperature, int q_mode, const float* q_point, uint64_t seed,
-                            uint64_t counter, int32_t* out_accepted, int32_t* out_token) {
-    if (!m || (n_draft > 0 && !draft) || n_draft < 0) return MJ_INVALID_ARG;
-    if (!(temperature > 1e-5f))
+// The LogitsProcessor options of a sampled call, checked, with the history ranked by token
+// (the penalty kernel looks drafts up in it); NULL = temperature only.
+static mj_status sampling_prep(mj_ctx* ctx, const mj_sampling* sp, SampleOpts& o,
+                               std::vector<int32_t>& tok, std::vector<int32_t>& cnt) {
+    o = SampleOpts{};
+    tok.clear();
+    cnt.clear();
+    if (!sp) return MJ_OK;
+    if (!std::isfinite(sp->top_p) || !std::isfinite(sp->repetition_penalty) ||
+        !std::isfinite(sp->presence_penalty) || !std::isfinite(sp->frequency_penalty) ||
+        sp->n_hist < 0 || sp->n_hist > MJ_MAX_HIST ||
+        (sp->n_hist > 0 && (!sp->hist_tokens || !sp->hist_counts)))
+        return mj_fail(ctx, MJ_INVALID_ARG, "sampling options: bad argument");
+    o.top_p = sp->top_p;
+    o.rep = sp->repetition_penalty;
+    o.pres = sp->presence_penalty;
+    o.freq = sp->frequency_penalty;
+    std::vector<std::pair<int32_t, int32_t>> h(sp->n_hist);
+    for (int i = 0; i < sp->n_hist; ++i) {
+        if (sp->hist_counts[i] < 0)
+            return mj_fail(ctx, MJ_INVALID_ARG, "sampling options: negative count");
+        h[i] = {sp->hist_tokens[i], sp->hist_counts[i]};
+    }
+    std::sort(h.begin(), h.end());
+    for (size_t i = 1; i < h.size(); ++i)
+        if (h[i].first == h[i - 1].first)
+            return mj_fail(ctx, MJ_INVALID_ARG, "sampling options: token %d listed twice",
+                           h[i].first);
+    for (auto& e : h) {
+        tok.push_back(e.first);
+        cnt.push_back(e.second);
+    }
+    o.n_hist = (int)h.size();
+    return MJ_OK;
+}
+
+mj_status mj_verify_sampled_ex(mj_model* m, int32_t y, const int32_t* draft, int n_draft,
+                               const mj_sampling* sp, int q_mode, const float* q_point,
+                               uint64_t seed, uint64_t counter, int32_t* out_accepted,
+                               int32_t* out_token) {
+    if (!m || !sp || (n_draft > 0 && !draft) || n_draft < 0) return MJ_INVALID_ARG;
+    if (!(sp->temperature > 1e-5f))
         return mj_fail(m->ctx, MJ_INVALID_ARG, "sampled verify needs temperature > 1e-5");
     if (q_mode != MJ_Q_POINT && q_mode != MJ_Q_UNIFORM)
         return mj_fail(m->ctx, MJ_INVALID_ARG, "unknown q_mode %d", q_mode);
     const int M = n_draft + 1;
     if (M > MJ_MAX_ROWS) return mj_fail(m->ctx, MJ_INVALID_ARG, "draft too long");
+    SampleOpts o;
+    std::vector<int32_t> ht, hc;
+    mj_status s = sampling_prep(m->ctx, sp, o, ht, hc);
+    if (s != MJ_OK) return s;
     StepDesc* sd = m->sd_host;
     sd->seed = seed;
     sd->counter = counter;
-    sd->temperature = temperature;
+    sd->temperature = sp->temperature;
     sd->q_mode = q_mode;
     sd->q_uniform = 1.0f / (float)m->cfg.vocab;
     sd->has_qpoint = q_point ? 1 : 0;
     for (int i = 0; i < n_draft; ++i) sd->q_point[i] = q_point ? q_point[i] : 1.0f;
+    sd->top_p = o.top_p;
+    sd->rep = o.rep;
+    sd->pres = o.pres;
+    sd->freq = o.freq;
+    sd->n_hist = o.n_hist;
+    if (o.n_hist > 0) {
+        hipSetDevice(m->ctx->device);
+        s = mj_hip(m->ctx, hipMemcpyAsync(m->hist_tok, ht.data(), ht.size() * 4,
+                                          hipMemcpyHostToDevice, m->ctx->stream), "history");
+        if (s == MJ_OK)
+            s = mj_hip(m->ctx, hipMemcpyAsync(m->hist_cnt, hc.data(), hc.size() * 4,
+                                              hipMemcpyHostToDevice, m->ctx->stream), "history");
+        if (s != MJ_OK) return s;
+    }
     int32_t rows[MJ_MAX_ROWS];
     rows[0] = y;
     for (int i = 0; i < n_draft; ++i) rows[i + 1] = draft[i];
-    mj_status s = feed_rows(m, rows, nullptr, M, PASS_SAMPLED);
+    s = feed_rows(m, rows, nullptr, M, o.top_p < 1.0f - 1e-6f ? PASS_SAMPLED_NUC : PASS_SAMPLED);
     if (s != MJ_OK) return s;
     const StepResult* r = m->res_host;
     m->offset += r->accepted + 1;
     if (out_accepted) *out_accepted = r->accepted;
     if (out_token) *out_token = r->token;
     return MJ_OK;
+}
+
+mj_status mj_verify_sampled(mj_model* m, int32_t y, const int32_t* draft, int n_draft,
+                            float temperature, int q_mode, const float* q_point, uint64_t seed,
+                            uint64_t counter, int32_t* out_accepted, int32_t* out_token) {
+    mj_sampling sp{};
+    sp.temperature = temperature;
+    sp.top_p = 1.0f;
+    sp.repetition_penalty = 1.0f;
+    return mj_verify_sampled_ex(m, y, draft, n_draft, &sp, q_mode, q_point, seed, counter,
+                                out_accepted, out_token);
 }
 
 // ------------------------------------------------------------------ op-level entries
@@ -899,26 +983,78 @@ mj_status mj_accept_greedy(mj_ctx* ctx, const int32_t* tokens, const int32_t* pa
                                             ctx->abort_dev, ctx->stream), "accept greedy");
 }
 
+mj_status mj_accept_sampled_ex(mj_ctx* ctx, const float* logits, int rows, int V,
+                               const int32_t* draft, const mj_sampling* sp, int q_mode,
+                               const float* q_point, uint64_t seed, uint64_t counter,
+                               int32_t* out) {
+    if (!ctx) return MJ_INVALID_ARG;
+    if (!logits || !out || !sp || rows < 1 || rows > MJ_MAX_ROWS || V < 1 || V > 196608 ||
+        (rows > 1 && !draft) || !(sp->temperature > 1e-5f) ||
+        (q_mode != MJ_Q_POINT && q_mode != MJ_Q_UNIFORM))
+        return mj_fail(ctx, MJ_INVALID_ARG, "accept_sampled: bad argument");
+    SampleOpts o;
+    std::vector<int32_t> ht, hc;
+    mj_status s = sampling_prep(ctx, sp, o, ht, hc);
+    if (s != MJ_OK) return s;
+    const bool pen = (std::fabs(o.rep - 1.0f) > 1e-6f && o.rep > 0.0f) || o.pres != 0.0f ||
+                     o.freq != 0.0f;
+    const bool nucleus = o.top_p < 1.0f - 1e-6f;
+    hipSetDevice(ctx->device);
+    auto layout = [&](Arena& a, float** rowmax, float** bsum, float** lcopy, int32_t** dt,
+                      int32_t** dc, void** nbase) {
+        *rowmax = (float*)a.take((size_t)rows * 4);
+        *bsum = (float*)a.take((size_t)rows * sample_nblocks(V) * 4);
+        *lcopy = pen ? (float*)a.take((size_t)rows * V * 4) : nullptr;
+        *dt = (int32_t*)a.take((size_t)ht.size() * 4 + 4);
+        *dc = (int32_t*)a.take((size_t)hc.size() * 4 + 4);
+        *nbase = nucleus ? a.take(nucleus_bytes(V)) : nullptr;
+    };
+    float *rowmax, *bsum, *lcopy;
+    int32_t *dt, *dc;
+    void* nbase;
+    Arena count;
+    layout(count, &rowmax, &bsum, &lcopy, &dt, &dc, &nbase);
+    s = mj_scratch_reserve(ctx, count.off);
+    if (s != MJ_OK) return s;
+    Arena real{ctx->scratch, 0};
+    layout(real, &rowmax, &bsum, &lcopy, &dt, &dc, &nbase);
+    hipStream_t st = ctx->stream;
+    // the penalties rewrite the logits: on a copy, the caller's buffer is read-only here
+    float* lg = const_cast<float*>(logits);
+    if (pen) {
+        s = mj_hip(ctx, hipMemcpyAsync(lcopy, logits, (size_t)rows * V * 4,
+                                       hipMemcpyDeviceToDevice, st), "logits copy");
+        if (s != MJ_OK) return s;
+        lg = lcopy;
+    }
+    if (!ht.empty()) {
+        s = mj_hip(ctx, hipMemcpyAsync(dt, ht.data(), ht.size() * 4, hipMemcpyHostToDevice, st),
+                   "history");
+        if (s == MJ_OK)
+            s = mj_hip(ctx, hipMemcpyAsync(dc, hc.data(), hc.size() * 4, hipMemcpyHostToDevice,
+                                           st), "history");
+        if (s == MJ_OK) s = mj_hip(ctx, hipStreamSynchronize(st), "history upload");
+        if (s != MJ_OK) return s;
+    }
+    o.hist_tok = dt;
+    o.hist_cnt = dc;
+    NucleusBuf nb{};
+    if (nucleus) nucleus_layout(nbase, V, nb);
+    return mj_hip(ctx, launch_accept_sampled(lg, rows, V, draft, sp->temperature, q_mode, q_point,
+                                             seed, counter, o, nucleus ? &nb : nullptr, rowmax,
+                                             bsum, out, nullptr, nullptr, ctx->abort_dev, st),
+                  "accept sampled");
+}
+
 mj_status mj_accept_sampled(mj_ctx* ctx, const float* logits, int rows, int V,
                             const int32_t* draft, float temperature, int q_mode,
                             const float* q_point, uint64_t seed, uint64_t counter, int32_t* out) {
-    if (!ctx) return MJ_INVALID_ARG;
-    if (!logits || !out || rows < 1 || rows > MJ_MAX_ROWS || V < 1 || V > 196608 ||
-        (rows > 1 && !draft) || !(temperature > 1e-5f) ||
-        (q_mode != MJ_Q_POINT && q_mode != MJ_Q_UNIFORM))
-        return mj_fail(ctx, MJ_INVALID_ARG, "accept_sampled: bad argument");
-    hipSetDevice(ctx->device);
-    Arena count;
-    count.take((size_t)rows * 4);
-    count.take((size_t)rows * sample_nblocks(V) * 4);
-    mj_status s = mj_scratch_reserve(ctx, count.off);
-    if (s != MJ_OK) return s;
-    Arena real{ctx->scratch, 0};
-    float* rowmax = (float*)real.take((size_t)rows * 4);
-    float* bsum = (float*)real.take((size_t)rows * sample_nblocks(V) * 4);
-    return mj_hip(ctx, launch_accept_sampled(logits, rows, V, draft, temperature, q_mode, q_point,
-                                             seed, counter, rowmax, bsum, out, nullptr, nullptr,
-                                             ctx->abort_dev, ctx->stream), "accept sampled");
+    mj_sampling sp{};
+    sp.temperature = temperature;
+    sp.top_p = 1.0f;
+    sp.repetition_penalty = 1.0f;
+    return mj_accept_sampled_ex(ctx, logits, rows, V, draft, &sp, q_mode, q_point, seed, counter,
+                                out);
 }
 
 }  // extern "C"

@@ -6,10 +6,18 @@
 //   on reject sample the residual (point q: p with p_d -> max(0, p_d - q); uniform q:
 //   max(p - q, 0)) by a cumulative walk to u1 * sum; after a full accept sample the bonus from
 //   the last row by a walk to u0 * sum of exps.
+// LogitsProcessor options: penalties (prepare, LogitsProcessor.swift:57-104) on every row, the
+// seen set and counts growing with the drafts accepted before it (walkDraft 86-87);
+// samplePrepared's nucleus (137-154) for the bonus and for a residual of zero mass: tokens
+// ranked by e descending, the lower id first on ties, kept up to the first ranked prefix whose
+// blocked prefix sum reaches top_p * Z, sampled in id order (the ranking is a radix sort of
+// the row's e bits).
 // Every float operation below happens in a fixed order (chunks of 16 summed sequentially,
 // blocks of 64 chunks summed sequentially, block totals summed sequentially; exp evaluated by
 // canon_expf; IEEE divisions) so the CPU oracle reproduces each decision bit for bit.
 #pragma clang fp contract(off)
+#include <hipcub/hipcub.hpp>
+
 #include "mj_device.h"
 #include "mj_internal.h"
 
@@ -18,7 +26,7 @@
 #define MAX_CHUNKS 12288  // V <= 196608
 
 struct SampleArgs {
-    const float* logits;   // [rows][V]
+    float* logits;         // [rows][V] (penalised in place)
     int rows, V;
     const int32_t* draft;  // [rows-1]
     float invT;
@@ -31,8 +39,10 @@ struct SampleArgs {
     int nblocks;
     int32_t* out;          // [2] or nullptr
     StepResult* res;       // or nullptr
-    const StepDesc* sd;    // when set: temperature, q, seed, counter and draft come from it
+    const StepDesc* sd;    // when set: temperature, q, seed, counter, draft, options from it
     const int* abort;
+    SampleOpts o;
+    NucleusBuf nb;         // nb.st == nullptr: no nucleus
 };
 
 // Effective per-call parameters (from the step descriptor when one is given).
@@ -45,8 +55,60 @@ __device__ __forceinline__ SampleArgs resolve(SampleArgs a) {
         a.seed = a.sd->seed;
         a.counter = a.sd->counter;
         a.draft = a.sd->tokens + 1;
+        a.o.top_p = a.sd->top_p;
+        a.o.rep = a.sd->rep;
+        a.o.pres = a.sd->pres;
+        a.o.freq = a.sd->freq;
+        a.o.n_hist = a.sd->n_hist;
     }
     return a;
+}
+
+__device__ __forceinline__ bool nucleus_on(const SampleArgs& a) {
+    return a.nb.st != nullptr && a.o.top_p < 1.0f - 1e-6f;
+}
+
+// LogitsProcessor.prepare for one token: repetition, presence, frequency (in that order)
+__device__ __forceinline__ float penalize1(float x, int count, float rep, float pres, float freq) {
+    if (fabsf(rep - 1.0f) > 1e-6f && rep > 0.0f) x = x > 0.0f ? __fdiv_rn(x, rep) : x * rep;
+    if (pres != 0.0f) x = x - pres;
+    if (freq != 0.0f && count > 0) x = x - freq * (float)count;
+    return x;
+}
+
+// Row i's penalties: every history token, then every draft d < i that is neither earlier among
+// the drafts nor in the history, each once with its total count (history count + occurrences
+// among drafts 0 .. i-1).  One block per row; each token is written by one thread.
+__global__ __launch_bounds__(256) void k_penalize(SampleArgs a) {
+    if (aborted(a.abort)) return;
+    a = resolve(a);
+    const bool rep_on = fabsf(a.o.rep - 1.0f) > 1e-6f && a.o.rep > 0.0f;
+    if (!rep_on && a.o.pres == 0.0f && a.o.freq == 0.0f) return;
+    const int i = blockIdx.x, t = threadIdx.x;
+    float* l = a.logits + (size_t)i * a.V;
+    for (int j = t; j < a.o.n_hist; j += 256) {
+        const int tok = a.o.hist_tok[j];
+        if (tok < 0 || tok >= a.V) continue;
+        int c = a.o.hist_cnt[j];
+        for (int d = 0; d < i; ++d) c += a.draft[d] == tok;
+        l[tok] = penalize1(l[tok], c, a.o.rep, a.o.pres, a.o.freq);
+    }
+    for (int d = t; d < i; d += 256) {
+        const int tok = a.draft[d];
+        if (tok < 0 || tok >= a.V) continue;
+        bool first = true;
+        for (int e = 0; e < d; ++e) first = first && a.draft[e] != tok;
+        int lo = 0, hi = a.o.n_hist;  // binary search of the ascending history
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (a.o.hist_tok[mid] < tok) lo = mid + 1; else hi = mid;
+        }
+        const bool in_hist = lo < a.o.n_hist && a.o.hist_tok[lo] == tok;
+        if (!first || in_hist) continue;
+        int c = 0;
+        for (int e = 0; e < i; ++e) c += a.draft[e] == tok;
+        l[tok] = penalize1(l[tok], c, a.o.rep, a.o.pres, a.o.freq);
+    }
 }
 
 __device__ __forceinline__ void row_uniforms(const SampleArgs& a, int row, float& u0, float& u1) {
@@ -112,7 +174,22 @@ __global__ __launch_bounds__(64) void k_sample_sums(SampleArgs a) {
     }
 }
 
-// Single block: totals, sequential accept decisions, then the residual or bonus walk.
+__device__ __forceinline__ void write_result(const SampleArgs& a, int acc, int tok) {
+    if (a.out) {
+        a.out[0] = acc;
+        a.out[1] = tok;
+    }
+    if (a.res) {
+        a.res->accepted = acc;
+        a.res->token = tok;
+        for (int i = 0; i <= acc; ++i) a.res->path[i] = i;
+        for (int i = 0; i < acc; ++i) a.res->emit[i] = a.draft[i];
+        a.res->emit[acc] = tok;
+    }
+}
+
+// Single block: totals, sequential accept decisions, then the residual or bonus walk (a
+// nucleus sample is left to k_nucleus_pick: the row, its uniform and Z go to the NucState).
 __global__ __launch_bounds__(1024) void k_sample_decide(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
@@ -190,6 +267,16 @@ __global__ __launch_bounds__(1024) void k_sample_decide(SampleArgs a) {
         __syncthreads();
         tgt = s_t;
     }
+    // samplePrepared with a nucleus: the bonus, or a residual without mass
+    if (nucleus_on(a) && (fr == D || !walk_resid)) {
+        if (t == 0) {
+            float u0, u1;
+            row_uniforms(a, row, u0, u1);
+            *a.nb.st = NucState{1, row, fr, fr == D ? u0 : u1, Z[row]};
+        }
+        return;  // block-uniform
+    }
+    if (t == 0 && a.nb.st) a.nb.st->need = 0;
     // block level
     if (t == 0) {
         float P = 0.0f;
@@ -247,28 +334,152 @@ __global__ __launch_bounds__(1024) void k_sample_decide(SampleArgs a) {
         }
         __syncthreads();
     }
-    if (t == 0) {
-        const int acc = fr;
-        const int tok = s_tok;
-        if (a.out) {
-            a.out[0] = acc;
-            a.out[1] = tok;
-        }
-        if (a.res) {
-            a.res->accepted = acc;
-            a.res->token = tok;
-            for (int i = 0; i <= acc; ++i) a.res->path[i] = i;
-            for (int i = 0; i < acc; ++i) a.res->emit[i] = a.draft[i];
-            a.res->emit[acc] = tok;
-        }
-    }
+    if (t == 0) write_result(a, fr, s_tok);
 }
 
-hipError_t launch_accept_sampled(const float* logits, int rows, int V, const int32_t* draft,
+// ---- nucleus (samplePrepared, LogitsProcessor.swift:137-164) --------------------------------
+// Canonical sum and walk of n values f(i) by a 1024-thread block, in or_canon_sum /
+// or_canon_walk's order: chunks of CH in order, blocks of BLK chunks in order, block totals in
+// order; the walk finds the first block, then chunk, then element whose running total reaches
+// tgt (the last index of the level otherwise).  cs / bs hold the chunk and block sums of f
+// (blk_sum fills them for blk_walk).
+template <class F>
+__device__ float blk_sum(F f, int n, float* cs, float* bs, float* s_out) {
+    const int t = threadIdx.x;
+    const int nch = (n + CH - 1) / CH, nbk = (nch + BLK - 1) / BLK;
+    for (int c = t; c < nch; c += 1024) {
+        float sum = 0.0f;
+        const int e = min(c * CH + CH, n);
+        for (int v = c * CH; v < e; ++v) sum = sum + f(v);
+        cs[c] = sum;
+    }
+    __syncthreads();
+    for (int b = t; b < nbk; b += 1024) {
+        float sum = 0.0f;
+        for (int c = b * BLK; c < min(b * BLK + BLK, nch); ++c) sum = sum + cs[c];
+        bs[b] = sum;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float S = 0.0f;
+        for (int b = 0; b < nbk; ++b) S = S + bs[b];
+        *s_out = S;
+    }
+    __syncthreads();
+    return *s_out;
+}
+
+template <class F>
+__device__ int blk_walk(F f, int n, float tgt, const float* cs, const float* bs, int* s_out) {
+    if (threadIdx.x == 0) {
+        const int nch = (n + CH - 1) / CH, nbk = (nch + BLK - 1) / BLK;
+        int res = n - 1;
+        float P = 0.0f;
+        for (int b = 0; b < nbk; ++b) {
+            const float Pn = P + bs[b];
+            if (tgt <= Pn) {
+                const int c0 = b * BLK, c1 = min(c0 + BLK, nch);
+                res = min(c1 * CH, n) - 1;
+                float Q = P;
+                for (int c = c0; c < c1; ++c) {
+                    const float Qn = Q + cs[c];
+                    if (tgt <= Qn) {
+                        const int e = min(c * CH + CH, n);
+                        res = e - 1;
+                        float R = Q;
+                        for (int v = c * CH; v < e; ++v) {
+                            R = R + f(v);
+                            if (tgt <= R) {
+                                res = v;
+                                break;
+                            }
+                        }
+                        break;
+                    }
+                    Q = Qn;
+                }
+                break;
+            }
+            P = Pn;
+        }
+        *s_out = res;
+    }
+    __syncthreads();
+    return *s_out;
+}
+
+// e bits and ids of the nucleus row (e >= 0: its bits order as the values do)
+__global__ __launch_bounds__(256) void k_nucleus_keys(SampleArgs a) {
+    if (aborted(a.abort)) return;
+    a = resolve(a);
+    const NucState st = *a.nb.st;
+    if (!st.need) return;
+    const int v = blockIdx.x * 256 + threadIdx.x;
+    if (v >= a.V) return;
+    a.nb.keys[v] = __float_as_uint(e_at(a, st.row, v, a.rowmax[st.row] * a.invT));
+    a.nb.ids[v] = v;
+}
+
+// After the ranking (ids_s / keys_s: e descending, lower id first among equal e): the kept
+// prefix, its mass in id order, and the sample.
+__global__ __launch_bounds__(1024) void k_nucleus_pick(SampleArgs a) {
+    if (aborted(a.abort)) return;
+    a = resolve(a);
+    const NucState st = *a.nb.st;
+    if (!st.need) return;
+    __shared__ float cs[MAX_CHUNKS];
+    __shared__ float bs[MAX_CHUNKS / BLK];
+    __shared__ float s_f;
+    __shared__ int s_i;
+    const float mxs = a.rowmax[st.row] * a.invT;
+    const float tp = a.o.top_p < 0.0f ? 0.0f : (a.o.top_p > 1.0f ? 1.0f : a.o.top_p);
+    const uint32_t* ks = a.nb.keys_s;
+    const auto ranked = [&](int i) { return __uint_as_float(ks[i]); };
+    blk_sum(ranked, a.V, cs, bs, &s_f);
+    const int k = blk_walk(ranked, a.V, tp * st.Z, cs, bs, &s_i);
+    const float es = ranked(k);
+    const int is = a.nb.ids_s[k];
+    const auto kept = [&](int v) {
+        const float e = e_at(a, st.row, v, mxs);
+        return (e > es || (e == es && v <= is)) ? e : 0.0f;
+    };
+    const float S = blk_sum(kept, a.V, cs, bs, &s_f);
+    const int tok = S > 0.0f ? blk_walk(kept, a.V, st.u * S, cs, bs, &s_i) : a.nb.ids_s[0];
+    if (threadIdx.x == 0) write_result(a, st.acc, tok);
+}
+
+static size_t sort_tmp_bytes(int V) {
+    size_t b = 0;
+    hipError_t e = hipcub::DeviceRadixSort::SortPairsDescending(
+        nullptr, b, (const uint32_t*)nullptr, (uint32_t*)nullptr, (const int32_t*)nullptr,
+        (int32_t*)nullptr, V, 0, 32, (hipStream_t)0);
+    return e == hipSuccess ? b : 0;
+}
+
+static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t nucleus_bytes(int V) {
+    return 4 * up256((size_t)V * 4) + up256(sort_tmp_bytes(V)) + up256(sizeof(NucState));
+}
+
+void nucleus_layout(void* base, int V, NucleusBuf& nb) {
+    char* p = (char*)base;
+    const size_t row = up256((size_t)V * 4);
+    nb.keys = (uint32_t*)p;
+    nb.ids = (int32_t*)(p + row);
+    nb.keys_s = (uint32_t*)(p + 2 * row);
+    nb.ids_s = (int32_t*)(p + 3 * row);
+    nb.tmp = p + 4 * row;
+    nb.tmp_bytes = sort_tmp_bytes(V);
+    nb.st = (NucState*)(p + 4 * row + up256(nb.tmp_bytes));
+}
+
+hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* draft,
                                  float temperature, int q_mode, const float* q_point,
-                                 uint64_t seed, uint64_t counter, float* rowmax, float* bsum,
-                                 int32_t* out, StepResult* res, const StepDesc* sd,
-                                 const int* abort, hipStream_t st) {
+                                 uint64_t seed, uint64_t counter, const SampleOpts& o,
+                                 const NucleusBuf* nb, float* rowmax, float* bsum, int32_t* out,
+                                 StepResult* res, const StepDesc* sd, const int* abort,
+                                 hipStream_t st) {
     SampleArgs a{};
     a.sd = sd;
     a.logits = logits;
@@ -287,13 +498,29 @@ hipError_t launch_accept_sampled(const float* logits, int rows, int V, const int
     a.out = out;
     a.res = res;
     a.abort = abort;
-    hipLaunchKernelGGL(k_rowmax, dim3(rows), dim3(1024), 0, st, a);
+    a.o = o;
+    if (nb) a.nb = *nb;
+    if (V > MAX_CHUNKS * CH || rows > MJ_ROWS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_penalize, dim3(rows), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_rowmax, dim3(rows), dim3(1024), 0, st, a);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_sample_sums, dim3(rows * a.nblocks), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_sample_decide, dim3(1), dim3(1024), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess || !nb) return e;
+    hipLaunchKernelGGL(k_nucleus_keys, dim3((V + 255) / 256), dim3(256), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    size_t tb = nb->tmp_bytes;
+    e = hipcub::DeviceRadixSort::SortPairsDescending(nb->tmp, tb, nb->keys, nb->keys_s, nb->ids,
+                                                      nb->ids_s, V, 0, 32, st);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_nucleus_pick, dim3(1), dim3(1024), 0, st, a);
     return hipGetLastError();
 }
 

@@ -213,6 +213,20 @@ class VerifyEngine:
                                                   seed, counter, C.byref(acc), C.byref(tok)))
         return acc.value, tok.value
 
+    def verify_sampled_ex(self, y: int, draft, q_mode: int, seed: int, counter: int,
+                          temperature: float, top_p=1.0, rep=1.0, pres=0.0, freq=0.0,
+                          hist=None, q_point=None) -> tuple[int, int]:
+        """mj_verify_sampled_ex: LogitsProcessor options; hist {token: count}."""
+        n = len(draft)
+        d = (C.c_int32 * max(n, 1))(*[int(t) for t in draft])
+        qp = None if q_point is None else (C.c_float * max(n, 1))(*[float(q) for q in q_point])
+        sp, keep = _lib.sampling(temperature, top_p, rep, pres, freq, hist)
+        acc, tok = C.c_int32(), C.c_int32()
+        self.ctx.check(self.lib.mj_verify_sampled_ex(self.h, int(y), d, n, C.byref(sp), q_mode,
+                                                     qp, seed, counter, C.byref(acc),
+                                                     C.byref(tok)))
+        return acc.value, tok.value
+
 
 def random_model(cfg: MapleLikeConfig, seed: int = 0, device: str = "cuda",
                  embed_std: float = 1.0):

@@ -128,5 +128,14 @@ class Context:
                                               temperature, q_mode, ptr(q_point), seed, counter,
                                               ptr(out)))
 
+    def accept_sampled_ex(self, logits, rows, V, draft, q_mode, seed, counter, out,
+                          temperature, top_p=1.0, rep=1.0, pres=0.0, freq=0.0, hist=None,
+                          q_point=None):
+        """mj_accept_sampled_ex: LogitsProcessor options; hist {token: count}."""
+        sp, keep = _lib.sampling(temperature, top_p, rep, pres, freq, hist)
+        self.check(self.lib.mj_accept_sampled_ex(self.h, ptr(logits), rows, V, ptr(draft),
+                                                 C.byref(sp), q_mode, ptr(q_point), seed,
+                                                 counter, ptr(out)))
+
     def selftest_mfma(self, A, B, D):
         self.check(self.lib.mj_selftest_mfma(self.h, ptr(A), ptr(B), ptr(D)))

@@ -817,6 +817,138 @@ int or_accept_sampled(const float* logits, int rows, int V, const int32_t* draft
     return result;
 }
 
+/* LogitsProcessor.prepare (LogitsProcessor.swift:57-104, order 91-104) over a full-vocabulary
+ * row, in place.  The seen set is the history tokens (unique, any order) plus the first n_extra
+ * draft tokens; a token's count is its history count plus its occurrences among those drafts
+ * (walkDraft adds each accepted draft to both, SpeculativeSampling.swift:86-87).  Each seen
+ * token is penalised once: repetition (x > 0 ? x / r : x * r; off when |r - 1| <= 1e-6 or
+ * r <= 0, 78-89), presence (x - pres; off at 0, 57-65), frequency (x - freq * count for
+ * count > 0; off at 0, 67-76). */
+static float penalize1(float x, int count, float rep, float pres, float freq) {
+    if (fabsf(rep - 1.0f) > 1e-6f && rep > 0.0f) x = x > 0.0f ? x / rep : x * rep;
+    if (pres != 0.0f) x = x - pres;
+    if (freq != 0.0f && count > 0) x = x - freq * (float)count;
+    return x;
+}
+
+void or_penalize_row(float* l, int V, const int32_t* hist_tok, const int32_t* hist_cnt,
+                     int n_hist, const int32_t* extra, int n_extra, float rep, float pres,
+                     float freq) {
+    for (int j = 0; j < n_hist; ++j) {
+        const int t = hist_tok[j];
+        if (t < 0 || t >= V) continue;
+        int c = hist_cnt[j];
+        for (int d = 0; d < n_extra; ++d) c += extra[d] == t;
+        l[t] = penalize1(l[t], c, rep, pres, freq);
+    }
+    for (int d = 0; d < n_extra; ++d) {
+        const int t = extra[d];
+        if (t < 0 || t >= V) continue;
+        int first = 1, in_hist = 0, c = 0;
+        for (int e = 0; e < d; ++e) first &= extra[e] != t;
+        for (int j = 0; j < n_hist; ++j) in_hist |= hist_tok[j] == t;
+        if (!first || in_hist) continue;
+        for (int e = 0; e < n_extra; ++e) c += extra[e] == t;
+        l[t] = penalize1(l[t], c, rep, pres, freq);
+    }
+}
+
+/* LogitsProcessor.samplePrepared's nucleus + multinomial (LogitsProcessor.swift:137-164) in
+ * the canonical order.  Tokens are ranked by e descending, the lower id first among equal e
+ * (the reference's unstable sort leaves ties unordered); the kept set is the shortest ranked
+ * prefix whose prefix sum, accumulated in or_canon_walk's blocked order over the ranked
+ * values, reaches clamp(top_p, 0, 1) * Z; the sample is or_canon_walk over the kept e in id
+ * order at u * (their or_canon_sum), or the top-ranked token when that sum is 0. */
+typedef struct {
+    float e;
+    int32_t id;
+} rank_item;
+
+static int rank_cmp(const void* a, const void* b) {
+    const rank_item* x = (const rank_item*)a;
+    const rank_item* y = (const rank_item*)b;
+    if (x->e != y->e) return x->e > y->e ? -1 : 1;
+    return x->id < y->id ? -1 : (x->id > y->id ? 1 : 0);
+}
+
+int or_nucleus_sample(const float* e, int V, float Z, float top_p, float u) {
+    rank_item* it = (rank_item*)malloc(sizeof(rank_item) * (size_t)V);
+    float* se = (float*)malloc(sizeof(float) * (size_t)V);
+    float* kept = (float*)malloc(sizeof(float) * (size_t)V);
+    for (int v = 0; v < V; ++v) {
+        it[v].e = e[v];
+        it[v].id = v;
+    }
+    qsort(it, (size_t)V, sizeof(rank_item), rank_cmp);
+    for (int i = 0; i < V; ++i) se[i] = it[i].e;
+    const float tp = top_p < 0.0f ? 0.0f : (top_p > 1.0f ? 1.0f : top_p);
+    const int k = or_canon_walk(se, V, tp * Z);
+    const float es = it[k].e;
+    const int is = it[k].id;
+    for (int v = 0; v < V; ++v) kept[v] = (e[v] > es || (e[v] == es && v <= is)) ? e[v] : 0.0f;
+    const float S = or_canon_sum(kept, V);
+    const int tok = S > 0.0f ? or_canon_walk(kept, V, u * S) : it[0].id;
+    free(it);
+    free(se);
+    free(kept);
+    return tok;
+}
+
+/* or_accept_sampled with LogitsProcessor's penalties and nucleus (walkDraft,
+ * SpeculativeSampling.swift:65-99): row i's logits are penalised with the history plus drafts
+ * 0 .. i-1; tryAccept's probabilities take no nucleus (27-59); the bonus row and a residual of
+ * zero mass are sampled through samplePrepared, i.e. with the nucleus when top_p < 1 - 1e-6.
+ * The residual's fallback and the bonus use u1 and u0 of their row, as or_accept_sampled. */
+int or_accept_sampled_ex(const float* logits, int rows, int V, const int32_t* draft,
+                         float temperature, float top_p, float rep, float pres, float freq,
+                         const int32_t* hist_tok, const int32_t* hist_cnt, int n_hist,
+                         int q_mode, const float* q_point, const float* uniforms,
+                         int32_t* out_token) {
+    const float invT = 1.0f / fmaxf(temperature, 1e-5f);
+    const int nucleus = top_p < 1.0f - 1e-6f;
+    float* l = (float*)malloc(sizeof(float) * (size_t)V);
+    float* e = (float*)malloc(sizeof(float) * (size_t)V);
+    float* r = (float*)malloc(sizeof(float) * (size_t)V);
+    const int D = rows - 1;
+    int result = D;
+    for (int i = 0; i <= D; ++i) {
+        memcpy(l, logits + (size_t)i * V, sizeof(float) * (size_t)V);
+        or_penalize_row(l, V, hist_tok, hist_cnt, n_hist, draft, i, rep, pres, freq);
+        float Z;
+        row_probs(l, V, invT, e, &Z);
+        if (i == D) {
+            *out_token = nucleus ? or_nucleus_sample(e, V, Z, top_p, uniforms[2 * D])
+                                 : or_canon_walk(e, V, uniforms[2 * D] * Z);
+            break;
+        }
+        const int d = draft[i];
+        const float p = (d >= 0 && d < V) ? e[d] / Z : 0.0f;
+        float q = q_mode == 1 ? 1.0f / (float)V : (q_point ? q_point[i] : 1.0f);
+        q = fmaxf(0.0f, q);
+        if (q > 0.0f && p > 0.0f) {
+            const float ratio = p / q;
+            if (uniforms[2 * i] <= fminf(1.0f, ratio)) continue;
+        }
+        for (int v = 0; v < V; ++v) {
+            const float pv = e[v] / Z;
+            r[v] = q_mode == 1 ? fmaxf(pv - q, 0.0f) : pv;
+        }
+        if (q_mode != 1 && d >= 0 && d < V && q > 0.0f) r[d] = fmaxf(0.0f, r[d] - q);
+        const float S = or_canon_sum(r, V);
+        if (S > 0.0f)
+            *out_token = or_canon_walk(r, V, uniforms[2 * i + 1] * S);
+        else
+            *out_token = nucleus ? or_nucleus_sample(e, V, Z, top_p, uniforms[2 * i + 1])
+                                 : or_canon_walk(e, V, uniforms[2 * i + 1] * Z);
+        result = i;
+        break;
+    }
+    free(l);
+    free(e);
+    free(r);
+    return result;
+}
+
 /* Literal restatement over candidate lists (no canonical order), used for the KATs of
  * SpeculativeSamplingTests.swift.  LogitsProcessor.probabilities 168-189, samplePrepared
  * 116-165 (no nucleus), SpeculativeSampling.tryAccept 27-59. */

@@ -146,6 +146,20 @@ int or_accept_sampled(const float* logits, int rows, int V, const int32_t* draft
                       float temperature, int q_mode, const float* q_point,
                       const float* uniforms, int32_t* out_token);
 
+/* LogitsProcessor.prepare over a full row in place: history tokens (unique) with counts plus
+ * the first n_extra drafts (seen, counted once each). */
+void or_penalize_row(float* l, int V, const int32_t* hist_tok, const int32_t* hist_cnt,
+                     int n_hist, const int32_t* extra, int n_extra, float rep, float pres,
+                     float freq);
+/* Nucleus + multinomial in the canonical order (ranked by e descending, lower id first). */
+int or_nucleus_sample(const float* e, int V, float Z, float top_p, float u);
+/* or_accept_sampled with penalties (history + accepted drafts) and top-p. */
+int or_accept_sampled_ex(const float* logits, int rows, int V, const int32_t* draft,
+                         float temperature, float top_p, float rep, float pres, float freq,
+                         const int32_t* hist_tok, const int32_t* hist_cnt, int n_hist,
+                         int q_mode, const float* q_point, const float* uniforms,
+                         int32_t* out_token);
+
 /* Restatement of SpeculativeSampling.tryAccept / LogitsProcessor over a candidate list
  * (used for the reference's own KATs).  rng: SplitMix64 state. */
 int or_try_accept(int draft_token, const int32_t* ids, const float* logits, int n,

@@ -53,6 +53,15 @@ def lib():
         L.or_accept_sampled.restype = C.c_int
         L.or_accept_sampled.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_float,
                                         C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.or_accept_sampled_ex.restype = C.c_int
+        L.or_accept_sampled_ex.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_float,
+                                           C.c_float, C.c_float, C.c_float, C.c_float,
+                                           C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                           C.c_void_p, C.c_void_p]
+        L.or_penalize_row.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int,
+                                      C.c_void_p, C.c_int, C.c_float, C.c_float, C.c_float]
+        L.or_nucleus_sample.restype = C.c_int
+        L.or_nucleus_sample.argtypes = [C.c_void_p, C.c_int, C.c_float, C.c_float, C.c_float]
         L.or_try_accept.restype = C.c_int
         L.or_try_accept.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_float,
                                     C.c_float, C.c_void_p, C.c_void_p]
@@ -424,6 +433,43 @@ def accept_sampled(logits, draft, temperature, q_mode, uniforms, q_point=None):
                                   C.c_float(temperature), q_mode,
                                   None if qp is None else qp.ctypes.data, u.ctypes.data,
                                   tok.ctypes.data)
+    return acc, int(tok[0])
+
+
+def penalize_row(logits, hist_tok=(), hist_cnt=(), extra=(), rep=1.0, pres=0.0, freq=0.0):
+    """LogitsProcessor.prepare over one full row (a copy is returned)."""
+    l = np.array(logits, np.float32, copy=True)
+    ht = _c(np.asarray(hist_tok, np.int32), np.int32)
+    hc = _c(np.asarray(hist_cnt, np.int32), np.int32)
+    ex = _c(np.asarray(extra, np.int32), np.int32)
+    lib().or_penalize_row(l.ctypes.data, l.size, ht.ctypes.data, hc.ctypes.data, ht.size,
+                          ex.ctypes.data, ex.size, C.c_float(rep), C.c_float(pres),
+                          C.c_float(freq))
+    return l
+
+
+def nucleus_sample(e, Z, top_p, u):
+    e = _c(e, np.float32)
+    return lib().or_nucleus_sample(e.ctypes.data, e.size, C.c_float(Z), C.c_float(top_p),
+                                   C.c_float(u))
+
+
+def accept_sampled_ex(logits, draft, temperature, q_mode, uniforms, q_point=None, top_p=1.0,
+                      rep=1.0, pres=0.0, freq=0.0, hist_tok=(), hist_cnt=()):
+    logits = _c(logits, np.float32)
+    rows, V = logits.shape
+    d = _c(draft, np.int32)
+    u = _c(uniforms, np.float32)
+    qp = None if q_point is None else _c(q_point, np.float32)
+    ht = _c(np.asarray(hist_tok, np.int32), np.int32)
+    hc = _c(np.asarray(hist_cnt, np.int32), np.int32)
+    tok = np.zeros(1, np.int32)
+    acc = lib().or_accept_sampled_ex(logits.ctypes.data, rows, V, d.ctypes.data,
+                                     C.c_float(temperature), C.c_float(top_p), C.c_float(rep),
+                                     C.c_float(pres), C.c_float(freq), ht.ctypes.data,
+                                     hc.ctypes.data, ht.size, q_mode,
+                                     None if qp is None else qp.ctypes.data, u.ctypes.data,
+                                     tok.ctypes.data)
     return acc, int(tok[0])
 
 

@@ -174,3 +174,48 @@ def test_accept_sampled_bit_exact(ctx, head_case, orc, q_mode, temp):
     print("accepted-count histogram", seen, flush=True)
     if temp < 0.5 or q_mode == 1:
         assert len(seen) >= 2  # both early rejects and long accepts were exercised
+
+
+@pytest.mark.parametrize("opts", [
+    dict(top_p=0.9),
+    dict(top_p=0.5, rep=1.3, pres=0.4, freq=0.25),
+    dict(rep=1.5, pres=0.8, freq=0.6),
+    dict(top_p=0.02, rep=0.8),
+])
+def test_accept_sampled_ex_bit_exact(ctx, head_case, orc, opts):
+    """LogitsProcessor options over the full 151936-token head: penalties on every row (the
+    history plus the drafts accepted before it) and samplePrepared's nucleus for the bonus and
+    for a residual without mass (a device radix sort ranks the row), bit for bit against the
+    oracle's canonical rule on the same logits and uniforms; the caller's logits stay as they
+    were."""
+    import torch
+
+    am = head_case["am"]
+    logits = head_case["logits"]
+    lh = host(logits)
+    rng = np.random.default_rng(31)
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    seen = {}
+    for trial in range(8):
+        draft = am[:M - 1].copy()
+        for i in range(6, M - 1):
+            draft[i] = rng.integers(0, V)
+        if trial % 4 == 0:
+            draft[int(rng.integers(0, 6))] = rng.integers(0, V)  # early reject
+        hist = {int(t): int(c) for t, c in zip(rng.integers(0, V, 200), rng.integers(0, 4, 200))}
+        for t in draft[:3]:
+            hist[int(t)] = hist.get(int(t), 0) + 1  # drafts already in the history
+        q_mode = trial % 2
+        dd = dev(draft.astype(np.int32))
+        torch.cuda.synchronize()
+        ctx.accept_sampled_ex(logits, M, V, dd, q_mode, 77, trial, out, 0.7, hist=hist, **opts)
+        ctx.sync()
+        got = tuple(int(v) for v in host(out))
+        u = orc.verify_uniforms(77, trial, M)
+        ht = np.array(list(hist.keys()), np.int32)
+        hc = np.array([hist[t] for t in ht.tolist()], np.int32)
+        ref = orc.accept_sampled_ex(lh, draft, 0.7, q_mode, u, hist_tok=ht, hist_cnt=hc, **opts)
+        assert got == ref, (trial, opts, got, ref)
+        seen[ref[0]] = seen.get(ref[0], 0) + 1
+    assert (host(logits).view(np.uint32) == lh.view(np.uint32)).all()
+    print("accepted-count histogram", opts, seen, flush=True)

@@ -289,6 +289,45 @@ def test_sampled_verify_bit_exact(model, orc, q_mode):
     print("sampled accepted histogram", hist, flush=True)
 
 
+@pytest.mark.parametrize("q_mode", [0, 1])
+def test_sampled_verify_ex_bit_exact(model, orc, q_mode):
+    """mj_verify_sampled_ex (penalties with a history, nucleus) through the model: the eager
+    pass's decision equals the oracle's on the pass's own logits, and a graph-replayed pass of
+    the same inputs decides the same, replay after replay."""
+    import torch
+
+    eng, cfg = model["eng"], model["cfg"]
+    rng = np.random.default_rng(40 + q_mode)
+    eng.rewind(0)
+    y = eng.prefill(rng.integers(0, cfg.vocab, 60).tolist())
+    cont = greedy_continuation(eng, y, 8)
+    L0 = eng.offset
+    cap = torch.empty((64, cfg.vocab), dtype=torch.float32, device="cuda")
+    opts = [dict(top_p=0.8, rep=1.2, pres=0.3, freq=0.2), dict(top_p=0.3),
+            dict(rep=1.4, freq=0.5)]
+    for trial in range(6):
+        o = opts[trial % 3]
+        hist = {int(t): int(c) for t, c in zip(rng.integers(0, cfg.vocab, 30),
+                                                 rng.integers(1, 3, 30))}
+        hist[int(cont[0])] = 2
+        draft = cont[:4] + [int(t) for t in rng.integers(0, cfg.vocab, 4)]
+        eng.rewind(L0)
+        eng.set_capture(logits=cap)
+        acc, tok = eng.verify_sampled_ex(y, draft, q_mode, 123, trial, 0.7, hist=hist, **o)
+        eng.set_capture()
+        lg = host(cap)[:9]
+        u = orc.verify_uniforms(123, trial, 9)
+        ht = np.array(list(hist.keys()), np.int32)
+        hc = np.array([hist[t] for t in ht.tolist()], np.int32)
+        ref = orc.accept_sampled_ex(lg, np.array(draft, np.int32), 0.7, q_mode, u,
+                                    hist_tok=ht, hist_cnt=hc, **o)
+        assert (acc, tok) == ref, (trial, o, acc, tok, ref)
+        for _ in range(2):  # graph replays
+            eng.rewind(L0)
+            assert eng.verify_sampled_ex(y, draft, q_mode, 123, trial, 0.7, hist=hist,
+                                         **o) == (acc, tok)
+
+
 def test_graph_replays_equal_eager(model):
     eng, cfg = model["eng"], model["cfg"]
     rng = np.random.default_rng(5)
