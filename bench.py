@@ -89,6 +89,33 @@ def timed_steps(eng, y, draft, parents, L0, steps, warmup):
     return toks, dt, dev_ms / steps, acc
 
 
+def timed_sampled(eng, y, draft, L0, steps, warmup, **opts):
+    """Sampled verify passes (T = 0.7, uniform draft q, fresh Philox counter each step); with
+    `opts` the LogitsProcessor options go through mj_verify_sampled_ex."""
+    import torch
+
+    def one(i):
+        eng.rewind(L0)
+        if opts:
+            return eng.verify_sampled_ex(y, draft, 1, 7, i, 0.7, **opts)
+        return eng.verify_sampled(y, draft, 0.7, 1, 7, i)
+
+    for i in range(warmup):
+        one(i)
+    torch.cuda.synchronize()
+    toks, dev_ms = 0, 0.0
+    t0 = time.perf_counter()
+    for i in range(steps):
+        acc, _ = one(warmup + i)
+        toks += acc + 1
+        dev_ms += eng.last_pass_ms()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"tokens_per_s": round(toks / dt, 3), "ms_per_step": round(dt / steps * 1e3, 4),
+            "device_ms_per_step": round(dev_ms / steps, 4),
+            "mean_tokens_per_step": round(toks / steps, 3)}
+
+
 def expert_bytes(cfg, inds_layers, M):
     """Algorithmic bytes of one up||gate and one down launch per layer (unique experts once)."""
     H, I, gs, k = cfg.H, cfg.I, cfg.gs, cfg.top_k
@@ -105,9 +132,10 @@ def expert_bytes(cfg, inds_layers, M):
     return np.array(up), np.array(dn), np.array(uniq)
 
 
-def cpu_baseline(eng, cfg, weights, y, draft, L0):
+def cpu_baseline(eng, cfg, weights, y, draft, L0, reps=5):
     """Oracle restatement timed on the host: layers 0-1 of the verify pass (from the GPU's own
-    layer inputs and KV cache) + the full fp16 lm_head for the 9 rows; scaled to 24 layers."""
+    layer inputs and KV cache) + the full fp16 lm_head for the 9 rows; scaled to 24 layers.
+    Median of `reps` timings with one OpenMP thread and with every core of the process."""
     import torch
 
     from oracle import oracle as orc
@@ -138,21 +166,47 @@ def cpu_baseline(eng, cfg, weights, y, draft, L0):
     head_h = head.cpu().numpy()
     fn = fnorm.cpu().numpy()
     par = np.array(list(range(-1, M - 1)), np.int32)
-    t0 = time.perf_counter()
-    for l in range(2):
-        orc.layer_forward(cfg.attn_cfg(), lw[l], hc[l, :M], kv0[l][0], kv0[l][1], L0, par)
-    t_layers = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    xf = orc.rms_norm(hc[cfg.n_layers, :M], fn, cfg.eps)
-    logits = orc.lm_head_logits(xf, head_h)
-    orc.argmax_rows(logits)
-    t_head = time.perf_counter() - t0
-    step_s = t_layers / 2 * cfg.n_layers + t_head
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return dict(value=round((acc + 1) / step_s, 4), unit="tokens/s", cores=threads, kind="port",
-                sample=(f"oracle verify pass, layers 0-1 of 24 ({t_layers:.2f} s, teacher-forced "
-                        f"from the GPU layer inputs) + fp16 lm_head over 9 rows ({t_head:.2f} s), "
-                        f"scaled to 24 layers: {step_s:.2f} s/step, {acc + 1} tokens/step"))
+
+    def sample():
+        """One timing of the bounded sample: (layers 0-1 seconds, lm_head seconds)."""
+        t0 = time.perf_counter()
+        for l in range(2):
+            orc.layer_forward(cfg.attn_cfg(), lw[l], hc[l, :M], kv0[l][0], kv0[l][1], L0, par)
+        t1 = time.perf_counter()
+        xf = orc.rms_norm(hc[cfg.n_layers, :M], fn, cfg.eps)
+        orc.argmax_rows(orc.lm_head_logits(xf, head_h))
+        return t1 - t0, time.perf_counter() - t1
+
+    all_threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or len(os.sched_getaffinity(0))
+    res = {}
+    for threads in (1, all_threads):
+        orc.set_threads(threads)
+        runs = [sample() for _ in range(reps)]
+        step = sorted(tl / 2 * cfg.n_layers + th for tl, th in runs)
+        res[threads] = (step[len(step) // 2], runs)
+        log(f"cpu baseline, {threads} thread(s): step s {['%.3f' % x for x in step]}")
+    orc.set_threads(all_threads)
+    med, runs = res[all_threads]
+    med1, runs1 = res[1]
+    tl, th = sorted(runs, key=lambda r: r[0] / 2 * cfg.n_layers + r[1])[len(runs) // 2]
+    return dict(value=round((acc + 1) / med, 4), unit="tokens/s", cores=all_threads, kind="port",
+                single_thread=dict(value=round((acc + 1) / med1, 4), cores=1),
+                statistic=f"median of {reps}", cpu_model=cpu_model(),
+                sample=(f"oracle verify pass, layers 0-1 of 24 ({tl:.3f} s, teacher-forced from "
+                        f"the GPU layer inputs) + fp16 lm_head over 9 rows ({th:.3f} s), scaled "
+                        f"to 24 layers: {med:.3f} s/step at {all_threads} threads, {med1:.3f} "
+                        f"s/step at 1 thread, {acc + 1} tokens/step"))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -205,6 +259,15 @@ def main():
     tdraft = tree_draft(cont, cfg.vocab, rng)
     ttoks, tdt, tdev, tacc = timed_steps(eng, y, tdraft, TREE16, L0, args.steps, args.warmup)
     log(f"tree16: {ttoks / tdt:.1f} tok/s, {tdt / args.steps * 1e3:.3f} ms/step, accepted {tacc}")
+    # sampled verify of the same chain: plain softmax, then top-p 0.9 with repetition 1.1,
+    # presence 0.1 and frequency 0.1 over the prompt's token counts
+    sampled = timed_sampled(eng, y, draft, L0, args.steps, args.warmup)
+    hist = {}
+    for t in prompt:
+        hist[int(t)] = hist.get(int(t), 0) + 1
+    sampled_opts = timed_sampled(eng, y, draft, L0, args.steps, args.warmup, top_p=0.9, rep=1.1,
+                                 pres=0.1, freq=0.1, hist=hist)
+    log(f"sampled: {sampled}; top-p + penalties: {sampled_opts}")
 
     # per-kernel times from HIP events (eager passes) and the routing of the pass
     icap = torch.empty((cfg.n_layers, 64, cfg.top_k), dtype=torch.int32, device="cuda")
@@ -294,6 +357,9 @@ def main():
         "cpu_baseline": cpu,
         "tree": {"tokens_per_s": round(ttoks / tdt, 3), "ms_per_step": round(tdt / args.steps * 1e3, 4),
                  "accepted": tacc, "rows": len(TREE16), "device_ms_per_step": round(tdev, 4)},
+        "sampled": dict(sampled, temperature=0.7, q="uniform 1/V"),
+        "sampled_top_p_penalties": dict(sampled_opts, temperature=0.7, top_p=0.9,
+                                        repetition=1.1, presence=0.1, frequency=0.1),
         "kernels": kernels,
         "unique_experts_per_layer": round(float(uniq.mean()), 2),
     }

@@ -167,12 +167,16 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
  * (SeedlessDecodeEngine.swift:481-498, SeedlessMetal.swift:3005-3111) for an fp16 head:
  * logits[m][v] = sum_k w[v][k] * x[m][k] (fp32), argmax per row with the lowest id winning
  * ties and banned ids skipped.  x fp16 [M][K], w fp16 [V][K]; out_argmax int32 [M];
- * out_max fp32 [M] (nullable); out_logits fp32 [M][V] (nullable; written when sampling).
- * banned int32 [n_banned] device (nullable), n_banned <= 64 (the reference stages at most 16,
- * SeedlessDecodeEngine.swift:470). */
+ * out_row_max fp32 [M] (nullable): the row's largest logit; out_row_logsumexp fp32 [M]
+ * (nullable): ln sum_v exp(logits[m][v] / temperature) over the ids not banned, so that
+ * ln p = logits / T - logsumexp is LogitsProcessor.probabilities' softmax
+ * (LogitsProcessor.swift:168-189; needs temperature > 1e-5, otherwise ignored);
+ * out_logits fp32 [M][V] (nullable; written when sampling).  banned int32 [n_banned] device
+ * (nullable), n_banned <= 64 (the reference stages at most 16, SeedlessDecodeEngine.swift:470). */
 mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, int K, int V,
-                            const int32_t* banned, int n_banned, int32_t* out_argmax,
-                            float* out_max, float* out_logits);
+                            const int32_t* banned, int n_banned, float temperature,
+                            int32_t* out_argmax, float* out_row_max, float* out_row_logsumexp,
+                            float* out_logits);
 
 /* lm_head verify over the Maple checkpoint's 4-bit head -- maple_lm_head_argmax/reduce
  * (SeedlessMetal.swift:3005-3111, bound by SeedlessDecodeEngine.swift:481-498 when head_bits
@@ -184,8 +188,9 @@ mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, in
  * 16, SeedlessDecodeEngine.swift:470).  Outputs as mj_lm_head_verify. */
 mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const void* scales,
                                const void* biases, int M, int K, int V, int group_size,
-                               const int32_t* banned, int n_banned, int32_t* out_argmax,
-                               float* out_max, float* out_logits);
+                               const int32_t* banned, int n_banned, float temperature,
+                               int32_t* out_argmax, float* out_row_max,
+                               float* out_row_logsumexp, float* out_logits);
 
 /* Greedy acceptance -- verifyDraftChain (SeedlessDecodeEngine.swift:1574-1603) generalised to
  * a tree: from row 0 step to the lowest-index child whose token equals the current row's

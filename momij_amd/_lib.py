@@ -110,9 +110,9 @@ _SIGS = {
     "mj_moe_block_noalloc": (i32, [vp, C.POINTER(MoeWeights), vp, vp, i32, i32, vp, vp]),
     "mj_attn_block": (i32, [vp, C.POINTER(AttnConfig), C.POINTER(AttnWeights), vp, vp, vp, i64,
                             vp, i32]),
-    "mj_lm_head_verify": (i32, [vp, vp, vp, i32, i32, i32, vp, i32, vp, vp, vp]),
-    "mj_lm_head_verify_q4": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp,
-                                   vp]),
+    "mj_lm_head_verify": (i32, [vp, vp, vp, i32, i32, i32, vp, i32, f32, vp, vp, vp, vp]),
+    "mj_lm_head_verify_q4": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, f32, vp, vp,
+                                   vp, vp]),
     "mj_suffix_index_create": (i32, [i32, C.POINTER(vp)]),
     "mj_suffix_index_destroy": (i32, [vp]),
     "mj_suffix_index_clear": (i32, [vp]),

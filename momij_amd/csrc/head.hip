@@ -25,6 +25,7 @@ struct HeadArgs {
     float* pval;         // [blocks][32]
     int* pidx;           // [blocks][32]
     const int* abort;
+    HeadLse lse;
 };
 
 template <int NT, int PL>
@@ -46,10 +47,13 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
     const int nstrips = (a.V + 15) / 16;
     float bv[NT];
     int bi[NT];
+    float lm[NT], ls[NT];  // running log-sum-exp of logits / T (log2 units) per lane and tile
 #pragma unroll
     for (int tl = 0; tl < NT; ++tl) {
         bv[tl] = -INFINITY;
         bi[tl] = 0x7fffffff;
+        lm[tl] = -INFINITY;
+        ls[tl] = 0.0f;
     }
     // Work unit: one K half of a 16-row strip.  Wave (slot, h) of a block takes half h of
     // strips blockIdx.x * 4 + slot + round * gridDim.x * 4; the h = 1 partial meets the h = 0
@@ -138,6 +142,22 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
                             bi[tl] = v;
                         }
                     }
+                    if (a.lse.pm) {
+                        float xk[4], mx = -INFINITY;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            xk[r] = keep[r] ? acc[tl][r] * a.lse.k : -INFINITY;
+                            mx = fmaxf(mx, xk[r]);
+                        }
+                        if (mx != -INFINITY) {
+                            const float mn = fmaxf(lm[tl], mx);
+                            float sum = ls[tl] * __builtin_amdgcn_exp2f(lm[tl] - mn);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) sum += __builtin_amdgcn_exp2f(xk[r] - mn);
+                            lm[tl] = mn;
+                            ls[tl] = sum;
+                        }
+                    }
                     if (a.logits && m < a.M) {
                         float* lp = a.logits + (size_t)m * a.V + v0 + 4 * lq;
                         if (v0 + 4 * lq + 3 < a.V) {
@@ -181,6 +201,22 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
     }
     __shared__ float sv[8][32];
     __shared__ int si[8][32];
+    __shared__ float slm[4][32], sls[4][32];
+    if (a.lse.pm) {  // the h = 0 waves hold the sums
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+            for (int o = 16; o < 64; o <<= 1)
+                lse_merge(lm[tl], ls[tl], __shfl_xor(lm[tl], o, MJ_WAVE),
+                          __shfl_xor(ls[tl], o, MJ_WAVE));
+        if (lane < 16 && h == 0) {
+#pragma unroll
+            for (int tl = 0; tl < NT; ++tl) {
+                slm[slot][tl * 16 + lane] = lm[tl];
+                sls[slot][tl * 16 + lane] = ls[tl];
+            }
+        }
+    }
     if (lane < 16) {
 #pragma unroll
         for (int tl = 0; tl < NT; ++tl) {
@@ -199,6 +235,12 @@ __global__ __launch_bounds__(512) void k_lm_head(HeadArgs a) {
             }
         a.pval[(size_t)blockIdx.x * 32 + t] = b;
         a.pidx[(size_t)blockIdx.x * 32 + t] = i;
+        if (a.lse.pm) {
+            float m = slm[0][t], sm = sls[0][t];
+            for (int w = 1; w < 4; ++w) lse_merge(m, sm, slm[w][t], sls[w][t]);
+            a.lse.pm[(size_t)blockIdx.x * 32 + t] = m;
+            a.lse.ps[(size_t)blockIdx.x * 32 + t] = sm;
+        }
     }
 }
 
@@ -238,6 +280,7 @@ struct HeadQ4Args {
     float* pval;         // [blocks][32]
     int* pidx;
     const int* abort;
+    HeadLse lse;
 };
 
 template <int PL>
@@ -294,12 +337,15 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
     const int hsh = 16 * (q & 1);      // this lane's half of a scale word in the remainder chain
     float bv[NT][4];
     int bi[NT][4];
+    float lm[NT][4], ls[NT][4];  // running log-sum-exp of logits / T (log2 units)
 #pragma unroll
     for (int tl = 0; tl < NT; ++tl)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             bv[tl][r] = -INFINITY;
             bi[tl][r] = 0x7fffffff;
+            lm[tl][r] = -INFINITY;
+            ls[tl][r] = 0.0f;
         }
     auto load_piece = [&](int strip, int pc, Q4Piece<PL>& pz) {
         const int vr = min(strip * 16 + n, a.V - 1);
@@ -426,6 +472,12 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
                             bv[tl][r] = val;
                             bi[tl][r] = v;
                         }
+                        if (keep && a.lse.pm) {
+                            const float xk = val * a.lse.k, mn = fmaxf(lm[tl][r], xk);
+                            ls[tl][r] = ls[tl][r] * __builtin_amdgcn_exp2f(lm[tl][r] - mn) +
+                                        __builtin_amdgcn_exp2f(xk - mn);
+                            lm[tl][r] = mn;
+                        }
                         if (a.logits && m < a.M && v < a.V) a.logits[(size_t)m * a.V + v] = val;
                     }
             }
@@ -461,6 +513,17 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
             }
     __shared__ float sv[4][32];
     __shared__ int si[4][32];
+    __shared__ float slm[4][32], sls[4][32];
+    if (a.lse.pm) {
+#pragma unroll
+        for (int tl = 0; tl < NT; ++tl)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1)
+                    lse_merge(lm[tl][r], ls[tl][r], __shfl_xor(lm[tl][r], o, MJ_WAVE),
+                              __shfl_xor(ls[tl][r], o, MJ_WAVE));
+    }
     if (h == 0 && n == 0) {
 #pragma unroll
         for (int tl = 0; tl < NT; ++tl)
@@ -468,6 +531,8 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
             for (int r = 0; r < 4; ++r) {
                 sv[slot][tl * 16 + 4 * q + r] = bv[tl][r];
                 si[slot][tl * 16 + 4 * q + r] = bi[tl][r];
+                slm[slot][tl * 16 + 4 * q + r] = lm[tl][r];
+                sls[slot][tl * 16 + 4 * q + r] = ls[tl][r];
             }
     }
     __syncthreads();
@@ -481,18 +546,25 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
             }
         a.pval[(size_t)blockIdx.x * 32 + t] = bb;
         a.pidx[(size_t)blockIdx.x * 32 + t] = ii;
+        if (a.lse.pm) {
+            float m = slm[0][t], sm = sls[0][t];
+            for (int w2 = 1; w2 < 4; ++w2) lse_merge(m, sm, slm[w2][t], sls[w2][t]);
+            a.lse.pm[(size_t)blockIdx.x * 32 + t] = m;
+            a.lse.ps[(size_t)blockIdx.x * 32 + t] = sm;
+        }
     }
 }
 
-// One wave per row: fold the block partials (value, lowest id on ties).
+// One wave per row: fold the block partials (value, lowest id on ties; log-sum-exp pairs).
 __global__ __launch_bounds__(64) void k_head_final(const float* pval, const int* pidx, int nblk,
                                                    int M, int32_t* out_idx, float* out_max,
-                                                   const int* abort) {
+                                                   HeadLse lse, const int* abort) {
     if (aborted(abort)) return;
     const int m = blockIdx.x, lane = threadIdx.x;
     if (m >= M) return;
     float b = -INFINITY;
     int i = 0x7fffffff;
+    float lm = -INFINITY, ls = 0.0f;
     for (int k0 = 0; k0 < nblk; k0 += 8 * 64) {  // eight partials a lane requested together
         float v[8];
         int j[8];
@@ -508,11 +580,25 @@ __global__ __launch_bounds__(64) void k_head_final(const float* pval, const int*
                 b = v[u];
                 i = j[u];
             }
+        if (lse.out) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int k = k0 + 64 * u + lane;
+                if (k < nblk) lse_merge(lm, ls, lse.pm[(size_t)k * 32 + m], lse.ps[(size_t)k * 32 + m]);
+            }
+        }
     }
     wave_argmax(b, i);
+    if (lse.out) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+            lse_merge(lm, ls, __shfl_xor(lm, o, MJ_WAVE), __shfl_xor(ls, o, MJ_WAVE));
+    }
     if (lane == 0) {
         out_idx[m] = i;
         if (out_max) out_max[m] = b;
+        // ln sum_v exp(logit_v / T) = ln 2 * (m + log2 s); -inf when every id is banned
+        if (lse.out) lse.out[m] = lm == -INFINITY ? -INFINITY : 0.69314718f * (lm + __log2f(ls));
     }
 }
 
@@ -533,16 +619,19 @@ int head_blocks() {
 // Rows go through in groups of <= 32 (two 16-row MFMA tiles staged in LDS per group).
 hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, int V,
                           const int32_t* banned, int n_banned, float* logits, float* pval,
-                          int* pidx, int32_t* out_idx, float* out_max, const int* abort,
-                          hipStream_t st) {
+                          int* pidx, int32_t* out_idx, float* out_max, HeadLse lse,
+                          const int* abort, hipStream_t st) {
     if (K % 256 != 0 || M < 1 || n_banned > MJ_HEAD_MAX_BANNED)  // halves of 128-k multiples
         return hipErrorInvalidValue;
     for (int m0 = 0; m0 < M; m0 += 32) {
         const int mg = M - m0 < 32 ? M - m0 : 32;
         // two blocks per CU for one 16-row tile; a 32-row group's LDS allows one
         const int nb = mg <= 16 ? head_blocks() : head_blocks() / 2;
+        HeadLse gl = lse;
+        if (!gl.out) gl.pm = gl.ps = nullptr;
+        else gl.out += m0;
         HeadArgs a{x + (size_t)m0 * K, w, mg, K, V, banned, n_banned,
-                   logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
+                   logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort, gl};
         const bool pl8 = (K / 64) % 8 == 0;  // 8-chunk pieces when the half strip allows
         if (mg <= 16) {
             const size_t lds = (size_t)16 * (K + 8) * 2;
@@ -561,7 +650,7 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg,
-                           out_idx + m0, out_max ? out_max + m0 : nullptr, abort);
+                           out_idx + m0, out_max ? out_max + m0 : nullptr, gl, abort);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -766,7 +855,8 @@ hipError_t set_gather3_attributes();
 hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_t* s,
                              const uint16_t* b, int M, int K, int V, const int32_t* banned,
                              int n_banned, float* logits, float* pval, int* pidx,
-                             int32_t* out_idx, float* out_max, const int* abort, hipStream_t st) {
+                             int32_t* out_idx, float* out_max, HeadLse lse, const int* abort,
+                             hipStream_t st) {
     if (K % 512 != 0 || K > 4096 || M < 1 || n_banned > MJ_HEAD_MAX_BANNED)
         return hipErrorInvalidValue;
     const bool pl4 = (K / 128) % 8 == 0;  // half strip of K / 128 groups: 8-group pieces
@@ -776,8 +866,11 @@ hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_
         const size_t lds = (size_t)nt * 16 * (K + 8) * 2 + (size_t)nt * 16 * (K / 64 + 1) * 4;
         if (lds > 140 * 1024) return hipErrorInvalidValue;
         const int nb = nt == 1 ? head_blocks() : head_blocks() / 2;
+        HeadLse gl = lse;
+        if (!gl.out) gl.pm = gl.ps = nullptr;
+        else gl.out += m0;
         HeadQ4Args qa{x + (size_t)m0 * K, w, s, b, mg, K, V, banned, n_banned,
-                      logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort};
+                      logits ? logits + (size_t)m0 * V : nullptr, pval, pidx, abort, gl};
         if (nt == 1 && pl4)
             launch_timed(k_lm_head_q4<1, 4>, dim3(nb), dim3(512), lds, st, qa);
         else if (nt == 1)
@@ -789,7 +882,7 @@ hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg,
-                           out_idx + m0, out_max ? out_max + m0 : nullptr, abort);
+                           out_idx + m0, out_max ? out_max + m0 : nullptr, gl, abort);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

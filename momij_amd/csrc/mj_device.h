@@ -160,6 +160,14 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
     }
 }
 
+// Running log-sum-exp in log2 units: (m, s) stands for s * 2^m.  (-inf, 0) is empty.
+__device__ __forceinline__ void lse_merge(float& m, float& s, float om, float os) {
+    const float mn = fmaxf(m, om);
+    if (mn == -INFINITY) return;
+    s = s * __builtin_amdgcn_exp2f(m - mn) + os * __builtin_amdgcn_exp2f(om - mn);
+    m = mn;
+}
+
 __device__ __forceinline__ f4 mfma16x16x4f32(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }

@@ -171,17 +171,26 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t st);
 int attn_max_chunks(int window, int64_t L_max, int M);
 
 // head.hip
+// Optional per-row log-sum-exp of logits / T: k = log2(e) / T, block partials pm / ps
+// [blocks][32] (log2-unit max and scaled sum), out [M] natural-log result.  out == nullptr: off.
+struct HeadLse {
+    float k;
+    float* pm;
+    float* ps;
+    float* out;
+};
 hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, int V,
                           const int32_t* banned, int n_banned, float* logits, float* pval,
-                          int* pidx, int32_t* out_idx, float* out_max, const int* abort,
-                          hipStream_t st);
+                          int* pidx, int32_t* out_idx, float* out_max, HeadLse lse,
+                          const int* abort, hipStream_t st);
 // Banned ids the 4-bit head stages in LDS (the reference passes at most 16,
 // SeedlessDecodeEngine.swift:470, 496).
 #define MJ_HEAD_MAX_BANNED 64
 hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_t* s,
                              const uint16_t* b, int M, int K, int V, const int32_t* banned,
                              int n_banned, float* logits, float* pval, int* pidx,
-                             int32_t* out_idx, float* out_max, const int* abort, hipStream_t st);
+                             int32_t* out_idx, float* out_max, HeadLse lse, const int* abort,
+                             hipStream_t st);
 int head_blocks();
 hipError_t launch_accept_greedy(const int32_t* tokens, const int32_t* parents,
                                 const int32_t* argmax, int n, StepResult* res, int32_t* out_flat,

@@ -261,11 +261,13 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                        launch_lm_head_q4(m->xf, (const uint32_t*)m->lm_head,
                                          (const uint16_t*)c.lm_head_scales,
                                          (const uint16_t*)c.lm_head_biases, M, H, c.vocab, nullptr,
-                                         0, logits, m->pval, m->pidx, m->argmax, m->maxv, ab, st),
+                                         0, logits, m->pval, m->pidx, m->argmax, m->maxv,
+                                         HeadLse{}, ab, st),
                        "lm_head q4");
         else
             s = mj_hip(ctx, launch_lm_head(m->xf, m->lm_head, M, H, c.vocab, nullptr, 0, logits,
-                                           m->pval, m->pidx, m->argmax, m->maxv, ab, st),
+                                           m->pval, m->pidx, m->argmax, m->maxv, HeadLse{}, ab,
+                                           st),
                        "lm_head");
         if (m->profiling) m->prof.end(st);
         if (s != MJ_OK) return s;
@@ -895,9 +897,29 @@ mj_status mj_attn_block(mj_ctx* ctx, const mj_attn_config* cfg, const mj_attn_we
     return mj_hip(ctx, launch_gather(o, EPI_ADD, M, 1, st), "o proj");
 }
 
+// Scratch for the head's block partials: value/index and, with a log-sum-exp output, the
+// (max, sum) pairs.  Returns the pointers in p[0..3] (p[2], p[3] null without lse).
+static mj_status head_scratch(mj_ctx* ctx, bool lse, void* p[4]) {
+    const size_t part = (size_t)head_blocks() * 32 * 4;
+    Arena count;
+    for (int i = 0; i < (lse ? 4 : 2); ++i) count.take(part);
+    mj_status s = mj_scratch_reserve(ctx, count.off);
+    if (s != MJ_OK) return s;
+    Arena real{ctx->scratch, 0};
+    for (int i = 0; i < 4; ++i) p[i] = i < (lse ? 4 : 2) ? real.take(part) : nullptr;
+    return MJ_OK;
+}
+
+// Temperature check shared by both heads: the log-sum-exp is of logits / T, T > 1e-5 (the
+// sampled regime of LogitsProcessor.probabilities, LogitsProcessor.swift:168-189).
+static bool head_lse_arg_ok(float temperature, const float* out_lse) {
+    return !out_lse || (temperature > 1e-5f && std::isfinite(temperature));
+}
+
 mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, int K, int V,
-                            const int32_t* banned, int n_banned, int32_t* out_argmax,
-                            float* out_max, float* out_logits) {
+                            const int32_t* banned, int n_banned, float temperature,
+                            int32_t* out_argmax, float* out_row_max, float* out_row_logsumexp,
+                            float* out_logits) {
     if (!ctx) return MJ_INVALID_ARG;
     if (!x || !w || !out_argmax || M < 1 || M > MJ_MAX_ROWS || V < 1 || n_banned < 0 ||
         (n_banned > 0 && !banned))
@@ -906,29 +928,32 @@ mj_status mj_lm_head_verify(mj_ctx* ctx, const void* x, const void* w, int M, in
     if (n_banned > MJ_HEAD_MAX_BANNED)
         return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify: n_banned=%d (at most %d)", n_banned,
                        MJ_HEAD_MAX_BANNED);
+    if (!head_lse_arg_ok(temperature, out_row_logsumexp))
+        return mj_fail(ctx, MJ_INVALID_ARG,
+                       "lm_head_verify: temperature %g (the log-sum-exp needs T > 1e-5)",
+                       (double)temperature);
     if (K % 256 != 0 || K > 4096)
         return mj_fail(ctx, MJ_UNSUPPORTED_SHAPE, "lm_head_verify: K=%d (need K%%256==0, <=4096)",
                        K);
     hipSetDevice(ctx->device);
     mj_status s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
     if (s != MJ_OK) return s;
-    Arena count;
-    count.take((size_t)head_blocks() * 32 * 4);
-    count.take((size_t)head_blocks() * 32 * 4);
-    s = mj_scratch_reserve(ctx, count.off);
+    void* p[4];
+    s = head_scratch(ctx, out_row_logsumexp != nullptr, p);
     if (s != MJ_OK) return s;
-    Arena real{ctx->scratch, 0};
-    float* pval = (float*)real.take((size_t)head_blocks() * 32 * 4);
-    int* pidx = (int*)real.take((size_t)head_blocks() * 32 * 4);
+    const HeadLse lse{1.4426950408889634f / temperature, (float*)p[2], (float*)p[3],
+                      out_row_logsumexp};
     return mj_hip(ctx, launch_lm_head((const uint16_t*)x, (const uint16_t*)w, M, K, V, banned,
-                                      n_banned, out_logits, pval, pidx, out_argmax, out_max,
-                                      ctx->abort_dev, ctx->stream), "lm_head");
+                                      n_banned, out_logits, (float*)p[0], (int*)p[1], out_argmax,
+                                      out_row_max, lse, ctx->abort_dev, ctx->stream),
+                  "lm_head");
 }
 
 mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const void* scales,
                                const void* biases, int M, int K, int V, int group_size,
-                               const int32_t* banned, int n_banned, int32_t* out_argmax,
-                               float* out_max, float* out_logits) {
+                               const int32_t* banned, int n_banned, float temperature,
+                               int32_t* out_argmax, float* out_row_max,
+                               float* out_row_logsumexp, float* out_logits) {
     if (!ctx) return MJ_INVALID_ARG;
     if (!x || !w || !scales || !biases || !out_argmax || M < 1 || M > MJ_MAX_ROWS || V < 1 ||
         n_banned < 0 || (n_banned > 0 && !banned))
@@ -937,6 +962,10 @@ mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const 
     if (n_banned > MJ_HEAD_MAX_BANNED)
         return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify_q4: n_banned=%d (at most %d)",
                        n_banned, MJ_HEAD_MAX_BANNED);
+    if (!head_lse_arg_ok(temperature, out_row_logsumexp))
+        return mj_fail(ctx, MJ_INVALID_ARG,
+                       "lm_head_verify_q4: temperature %g (the log-sum-exp needs T > 1e-5)",
+                       (double)temperature);
     if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)scales | (uintptr_t)biases) & 15)
         return mj_fail(ctx, MJ_INVALID_ARG, "lm_head_verify_q4: operands need 16-byte alignment");
     const int kmax = M > 16 ? 2048 : 4096;  // staged hidden rows fit 140 KB of LDS
@@ -947,19 +976,16 @@ mj_status mj_lm_head_verify_q4(mj_ctx* ctx, const void* x, const void* w, const 
     hipSetDevice(ctx->device);
     mj_status s = mj_hip(ctx, set_kernel_attributes(), "kernel attributes");
     if (s != MJ_OK) return s;
-    Arena count;
-    count.take((size_t)head_blocks() * 32 * 4);
-    count.take((size_t)head_blocks() * 32 * 4);
-    s = mj_scratch_reserve(ctx, count.off);
+    void* p[4];
+    s = head_scratch(ctx, out_row_logsumexp != nullptr, p);
     if (s != MJ_OK) return s;
-    Arena real{ctx->scratch, 0};
-    float* pval = (float*)real.take((size_t)head_blocks() * 32 * 4);
-    int* pidx = (int*)real.take((size_t)head_blocks() * 32 * 4);
+    const HeadLse lse{1.4426950408889634f / temperature, (float*)p[2], (float*)p[3],
+                      out_row_logsumexp};
     return mj_hip(ctx,
                   launch_lm_head_q4((const uint16_t*)x, (const uint32_t*)w,
                                     (const uint16_t*)scales, (const uint16_t*)biases, M, K, V,
-                                    banned, n_banned, out_logits, pval, pidx, out_argmax, out_max,
-                                    ctx->abort_dev, ctx->stream),
+                                    banned, n_banned, out_logits, (float*)p[0], (int*)p[1],
+                                    out_argmax, out_row_max, lse, ctx->abort_dev, ctx->stream),
                   "lm_head q4");
 }
 

@@ -122,32 +122,21 @@ __global__ __launch_bounds__(256) void k_qmv2(QmvArgs a) {
     const int wb = (gw % a.waves_per_pair) * a.rows_per_wave;
     const int wend = min(wb + a.rows_per_wave, nout);
     const int sub = lane / LPR, li = lane % LPR;
-    const int e = a.inds[p];
-
-    // activation block li in qx order, with its sums
-    const uint16_t* xr = a.x + (size_t)(a.lhs_per ? p : 0) * a.K + 64 * li;
-    uint32_t xp[32];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const u4v lo = *(const u4v*)(xr + 16 * c);
-        const u4v hi = *(const u4v*)(xr + 16 * c + 8);
-        const uint32_t u[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        perm16(u, xp + 8 * c);
-    }
-    float X = 0.0f, Bx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        X = dot2(xp[i], 0x3C003C00u, X);
-        Bx = dot2(xp[i], (i & 1) ? 0x44004400u : 0x4C004C00u, Bx);
-    }
     const int kw = a.K >> 4, kg = a.K / a.gs;
     const int gidx = (64 * li) / a.gs;
-
-    for (int o0 = wb; o0 < wend; o0 += OUT_PER_IT) {
-        int oi[U];
-        bool ok[U];
-        u4v cw[U];
-        float sc[U], bi[U];
+    // The weight stream is the long latency: the expert id and the activation block are
+    // fetched first, the first iteration's codes, scales and biases requested as soon as the
+    // id is in, and the activation block formed while they arrive.
+    const int e = a.inds[p];
+    const uint16_t* xr = a.x + (size_t)(a.lhs_per ? p : 0) * a.K + 64 * li;
+    u4v xraw[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) xraw[c] = *(const u4v*)(xr + 8 * c);
+    int oi[U];
+    bool ok[U];
+    u4v cw[U];
+    uint16_t sh[U], bh[U];
+    auto request = [&](int o0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int row;
@@ -161,9 +150,29 @@ __global__ __launch_bounds__(256) void k_qmv2(QmvArgs a) {
             ok[u] = oi[u] < wend;
             const size_t rr = (size_t)e * a.N + (ok[u] ? row : 0);
             cw[u] = *(const u4v*)(a.w + rr * kw + 4 * li);
-            sc[u] = h2f(a.s[rr * kg + gidx]);
-            bi[u] = h2f(a.b[rr * kg + gidx]);
+            sh[u] = a.s[rr * kg + gidx];
+            bh[u] = a.b[rr * kg + gidx];
         }
+    };
+    if (wb < wend) request(wb);
+
+    // activation block li in qx order, with its sums
+    uint32_t xp[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u4v lo = xraw[2 * c], hi = xraw[2 * c + 1];
+        const uint32_t u[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        perm16(u, xp + 8 * c);
+    }
+    float X = 0.0f, Bx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        X = dot2(xp[i], 0x3C003C00u, X);
+        Bx = dot2(xp[i], (i & 1) ? 0x44004400u : 0x4C004C00u, Bx);
+    }
+
+    for (int o0 = wb; o0 < wend; o0 += OUT_PER_IT) {
+        if (o0 != wb) request(o0);
         float part[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -176,7 +185,7 @@ __global__ __launch_bounds__(256) void k_qmv2(QmvArgs a) {
                 for (int i = 0; i < 8; ++i) acc[wd] = dot2(v[i], xp[8 * wd + i], acc[wd]);
             }
             const float t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-            part[u] = sc[u] * (t - Bx) + bi[u] * X;
+            part[u] = h2f(sh[u]) * (t - Bx) + h2f(bh[u]) * X;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {

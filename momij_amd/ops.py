@@ -103,17 +103,18 @@ class Context:
                                           ptr(vcache), L, par, M))
 
     def lm_head_verify(self, x, w, M, K, V, out_argmax, out_max=None, out_logits=None,
-                       banned=None, n_banned=0):
+                       banned=None, n_banned=0, temperature=1.0, out_lse=None):
         self.check(self.lib.mj_lm_head_verify(self.h, ptr(x), ptr(w), M, K, V, ptr(banned),
-                                              n_banned, ptr(out_argmax), ptr(out_max),
-                                              ptr(out_logits)))
+                                              n_banned, float(temperature), ptr(out_argmax),
+                                              ptr(out_max), ptr(out_lse), ptr(out_logits)))
 
     def lm_head_verify_q4(self, x, w, scales, biases, M, K, V, out_argmax, out_max=None,
-                          out_logits=None, banned=None, n_banned=0, group_size=64):
+                          out_logits=None, banned=None, n_banned=0, group_size=64,
+                          temperature=1.0, out_lse=None):
         self.check(self.lib.mj_lm_head_verify_q4(self.h, ptr(x), ptr(w), ptr(scales),
                                                  ptr(biases), M, K, V, group_size, ptr(banned),
-                                                 n_banned, ptr(out_argmax), ptr(out_max),
-                                                 ptr(out_logits)))
+                                                 n_banned, float(temperature), ptr(out_argmax),
+                                                 ptr(out_max), ptr(out_lse), ptr(out_logits)))
 
     def accept_greedy(self, tokens, parents, argmax, n_rows, out):
         par = None

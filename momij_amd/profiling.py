@@ -9,6 +9,7 @@ library's kernels of the passes with a given row count (9 = y plus an 8-token ch
     python -m momij_amd.profiling counters <run_counter_collection.csv> --rows 9 --scale F
     python -m momij_amd.profiling traffic  <fetch.csv> <write.csv> --rows 9 --kernel NAME
                                            --copy-mb 512 [--out FILE.json]
+    python -m momij_amd.profiling multi    <run_counter_collection.csv> --rows 9 (0: all)
 
 `trace` prints, per kernel and grid size, launches per pass and the mean / median duration;
 `--last N` restricts it to the last N passes of that row count (the eager, event-timed passes
@@ -17,7 +18,9 @@ dispatch in MB, multiplied by `--scale` (the calibration factor of the counter: 
 plain copy's known bytes to what the counter reports for it).  `traffic` takes a FETCH_SIZE and
 a WRITE_SIZE collection of runs that end with one plain device copy of `--copy-mb` MiB
 (bench.py --copy-calib-mb), derives each counter's factor from that copy, and reports the HBM
-bytes per dispatch of the kernel whose name starts with NAME.
+bytes per dispatch of the kernel whose name starts with NAME.  `multi` prints the mean per
+dispatch of every counter of a collection (e.g. SQ_VALU_MFMA_BUSY_CYCLES with GRBM_GUI_ACTIVE),
+per kernel.
 """
 from __future__ import annotations
 
@@ -98,6 +101,38 @@ def counter_summary(path: str, n_rows: int, scale: float) -> str:
     return "\n".join(out)
 
 
+def multi_counter_summary(path: str, n_rows: int | None) -> str:
+    """Mean value per dispatch of every counter in a collection, per kernel (passes of
+    `n_rows` rows, or every dispatch of this library's kernels when n_rows is None)."""
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    if n_rows is None:
+        ks = [r for r in rows if _ours(r["Kernel_Name"])]
+    else:
+        ks = [r for n, p in split_passes(rows, "Grid_Size", "Workgroup_Size") if n == n_rows
+              for r in p]
+    per = collections.defaultdict(lambda: collections.defaultdict(float))  # (key, id) -> ctr
+    keys = {}
+    names = []
+    for r in ks:
+        k = _key(r["Kernel_Name"], int(r["Grid_Size"]), int(r["Workgroup_Size"]))
+        d = int(r["Dispatch_Id"])
+        keys[d] = k
+        c = r["Counter_Name"]
+        if c not in names:
+            names.append(c)
+        per[d][c] += float(r["Counter_Value"])
+    by = collections.defaultdict(list)
+    for d, vals in per.items():
+        by[keys[d]].append(vals)
+    out = [f"mean per dispatch; dispatches counted: {len(per)}",
+           f"{'kernel [workgroups]':44s} {'n':>5s} " + " ".join(f"{c:>28s}" for c in names)]
+    for k, v in sorted(by.items()):
+        out.append(f"{k:44s} {len(v):5d} " +
+                   " ".join(f"{statistics.mean(x.get(c, 0.0) for x in v):28.1f}" for c in names))
+    return "\n".join(out)
+
+
 def copy_scale(path: str, copy_bytes: int) -> float:
     """Known bytes / counted bytes of the largest plain copy dispatch in a collection."""
     rows = [r for r in csv.DictReader(open(path)) if "copyBuffer" in r["Kernel_Name"]]
@@ -132,7 +167,7 @@ def traffic_summary(fetch_csv: str, write_csv: str, n_rows: int, kernel: str,
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("kind", choices=["trace", "counters", "traffic"])
+    ap.add_argument("kind", choices=["trace", "counters", "traffic", "multi"])
     ap.add_argument("csv")
     ap.add_argument("csv2", nargs="?")
     ap.add_argument("--kernel", default="void k_gather5<8, 64, 2, 8, 2, true, false>")
@@ -146,6 +181,8 @@ def main():
         print(trace_summary(a.csv, a.rows, a.last))
     elif a.kind == "counters":
         print(counter_summary(a.csv, a.rows, a.scale))
+    elif a.kind == "multi":
+        print(multi_counter_summary(a.csv, a.rows if a.rows > 0 else None))
     else:
         import json
 

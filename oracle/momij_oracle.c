@@ -11,6 +11,7 @@
 #include "momij_oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -1082,3 +1083,7 @@ int or_walk_draft_greedy(const int32_t* draft, int n_draft, const int32_t* row_i
     uint64_t st = 1;
     return or_walk_draft(draft, n_draft, row_ids, row_logits, n_cand, 0.0f, &st, out_next);
 }
+
+void or_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+
+int or_max_threads(void) { return omp_get_max_threads(); }

@@ -185,6 +185,10 @@ void or_layer_forward(const or_cfg* cfg, const or_layer_w* w, const float* inv_f
 void or_kv_commit(uint16_t* kcache, uint16_t* vcache, int nKV, int64_t C, int D, int64_t L,
                   const int32_t* path, int n_path);
 
+/* OpenMP threads of the parallel loops (the timed CPU baseline runs at 1 and at all cores). */
+void or_set_threads(int n);
+int or_max_threads(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,8 @@ def lib():
         L.or_accept_sampled.restype = C.c_int
         L.or_accept_sampled.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_float,
                                         C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.or_set_threads.argtypes = [C.c_int]
+        L.or_max_threads.restype = C.c_int
         L.or_accept_sampled_ex.restype = C.c_int
         L.or_accept_sampled_ex.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_float,
                                            C.c_float, C.c_float, C.c_float, C.c_float,
@@ -154,6 +156,15 @@ def score_resid(down, scores, h):
     lib().or_score_resid(down.ctypes.data, scores.ctypes.data, out.ctypes.data, M, k,
                          out.shape[1])
     return out
+
+
+def set_threads(n: int):
+    """OpenMP threads of the oracle's parallel loops."""
+    lib().or_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(lib().or_max_threads())
 
 
 def rms_norm(x, w, eps):

@@ -61,6 +61,74 @@ def test_lm_head_config3(head_case, orc):
     assert (c["mx"] == got.max(1)).all()
 
 
+# log-sum-exp bar: the fp32 running sums see at most a few hundred roundings (per-lane strip
+# sums, then lane, wave and block merges), 2e-5 relative in the worst case, i.e. 2e-5 absolute
+# in the logarithm; plus the logits' own rounding (1e-6 relative, |logit / T| < 10)
+LSE_TOL = 3e-5
+
+
+def _lse64(logits, T, banned=()):
+    z = logits.astype(np.float64) / T
+    if len(banned):
+        z[:, list(banned)] = -np.inf
+    mx = z.max(1, keepdims=True)
+    return (mx[:, 0] + np.log(np.exp(z - mx).sum(1)))
+
+
+def test_lm_head_logsumexp_config3(ctx, head_case):
+    """Per-row ln sum exp(logit / T) from the head pass (LogitsProcessor.probabilities'
+    normaliser, LogitsProcessor.swift:168-189) at T = 0.7, with the two largest ids of every
+    row banned so that the banned filter moves the result by ~1e-3 (well past the tolerance).
+    Checked against a float64 log-sum-exp of the oracle's logits and of the kernel's own;
+    argmax and row max must not change when the sum is requested."""
+    import torch
+
+    c = head_case
+    T = 0.7
+    ref = c["ref"]
+    top2 = np.argsort(-ref, axis=1)[:, :2]
+    ban = sorted(set(top2.reshape(-1).tolist()))
+    assert len(ban) <= 64
+    dban = torch.tensor(ban, dtype=torch.int32, device="cuda")
+    am = torch.empty(M, dtype=torch.int32, device="cuda")
+    mx = torch.empty(M, dtype=torch.float32, device="cuda")
+    lse = torch.empty(M, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.lm_head_verify(c["x"], c["w"], M, K, V, am, mx, None, dban, len(ban), T, lse)
+    ctx.sync()
+    got = host(lse).astype(np.float64)
+    want = _lse64(ref, T, ban)
+    own = _lse64(host(c["logits"]), T, ban)
+    print("lse", got.tolist(), "err", np.abs(got - want).max(), flush=True)
+    assert np.abs(got - want).max() < LSE_TOL
+    assert np.abs(got - own).max() < LSE_TOL
+    unbanned = _lse64(ref, T)
+    assert np.abs(unbanned - want).min() > 10 * LSE_TOL  # the banned ids matter
+    keep = np.ones(V, bool)
+    keep[ban] = False
+    ids = np.where(keep)[0]
+    sub = ref[:, keep]
+    assert (host(am) == ids[sub.argmax(1)]).all()
+    assert (host(mx) == host(c["logits"])[:, keep].max(1)).all()
+
+
+def test_lm_head_logsumexp_needs_temperature(ctx):
+    import torch
+
+    from momij_amd.ops import MomijError
+
+    w = torch.zeros((256, 256), dtype=torch.float16, device="cuda")
+    x = torch.zeros((1, 256), dtype=torch.float16, device="cuda")
+    am = torch.empty(1, dtype=torch.int32, device="cuda")
+    lse = torch.empty(1, dtype=torch.float32, device="cuda")
+    with pytest.raises(MomijError):
+        ctx.lm_head_verify(x, w, 1, 256, 256, am, temperature=0.0, out_lse=lse)
+    ctx.lm_head_verify(x, w, 1, 256, 256, am, temperature=2.0, out_lse=lse)
+    ctx.sync()
+    # all logits 0: ln 256
+    assert abs(float(host(lse)[0]) - np.log(256.0)) < 1e-5
+
+
 def test_lm_head_banned_and_ties(ctx):
     import torch
 
@@ -91,13 +159,16 @@ def test_lm_head_many_rows(ctx, orc, Ms):
     x = rng.standard_normal((Ms, K)).astype(np.float16)
     am = torch.empty(Ms, dtype=torch.int32, device="cuda")
     lg = torch.empty((Ms, Vs), dtype=torch.float32, device="cuda")
+    lse = torch.empty(Ms, dtype=torch.float32, device="cuda")
     dw, dx = dev(w), dev(x)
     torch.cuda.synchronize()
-    ctx.lm_head_verify(dx, dw, Ms, K, Vs, am, None, lg)
+    ctx.lm_head_verify(dx, dw, Ms, K, Vs, am, None, lg, temperature=1.3, out_lse=lse)
     ctx.sync()
     ref = orc.lm_head_logits(x, w)
     idx, _, _ = orc.argmax_rows(ref)
     assert (host(am) == idx).all()
+    want = _lse64(ref, 1.3)
+    assert np.abs(host(lse) - want).max() < LSE_TOL
     assert_close(host(lg), ref, rel_tol=1e-5, abs_tol=1e-4, what=f"{Ms} rows")
 
 

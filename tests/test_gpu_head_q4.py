@@ -23,18 +23,36 @@ def ctx():
     c.close()
 
 
-def _run(ctx, x, w, s, b, M, K, V, banned=None, logits=True):
+def _run(ctx, x, w, s, b, M, K, V, banned=None, logits=True, T=None):
+    """Runs the head; with T it also returns the per-row log-sum-exp of logits / T."""
     import torch
 
     am = torch.empty(M, dtype=torch.int32, device="cuda")
     mx = torch.empty(M, dtype=torch.float32, device="cuda")
     lg = torch.empty((M, V), dtype=torch.float32, device="cuda") if logits else None
+    lse = torch.empty(M, dtype=torch.float32, device="cuda") if T else None
     db = dev(np.asarray(banned, np.int32)) if banned is not None else None
     torch.cuda.synchronize()
     ctx.lm_head_verify_q4(dev(x), dev(w), dev(s), dev(b), M, K, V, am, mx, lg, db,
-                          0 if banned is None else len(banned))
+                          0 if banned is None else len(banned), temperature=T or 1.0,
+                          out_lse=lse)
     ctx.sync()
-    return host(am), host(mx), (host(lg) if logits else None)
+    out = (host(am), host(mx), (host(lg) if logits else None))
+    return out + (host(lse).astype(np.float64),) if T else out
+
+
+# log-sum-exp bar: the fp32 running sums see at most a few hundred roundings (per-lane strip
+# sums, then lane, wave and block merges), 2e-5 relative in the worst case, i.e. 2e-5 absolute
+# in the logarithm; plus the logits' own rounding (1e-6 relative, |logit / T| < 10)
+LSE_TOL = 3e-5
+
+
+def _lse64(logits, T, banned=()):
+    z = logits.astype(np.float64) / T
+    if len(banned):
+        z[:, list(banned)] = -np.inf
+    mx = z.max(1, keepdims=True)
+    return mx[:, 0] + np.log(np.exp(z - mx).sum(1))
 
 
 def _bound(x, w, s, b, rows):
@@ -70,6 +88,16 @@ def test_lm_head_q4_full_vocab(ctx, orc):
     assert (am == idx).all(), (am, idx)
     assert_close(lg, ref, rel_tol=1e-5, abs_tol=1e-4, what="q4 full vocab logits")
     assert (mx == lg.max(1)).all()
+    # log-sum-exp of logits / 0.7 with each row's top two ids banned (moves it by ~1e-3)
+    ban = sorted(set(top2.reshape(-1).tolist()))
+    am2, _, _, lse = _run(ctx, x, w, s, b, M, K, V, banned=ban, logits=False, T=0.7)
+    want = _lse64(ref, 0.7, ban)
+    print("lse err", np.abs(lse - want).max(), flush=True)
+    assert np.abs(lse - want).max() < LSE_TOL
+    assert np.abs(_lse64(ref, 0.7) - want).min() > 10 * LSE_TOL
+    keep = np.ones(V, bool)
+    keep[ban] = False
+    assert (am2 == np.where(keep)[0][ref[:, keep].argmax(1)]).all()
 
 
 @pytest.mark.parametrize("M,K,V", [(17, 2048, 20000), (36, 1024, 5003), (9, 4096, 3000),
@@ -81,8 +109,10 @@ def test_lm_head_q4_shapes(ctx, orc, M, K, V):
     rng = np.random.default_rng(M * 7 + K + V)
     w, s, b = synth.qweight4(rng, V, K)
     x = synth.normal_f16(rng, (M, K))
-    am, mx, lg = _run(ctx, x, w, s, b, M, K, V)
+    am, mx, lg, lse = _run(ctx, x, w, s, b, M, K, V, T=1.3)
     ref = orc.lm_head_q4_logits(x, w, s, b)
+    want = _lse64(ref, 1.3)
+    assert np.abs(lse - want).max() < LSE_TOL
     idx, best, second = orc.argmax_rows(ref)
     bound = _bound(x, w, s, b, np.argsort(-ref, axis=1)[:, :2])
     clear = (best - second) > bound
