@@ -62,7 +62,8 @@ void or_resid_add(uint16_t* h, const uint16_t* delta, int M, int H);
 void or_router_logits(const uint16_t* W, const uint16_t* x, float* logits, int M, int E, int H);
 void or_route_topk(const float* logits, int32_t* inds, float* scores, int M, int E, int k);
 
-/* MoE block.  flags: bit0 = pre-norm with norm_w, bit1 = residual (y = x + moe). */
+/* MoE block.  flags: bit0 = pre-norm with norm_w, bit1 = residual (y = x + moe).
+ * out_inds int32 [M][top_k] and out_scores fp32 [M][top_k] are required (the gathers read them). */
 #define OR_MOE_PRENORM 1
 #define OR_MOE_RESIDUAL 2
 typedef struct or_moe_w {
