@@ -262,9 +262,8 @@ def main():
     # sampled verify of the same chain: plain softmax, then top-p 0.9 with repetition 1.1,
     # presence 0.1 and frequency 0.1 over the prompt's token counts
     sampled = timed_sampled(eng, y, draft, L0, args.steps, args.warmup)
-    hist = {}
-    for t in prompt:
-        hist[int(t)] = hist.get(int(t), 0) + 1
+    htok, hcnt = np.unique(np.asarray(prompt, np.int32), return_counts=True)
+    hist = (htok.astype(np.int32), hcnt.astype(np.int32))  # ascending tokens, counts
     sampled_opts = timed_sampled(eng, y, draft, L0, args.steps, args.warmup, top_p=0.9, rep=1.1,
                                  pres=0.1, freq=0.1, hist=hist)
     log(f"sampled: {sampled}; top-p + penalties: {sampled_opts}")

@@ -75,8 +75,20 @@ MJ_MAX_HIST = 65536
 
 
 def sampling(temperature, top_p=1.0, rep=1.0, pres=0.0, freq=0.0, hist=None):
-    """mj_sampling for the given options; hist: {token: count} (the seen set and counts).
-    Returns (struct, keep-alive arrays)."""
+    """mj_sampling for the given options.  hist: the seen set and counts, either a dict
+    {token: count} or a pair of int32 numpy arrays (tokens, counts) used in place (ascending
+    tokens spare the library a sort).  Returns (struct, keep-alive objects)."""
+    if isinstance(hist, tuple):
+        import numpy as np
+
+        ht = np.ascontiguousarray(hist[0], dtype=np.int32)
+        hc = np.ascontiguousarray(hist[1], dtype=np.int32)
+        if ht.shape != hc.shape or ht.ndim != 1:
+            raise ValueError("hist arrays must be two 1-D arrays of one length")
+        n = int(ht.shape[0])
+        sp = Sampling(float(temperature), float(top_p), float(rep), float(pres), float(freq),
+                      ht.ctypes.data if n else None, hc.ctypes.data if n else None, n)
+        return sp, (ht, hc)
     toks = list(hist.keys()) if hist else []
     ht = (C.c_int32 * max(len(toks), 1))(*[int(t) for t in toks])
     hc = (C.c_int32 * max(len(toks), 1))(*[int(hist[t]) for t in toks])

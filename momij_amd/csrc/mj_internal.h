@@ -246,6 +246,7 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
                                  StepResult* res, const StepDesc* sd, const int* abort,
                                  hipStream_t st);
 int sample_nblocks(int V);
+size_t sample_scratch_floats(int rows, int V);  // the bsum buffer of launch_accept_sampled
 
 // large-LDS kernels need their limit raised once per process
 hipError_t set_kernel_attributes();

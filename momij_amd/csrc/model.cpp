@@ -49,6 +49,8 @@ struct mj_model {
     int* pidx;
     int32_t* argmax;
     int32_t *hist_tok, *hist_cnt;  // sampled passes: the seen tokens (ascending) and counts
+    int32_t* hist_host = nullptr;   // pinned [2][MJ_MAX_HIST]: the history now on the device
+    int hist_n = -1;                // its length (-1: none uploaded)
     NucleusBuf nuc{};
     int32_t *inds_all;
     float* scores_all;
@@ -478,7 +480,7 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         m->maxv = (float*)a.take((size_t)R * 4);
         m->rowmax = (float*)a.take((size_t)R * 4);
         m->logits = (float*)a.take((size_t)R * c.vocab * 4);
-        m->bsum = (float*)a.take((size_t)R * sample_nblocks(c.vocab) * 4);
+        m->bsum = (float*)a.take(sample_scratch_floats(R, c.vocab) * 4);
         m->hist_tok = (int32_t*)a.take((size_t)MJ_MAX_HIST * 4);
         m->hist_cnt = (int32_t*)a.take((size_t)MJ_MAX_HIST * 4);
         nucleus_layout(a.take(nucleus_bytes(c.vocab)), c.vocab, m->nuc);
@@ -511,6 +513,8 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         hipMalloc(&m->inv_freq, inv.size() * 4) != hipSuccess ||
         hipHostMalloc(&m->sd_host, sizeof(StepDesc), hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc(&m->res_host, sizeof(StepResult), hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc(&m->hist_host, (size_t)2 * MJ_MAX_HIST * 4, hipHostMallocDefault) !=
+            hipSuccess ||
         hipEventCreate(&m->ev0) != hipSuccess || hipEventCreate(&m->ev1) != hipSuccess) {
         mj_model_destroy(m);
         return mj_fail(ctx, MJ_HIP_ERROR, "model_create: allocation failed");
@@ -546,6 +550,7 @@ mj_status mj_model_destroy(mj_model* m) {
     if (m->inv_freq) hipFree(m->inv_freq);
     if (m->sd_host) hipHostFree(m->sd_host);
     if (m->res_host) hipHostFree(m->res_host);
+    if (m->hist_host) hipHostFree(m->hist_host);
     if (m->ev0) hipEventDestroy(m->ev0);
     if (m->ev1) hipEventDestroy(m->ev1);
     delete m;
@@ -700,12 +705,14 @@ static mj_status sampling_prep(mj_ctx* ctx, const mj_sampling* sp, SampleOpts& o
     o.pres = sp->presence_penalty;
     o.freq = sp->frequency_penalty;
     std::vector<std::pair<int32_t, int32_t>> h(sp->n_hist);
+    bool sorted = true;
     for (int i = 0; i < sp->n_hist; ++i) {
         if (sp->hist_counts[i] < 0)
             return mj_fail(ctx, MJ_INVALID_ARG, "sampling options: negative count");
         h[i] = {sp->hist_tokens[i], sp->hist_counts[i]};
+        sorted = sorted && (i == 0 || h[i - 1].first <= h[i].first);
     }
-    std::sort(h.begin(), h.end());
+    if (!sorted) std::sort(h.begin(), h.end());
     for (size_t i = 1; i < h.size(); ++i)
         if (h[i].first == h[i - 1].first)
             return mj_fail(ctx, MJ_INVALID_ARG, "sampling options: token %d listed twice",
@@ -746,13 +753,21 @@ mj_status mj_verify_sampled_ex(mj_model* m, int32_t y, const int32_t* draft, int
     sd->pres = o.pres;
     sd->freq = o.freq;
     sd->n_hist = o.n_hist;
-    if (o.n_hist > 0) {
+    // the history goes up only when it differs from the one already on the device (the previous
+    // call waited for its pass, so the pinned copy is free to rewrite)
+    const size_t hn = ht.size();
+    if (o.n_hist > 0 &&
+        (m->hist_n != (int)hn || std::memcmp(m->hist_host, ht.data(), hn * 4) != 0 ||
+         std::memcmp(m->hist_host + MJ_MAX_HIST, hc.data(), hn * 4) != 0)) {
+        std::memcpy(m->hist_host, ht.data(), hn * 4);
+        std::memcpy(m->hist_host + MJ_MAX_HIST, hc.data(), hn * 4);
         hipSetDevice(m->ctx->device);
-        s = mj_hip(m->ctx, hipMemcpyAsync(m->hist_tok, ht.data(), ht.size() * 4,
+        s = mj_hip(m->ctx, hipMemcpyAsync(m->hist_tok, m->hist_host, hn * 4,
                                           hipMemcpyHostToDevice, m->ctx->stream), "history");
         if (s == MJ_OK)
-            s = mj_hip(m->ctx, hipMemcpyAsync(m->hist_cnt, hc.data(), hc.size() * 4,
+            s = mj_hip(m->ctx, hipMemcpyAsync(m->hist_cnt, m->hist_host + MJ_MAX_HIST, hn * 4,
                                               hipMemcpyHostToDevice, m->ctx->stream), "history");
+        m->hist_n = s == MJ_OK ? (int)hn : -1;
         if (s != MJ_OK) return s;
     }
     int32_t rows[MJ_MAX_ROWS];
@@ -1029,7 +1044,7 @@ mj_status mj_accept_sampled_ex(mj_ctx* ctx, const float* logits, int rows, int V
     auto layout = [&](Arena& a, float** rowmax, float** bsum, float** lcopy, int32_t** dt,
                       int32_t** dc, void** nbase) {
         *rowmax = (float*)a.take((size_t)rows * 4);
-        *bsum = (float*)a.take((size_t)rows * sample_nblocks(V) * 4);
+        *bsum = (float*)a.take(sample_scratch_floats(rows, V) * 4);
         *lcopy = pen ? (float*)a.take((size_t)rows * V * 4) : nullptr;
         *dt = (int32_t*)a.take((size_t)ht.size() * 4 + 4);
         *dc = (int32_t*)a.take((size_t)hc.size() * 4 + 4);

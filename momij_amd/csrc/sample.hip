@@ -24,6 +24,16 @@
 #define CH 16
 #define BLK 64
 #define MAX_CHUNKS 12288  // V <= 196608
+#define RMB 32            // blocks a row's maximum is split over
+#define DEC_STAGE 8192    // block sums the decision kernel stages in LDS (the rest it reads)
+
+// Hand-off from the accept decisions to the residual walk: phase 1 = row fr was rejected and
+// its residual still has to be summed (k_resid_sums) and walked (k_resid_walk).
+struct SampleState {
+    int phase, fr, d, pad;
+    float q, Zr, pad2, pad3;
+};
+static_assert(sizeof(SampleState) == 32, "state fits its 8 floats");
 
 struct SampleArgs {
     float* logits;         // [rows][V] (penalised in place)
@@ -35,8 +45,11 @@ struct SampleArgs {
     const float* q_point;  // [rows-1] or nullptr (= 1)
     uint64_t seed, counter;
     float* rowmax;         // [rows]
-    float* bsum;           // [rows][nblocks]
+    float* bsum;           // [rows][nblocks] block sums of e
     int nblocks;
+    float* mpart;          // [rows][RMB] partial row maxima
+    float* rbs;            // [nblocks] block sums of the residual of the rejected row
+    struct SampleState* state;
     int32_t* out;          // [2] or nullptr
     StepResult* res;       // or nullptr
     const StepDesc* sd;    // when set: temperature, q, seed, counter, draft, options from it
@@ -132,21 +145,21 @@ __device__ __forceinline__ float r_at(const SampleArgs& a, int row, int v, float
     return pv;
 }
 
-__global__ __launch_bounds__(1024) void k_rowmax(SampleArgs a) {
+// Row maxima in RMB slices a row (a maximum is exact in any order): block (row, j) writes the
+// maximum of its slice; the sums kernel folds the RMB partials.
+__global__ __launch_bounds__(256) void k_rowmax(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
-    const int row = blockIdx.x, t = threadIdx.x;
+    const int row = blockIdx.x / RMB, j = blockIdx.x % RMB, t = threadIdx.x;
+    const int span = (a.V + RMB - 1) / RMB;
+    const int v0 = j * span, v1 = min(a.V, v0 + span);
     float m = -INFINITY;
-    for (int v = t; v < a.V; v += 1024) m = fmaxf(m, a.logits[(size_t)row * a.V + v]);
+    for (int v = v0 + t; v < v1; v += 256) m = fmaxf(m, a.logits[(size_t)row * a.V + v]);
     m = wave_max(m);
-    __shared__ float sm[16];
+    __shared__ float sm[4];
     if ((t & 63) == 0) sm[t >> 6] = m;
     __syncthreads();
-    if (t == 0) {
-        float b = sm[0];
-        for (int w = 1; w < 16; ++w) b = fmaxf(b, sm[w]);
-        a.rowmax[row] = b;
-    }
+    if (t == 0) a.mpart[row * RMB + j] = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
 }
 
 // Block sums of e_v: one 64-thread block per (row, 1024-element block), lane = chunk.
@@ -157,7 +170,10 @@ __global__ __launch_bounds__(64) void k_sample_sums(SampleArgs a) {
     const int lane = threadIdx.x;
     const int nch = (a.V + CH - 1) / CH;
     const int chunk = b * BLK + lane;
-    const float mxs = a.rowmax[row] * a.invT;
+    float mx = lane < RMB ? a.mpart[row * RMB + lane] : -INFINITY;
+    mx = wave_max(mx);
+    if (b == 0 && lane == 0) a.rowmax[row] = mx;
+    const float mxs = mx * a.invT;
     float cs = 0.0f;
     if (chunk < nch) {
         const int e = min(chunk * CH + CH, a.V);
@@ -188,102 +204,27 @@ __device__ __forceinline__ void write_result(const SampleArgs& a, int acc, int t
     }
 }
 
-// Single block: totals, sequential accept decisions, then the residual or bonus walk (a
-// nucleus sample is left to k_nucleus_pick: the row, its uniform and Z go to the NucState).
-__global__ __launch_bounds__(1024) void k_sample_decide(SampleArgs a) {
-    if (aborted(a.abort)) return;
-    a = resolve(a);
+// Walk of row `row` to tgt over its mass -- the residual (walk_resid: block sums in rbs) or e
+// (block sums in bsum) -- block, then chunk (the chosen block's 64 chunk sums recomputed in the
+// same order), then element; writes (fr, token).  Whole block (>= 64 threads).
+__device__ void walk_write(const SampleArgs& a, int row, int fr, bool walk_resid, float tgt,
+                           float mxs, float Zr, float q, int d) {
     const int t = threadIdx.x;
-    const int D = a.rows - 1;
     const int nch = (a.V + CH - 1) / CH;
-    __shared__ float Z[MJ_ROWS];
-    __shared__ float cs[MAX_CHUNKS];
-    __shared__ float bs[MAX_CHUNKS / BLK];
-    __shared__ int s_fr, s_blk, s_bidx, s_tok;
-    __shared__ float s_t, s_P;
-    if (t < a.rows) {
-        float z = 0.0f;
-        for (int b = 0; b < a.nblocks; ++b) z = z + a.bsum[(size_t)t * a.nblocks + b];
-        Z[t] = z;
-    }
+    __shared__ float sbs[MAX_CHUNKS / BLK];
+    __shared__ float cs[BLK];
+    __shared__ float ev[CH];
+    __shared__ int s_bidx, s_cidx, s_tok;
+    __shared__ float s_P, s_Q;
+    // the row's block sums, requested together
+    for (int b = t; b < a.nblocks; b += blockDim.x)
+        sbs[b] = walk_resid ? a.rbs[b] : a.bsum[(size_t)row * a.nblocks + b];
     __syncthreads();
-    if (t == 0) {
-        int fr = D;
-        for (int i = 0; i < D; ++i) {
-            const int d = a.draft[i];
-            const float mxs = a.rowmax[i] * a.invT;
-            const float p = (d >= 0 && d < a.V) ? __fdiv_rn(e_at(a, i, d, mxs), Z[i]) : 0.0f;
-            float q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[i] : 1.0f);
-            q = fmaxf(0.0f, q);
-            float u0, u1;
-            row_uniforms(a, i, u0, u1);
-            if (q > 0.0f && p > 0.0f && u0 <= fminf(1.0f, __fdiv_rn(p, q))) continue;
-            fr = i;
-            break;
-        }
-        s_fr = fr;
-    }
-    __syncthreads();
-    const int fr = s_fr;
-    // which mass is walked: residual of row fr (mode 1), or e of row fr / D (mode 0)
-    int row = fr, walk_resid = 0, d = -1;
-    float q = 0.0f;
-    const float mxs = a.rowmax[row] * a.invT;
-    float tgt = 0.0f;
-    if (fr < D) {
-        d = a.draft[fr];
-        q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[fr] : 1.0f);
-        q = fmaxf(0.0f, q);
-        for (int c = t; c < nch; c += 1024) {
-            float s = 0.0f;
-            const int e = min(c * CH + CH, a.V);
-            for (int v = c * CH; v < e; ++v) s = s + r_at(a, row, v, mxs, Z[row], q, d);
-            cs[c] = s;
-        }
-        __syncthreads();
-        for (int b = t; b < a.nblocks; b += 1024) {
-            float s = 0.0f;
-            for (int c = b * BLK; c < min(b * BLK + BLK, nch); ++c) s = s + cs[c];
-            bs[b] = s;
-        }
-        __syncthreads();
-        if (t == 0) {
-            float S = 0.0f;
-            for (int b = 0; b < a.nblocks; ++b) S = S + bs[b];
-            float u0, u1;
-            row_uniforms(a, row, u0, u1);
-            s_t = S > 0.0f ? u1 * S : u1 * Z[row];
-            s_blk = S > 0.0f ? 1 : 0;
-        }
-        __syncthreads();
-        walk_resid = s_blk;
-        tgt = s_t;
-    } else {
-        if (t == 0) {
-            float u0, u1;
-            row_uniforms(a, row, u0, u1);
-            s_t = u0 * Z[row];
-        }
-        __syncthreads();
-        tgt = s_t;
-    }
-    // samplePrepared with a nucleus: the bonus, or a residual without mass
-    if (nucleus_on(a) && (fr == D || !walk_resid)) {
-        if (t == 0) {
-            float u0, u1;
-            row_uniforms(a, row, u0, u1);
-            *a.nb.st = NucState{1, row, fr, fr == D ? u0 : u1, Z[row]};
-        }
-        return;  // block-uniform
-    }
-    if (t == 0 && a.nb.st) a.nb.st->need = 0;
-    // block level
     if (t == 0) {
         float P = 0.0f;
         int blk = -1;
         for (int b = 0; b < a.nblocks; ++b) {
-            const float bsv = walk_resid ? bs[b] : a.bsum[(size_t)row * a.nblocks + b];
-            const float Pn = P + bsv;
+            const float Pn = P + sbs[b];
             if (tgt <= Pn) {
                 blk = b;
                 break;
@@ -297,44 +238,183 @@ __global__ __launch_bounds__(1024) void k_sample_decide(SampleArgs a) {
     __syncthreads();
     const int blk = s_bidx;
     if (blk >= 0) {
-        // chunk sums of the chosen block (e-walk recomputes them; residual has them)
-        if (!walk_resid && t < BLK) {
+        if (t < BLK) {
             const int c = blk * BLK + t;
-            float s = 0.0f;
+            float sum = 0.0f;
             if (c < nch) {
                 const int e = min(c * CH + CH, a.V);
-                for (int v = c * CH; v < e; ++v) s = s + e_at(a, row, v, mxs);
+                for (int v = c * CH; v < e; ++v)
+                    sum = sum + (walk_resid ? r_at(a, row, v, mxs, Zr, q, d) : e_at(a, row, v, mxs));
             }
-            cs[c < MAX_CHUNKS ? c : 0] = s;
+            cs[t] = sum;
         }
         __syncthreads();
         if (t == 0) {
             const int c0 = blk * BLK, c1 = min(c0 + BLK, nch);
             float Q = s_P;
-            int tok = min(c1 * CH, a.V) - 1;
+            int cc = -1;
             for (int c = c0; c < c1; ++c) {
-                const float Qn = Q + cs[c];
+                const float Qn = Q + cs[c - c0];
                 if (tgt <= Qn) {
-                    float R = Q;
-                    const int e = min(c * CH + CH, a.V);
-                    tok = e - 1;
-                    for (int v = c * CH; v < e; ++v) {
-                        R = R + (walk_resid ? r_at(a, row, v, mxs, Z[row], q, d)
-                                            : e_at(a, row, v, mxs));
-                        if (tgt <= R) {
-                            tok = v;
-                            break;
-                        }
-                    }
+                    cc = c;
                     break;
                 }
                 Q = Qn;
             }
-            s_tok = tok;
+            s_cidx = cc;
+            s_Q = Q;
+            if (cc < 0) s_tok = min(c1 * CH, a.V) - 1;
         }
         __syncthreads();
+        const int cc = s_cidx;
+        if (cc >= 0) {
+            // the chunk's element values, each computed once, then the running total in order
+            const int e = min(cc * CH + CH, a.V);
+            if (t < CH && cc * CH + t < e) {
+                const int v = cc * CH + t;
+                ev[t] = walk_resid ? r_at(a, row, v, mxs, Zr, q, d) : e_at(a, row, v, mxs);
+            }
+            __syncthreads();
+            if (t == 0) {
+                float R = s_Q;
+                int tok = e - 1;
+                for (int v = cc * CH; v < e; ++v) {
+                    R = R + ev[v - cc * CH];
+                    if (tgt <= R) {
+                        tok = v;
+                        break;
+                    }
+                }
+                s_tok = tok;
+            }
+            __syncthreads();
+        }
     }
     if (t == 0) write_result(a, fr, s_tok);
+}
+
+// Single block: row totals and the sequential accept decisions.  A full accept samples the bonus
+// here (or leaves it to the nucleus kernels); a reject hands row fr to k_resid_sums /
+// k_resid_walk through the state.
+__global__ __launch_bounds__(64) void k_sample_decide(SampleArgs a) {
+    if (aborted(a.abort)) return;
+    a = resolve(a);
+    const int t = threadIdx.x;
+    const int D = a.rows - 1;
+    __shared__ float Z[MJ_ROWS];
+    __shared__ float ed[MJ_ROWS];
+    __shared__ float sbs[DEC_STAGE];
+    __shared__ int s_fr;
+    // every row's block sums and the drafts' e values, requested together; then each row's
+    // total in block order
+    const int per = a.nblocks;
+    const int nst = min(a.rows * per, DEC_STAGE);
+    for (int idx = t; idx < nst; idx += blockDim.x) sbs[idx] = a.bsum[idx];
+    if (t < D) {
+        const int d = a.draft[t];
+        ed[t] = (d >= 0 && d < a.V) ? e_at(a, t, d, a.rowmax[t] * a.invT) : 0.0f;
+    }
+    __syncthreads();
+    if (t < a.rows) {
+        float z = 0.0f;
+        for (int b = 0; b < per; ++b) {
+            const int idx = t * per + b;
+            z = z + (idx < DEC_STAGE ? sbs[idx] : a.bsum[idx]);
+        }
+        Z[t] = z;
+    }
+    __syncthreads();
+    if (t == 0) {
+        int fr = D;
+        for (int i = 0; i < D; ++i) {
+            const int d = a.draft[i];
+            const float p = (d >= 0 && d < a.V) ? __fdiv_rn(ed[i], Z[i]) : 0.0f;
+            float q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[i] : 1.0f);
+            q = fmaxf(0.0f, q);
+            float u0, u1;
+            row_uniforms(a, i, u0, u1);
+            if (q > 0.0f && p > 0.0f && u0 <= fminf(1.0f, __fdiv_rn(p, q))) continue;
+            fr = i;
+            break;
+        }
+        s_fr = fr;
+        if (fr < D) {
+            float q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[fr] : 1.0f);
+            *a.state = SampleState{1, fr, a.draft[fr], 0, fmaxf(0.0f, q), Z[fr], 0.0f, 0.0f};
+        } else {
+            *a.state = SampleState{0, fr, -1, 0, 0.0f, Z[fr], 0.0f, 0.0f};
+        }
+    }
+    __syncthreads();
+    const int fr = s_fr;
+    if (fr < D) return;  // the residual kernels finish (block-uniform)
+    // the bonus: sample the last row by a walk to u0 * Z over e (samplePrepared)
+    float u0, u1;
+    row_uniforms(a, fr, u0, u1);
+    if (nucleus_on(a)) {
+        if (t == 0) *a.nb.st = NucState{1, fr, fr, u0, Z[fr]};
+        return;  // block-uniform
+    }
+    if (t == 0 && a.nb.st) a.nb.st->need = 0;
+    walk_write(a, fr, fr, false, u0 * Z[fr], a.rowmax[fr] * a.invT, Z[fr], 0.0f, -1);
+}
+
+// Residual block sums of the rejected row (same chunk / block order as the e sums): one 64-thread
+// block per 1024-element block, lane = chunk.
+__global__ __launch_bounds__(64) void k_resid_sums(SampleArgs a) {
+    if (aborted(a.abort)) return;
+    a = resolve(a);
+    const SampleState st = *a.state;
+    if (st.phase != 1) return;
+    const int b = blockIdx.x, lane = threadIdx.x;
+    const int nch = (a.V + CH - 1) / CH;
+    const int chunk = b * BLK + lane;
+    const float mxs = a.rowmax[st.fr] * a.invT;
+    float cs = 0.0f;
+    if (chunk < nch) {
+        const int e = min(chunk * CH + CH, a.V);
+        for (int v = chunk * CH; v < e; ++v) cs = cs + r_at(a, st.fr, v, mxs, st.Zr, st.q, st.d);
+    }
+    __shared__ float sc[BLK];
+    sc[lane] = cs;
+    __syncthreads();
+    if (lane == 0) {
+        float bs = 0.0f;
+        for (int c = 0; c < BLK; ++c)
+            if (b * BLK + c < nch) bs = bs + sc[c];
+        a.rbs[b] = bs;
+    }
+}
+
+// The rejected row's sample: the residual total S, then a walk to u1 * S over the residual, or,
+// with no residual mass, samplePrepared of the row (nucleus kernels, or a walk to u1 * Z over e).
+__global__ __launch_bounds__(64) void k_resid_walk(SampleArgs a) {
+    if (aborted(a.abort)) return;
+    a = resolve(a);
+    const SampleState st = *a.state;
+    if (st.phase != 1) return;
+    const int t = threadIdx.x;
+    __shared__ float s_S;
+    __shared__ float srb[MAX_CHUNKS / BLK];
+    for (int b = t; b < a.nblocks; b += blockDim.x) srb[b] = a.rbs[b];
+    __syncthreads();
+    if (t == 0) {
+        float S = 0.0f;
+        for (int b = 0; b < a.nblocks; ++b) S = S + srb[b];
+        s_S = S;
+    }
+    __syncthreads();
+    const float S = s_S;
+    float u0, u1;
+    row_uniforms(a, st.fr, u0, u1);
+    const bool walk_resid = S > 0.0f;
+    if (nucleus_on(a) && !walk_resid) {
+        if (t == 0) *a.nb.st = NucState{1, st.fr, st.fr, u1, st.Zr};
+        return;  // block-uniform
+    }
+    if (t == 0 && a.nb.st) a.nb.st->need = 0;
+    walk_write(a, st.fr, st.fr, walk_resid, walk_resid ? u1 * S : u1 * st.Zr,
+               a.rowmax[st.fr] * a.invT, st.Zr, st.q, st.d);
 }
 
 // ---- nucleus (samplePrepared, LogitsProcessor.swift:137-164) --------------------------------
@@ -493,8 +573,13 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
     a.seed = seed;
     a.counter = counter;
     a.rowmax = rowmax;
-    a.bsum = bsum;
     a.nblocks = ((V + CH - 1) / CH + BLK - 1) / BLK;
+    // the bsum buffer (sample_scratch_floats, 16-byte aligned): the hand-off state, block sums,
+    // partial maxima, residual block sums
+    a.state = (SampleState*)bsum;
+    a.bsum = bsum + 8;
+    a.mpart = a.bsum + (size_t)rows * a.nblocks;
+    a.rbs = a.mpart + (size_t)rows * RMB;
     a.out = out;
     a.res = res;
     a.abort = abort;
@@ -504,13 +589,19 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
     hipLaunchKernelGGL(k_penalize, dim3(rows), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_rowmax, dim3(rows), dim3(1024), 0, st, a);
+    hipLaunchKernelGGL(k_rowmax, dim3(rows * RMB), dim3(256), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_sample_sums, dim3(rows * a.nblocks), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_sample_decide, dim3(1), dim3(1024), 0, st, a);
+    hipLaunchKernelGGL(k_sample_decide, dim3(1), dim3(64), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_resid_sums, dim3(a.nblocks), dim3(64), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_resid_walk, dim3(1), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess || !nb) return e;
     hipLaunchKernelGGL(k_nucleus_keys, dim3((V + 255) / 256), dim3(256), 0, st, a);
@@ -525,3 +616,10 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
 }
 
 int sample_nblocks(int V) { return ((V + CH - 1) / CH + BLK - 1) / BLK; }
+
+// floats of the buffer passed as bsum: 8 for the state, rows x nblocks block sums, rows x RMB
+// partial maxima, nblocks residual block sums
+size_t sample_scratch_floats(int rows, int V) {
+    const size_t nb = (size_t)sample_nblocks(V);
+    return 8 + (size_t)rows * nb + (size_t)rows * RMB + nb;
+}

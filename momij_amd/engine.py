@@ -216,7 +216,8 @@ class VerifyEngine:
     def verify_sampled_ex(self, y: int, draft, q_mode: int, seed: int, counter: int,
                           temperature: float, top_p=1.0, rep=1.0, pres=0.0, freq=0.0,
                           hist=None, q_point=None) -> tuple[int, int]:
-        """mj_verify_sampled_ex: LogitsProcessor options; hist {token: count}."""
+        """mj_verify_sampled_ex: LogitsProcessor options; hist {token: count} or a pair of
+        int32 arrays (tokens, counts)."""
         n = len(draft)
         d = (C.c_int32 * max(n, 1))(*[int(t) for t in draft])
         qp = None if q_point is None else (C.c_float * max(n, 1))(*[float(q) for q in q_point])

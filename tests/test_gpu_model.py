@@ -322,9 +322,10 @@ def test_sampled_verify_ex_bit_exact(model, orc, q_mode):
         ref = orc.accept_sampled_ex(lg, np.array(draft, np.int32), 0.7, q_mode, u,
                                     hist_tok=ht, hist_cnt=hc, **o)
         assert (acc, tok) == ref, (trial, o, acc, tok, ref)
-        for _ in range(2):  # graph replays
+        order = np.argsort(ht)
+        for hh in (hist, (ht[order], hc[order])):  # graph replays: dict, then sorted arrays
             eng.rewind(L0)
-            assert eng.verify_sampled_ex(y, draft, q_mode, 123, trial, 0.7, hist=hist,
+            assert eng.verify_sampled_ex(y, draft, q_mode, 123, trial, 0.7, hist=hh,
                                          **o) == (acc, tok)
 
 
