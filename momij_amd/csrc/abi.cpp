@@ -403,6 +403,9 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
     // One row takes it too, so a row's result does not depend on how many rows share its pass
     // (a verify row equals the one-row decode step at its position, bit for bit).
     const bool tile = fused && M >= 1 && M <= MJ_MAX_ROWS && up_tile && dn_tile;
+    // up to 16 rows over at most 64 experts: the up || gate product ranks the logits itself
+    // (its blocks build the slot records in LDS), one launch fewer
+    const bool topk_in_up = tile && E <= 64 && M <= MJ_G5_FUSED_ROWS;
     if (fused) {
         RouteArgs ra{};
         ra.x = x;
@@ -425,8 +428,10 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.abort = ab;
         s = mj_hip(ctx, launch_route_logits(ra, H, st), "route");
         if (s != MJ_OK) return s;
-        s = mj_hip(ctx, launch_route_topk(ra, st), "route top-k");
-        if (s != MJ_OK) return s;
+        if (!topk_in_up) {
+            s = mj_hip(ctx, launch_route_topk(ra, st), "route top-k");
+            if (s != MJ_OK) return s;
+        }
         if (M == 1 && !tile && (flags & MJ_MOE_PRENORM)) xn = ms.xn;
     }
     if (M == 1 && !tile) {
@@ -513,6 +518,15 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         up.gs = w->gs;
         up.x_div = k;
         up.abort = ab;
+        if (topk_in_up) {
+            up.rlogits = ms.logits;
+            up.rM = M;
+            up.rE = E;
+            up.rk = k;
+            up.rinds = inds;
+            up.rscores = scores;
+            up.rsrec = ms.srec;
+        }
         if (prof) prof->begin(PROF_UP, st);
         s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, tile ? E : nb, st), "up gather");
         if (prof) prof->end(st);
@@ -524,6 +538,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
             if (s != MJ_OK) return s;
         }
         GatherArgs dn = up;
+        dn.rlogits = nullptr;  // the down product reads the records the up product wrote
         dn.xperm = ms.act;
         dn.xsum = dn_tile ? nullptr : ms.act_sum;
         dn.w = w->down_w;

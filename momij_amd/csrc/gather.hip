@@ -20,6 +20,7 @@
 
 #include "mj_device.h"
 #include "mj_internal.h"
+#include "moe_topk.h"
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -114,6 +115,9 @@ __device__ __forceinline__ void lds_only_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// static LDS of the fused routing's slot records (persistent up || gate kernels)
+constexpr size_t G5_FUSED_REC_BYTES = 64 * MJ_G5_FUSED_ROWS;
+
 template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false>
 // four waves per SIMD: two 8-wave blocks (or one 16-wave block) per CU
 __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gather5(
@@ -146,10 +150,127 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     int e = 0, np = a.dense_rows;
     int item = blockIdx.x;
     int rec_n = 0;  // the next item's record (persistent mode)
+    extern __shared__ __align__(16) char g5lds[];
+
+    // Fused routing (persistent up || gate product, rlogits set): every block ranks the router
+    // logits itself -- the same top-k as the route kernel (row_topk) -- and keeps, per expert
+    // t in lane t, the rows that picked it (em: bit r) and t's rank in each of them (er: 3 bits
+    // a row).  A slot's record follows from these in registers: slots number the routed experts
+    // in increasing id (as the route kernel's), a record lists its pairs (row * k + rank) by
+    // row.  The last block also writes inds / scores and the global records for the down
+    // product.
+    struct FusedRoute {
+        // rank of expert t in row r, 0xFF where r did not pick t (rows of one expert in one
+        // 16-byte read)
+        uint8_t rank[64][MJ_G5_FUSED_ROWS];
+    };
+    constexpr bool FUSABLE = PER && EPI == EPI_SWIGLU;
+    __shared__ __align__(16) std::conditional_t<FUSABLE, FusedRoute, char> s_fr;
+    const bool fused = FUSABLE && a.rlogits != nullptr;
+    uint32_t em = 0;
+    uint64_t er = 0;
+    // record of slot sl in the global records' form: pair j in lane j, expert id and pair count
+    // in the high halves of lanes 0 and 1 (count 0 past the last routed expert)
+    auto fused_rec = [&](int sl) -> int {
+        const uint64_t on = __ballot(em != 0u);
+        const int mys = __popcll(on & ((1ull << lane) - 1ull));
+        const uint64_t hit = __ballot(em != 0u && mys == sl);
+        if (hit == 0) return 0;
+        const int ex = __builtin_ctzll(hit);
+        const uint32_t rm = __builtin_amdgcn_readlane(em, ex);
+        const uint64_t rx = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(er >> 32), ex) << 32) |
+                            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)er, ex);
+        // lane r < 16 (row r) sends its pair to lane "rows of ex before r"; the lanes that
+        // send nothing send to lane 63, which no record entry uses (at most 16 pairs)
+        const int r16 = lane & 15;
+        const bool mine = lane < 16 && ((rm >> r16) & 1u);
+        const int pos = __popc(rm & ((1u << r16) - 1u));
+        const int pr = r16 * a.rk + (int)((rx >> (3 * r16)) & 7u);
+        const int got = __builtin_amdgcn_ds_permute((mine ? pos : 63) * 4, pr);
+        return got | (lane == 0 ? ex << 16 : lane == 1 ? __popc(rm) << 16 : 0);
+    };
+    if constexpr (FUSABLE) {
+        static_assert(sizeof(FusedRoute) == G5_FUSED_REC_BYTES, "record bytes");
+        static_assert(MJ_G5_FUSED_ROWS <= 2 * WPB && MJ_G5_FUSED_ROWS <= 16, "two rows a wave");
+        if (fused) {
+            const int M = a.rM, E = a.rE, k = a.rk;
+            // row scratch in the weight tile area, free until the first item's loads
+            float* s_row = (float*)g5lds + 64 * wv;                  // [WPB][64]
+            float* s_gate = (float*)(g5lds + 256 * WPB) + 8 * wv;    // [WPB][8]
+            int* s_ind = (int*)(g5lds + 288 * WPB) + 8 * wv;         // [WPB][8]
+            // both rows' logits (clamped row and expert: no branch waits) and the abort flag
+            // requested together
+            float v[2];
+#pragma unroll
+            for (int sr = 0; sr < 2; ++sr)
+                v[sr] = a.rlogits[min(wv + WPB * sr, M - 1) * E + min(lane, E - 1)];
+            if (aborted(a.abort)) return;
+            const bool wr = blockIdx.x == gridDim.x - 1;  // writes inds / scores / records
+#pragma unroll
+            for (int sr = 0; sr < 2; ++sr) {
+                const int r = wv + WPB * sr;
+                if (r >= M) break;
+                s_row[lane] = lane < E ? v[sr] + 0.0f : -INFINITY;
+                __builtin_amdgcn_wave_barrier();
+                if (wr) {  // the selection with its weights
+                    int ind = 0;
+                    float gate = 0.0f;
+                    s_fr.rank[lane][r] = 0xFF;
+                    row_topk<1>(s_row, E, k, s_ind, s_gate, ind, gate);
+                    if (lane < k) {  // (in order after the 0xFF above: one wave's LDS writes)
+                        s_fr.rank[ind][r] = (uint8_t)lane;
+                        a.rinds[r * k + lane] = ind;
+                        a.rscores[r * k + lane] = gate;
+                    }
+                } else {  // the selection only: the ranks of row_topk, no weights
+                    const int rank = row_rank64(s_row, E);
+                    s_fr.rank[lane][r] = lane < E && rank < k ? (uint8_t)rank : (uint8_t)0xFF;
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+            __syncthreads();
+            // lane t: the rows that picked expert t, and its rank in each (bytes of rows >= M
+            // were never written)
+            static_assert(MJ_G5_FUSED_ROWS == 16, "one 16-byte read an expert");
+            const u4v rb = *(const u4v*)s_fr.rank[lane];
+#pragma unroll
+            for (int r = 0; r < MJ_G5_FUSED_ROWS; ++r) {
+                const uint32_t b = (rb[r >> 2] >> (8 * (r & 3))) & 0xFFu;
+                if (r < M && b != 0xFFu) {
+                    em |= 1u << r;
+                    er |= (uint64_t)(b & 7u) << (3 * r);
+                }
+            }
+            if (wr && wv == 0) {
+                const uint64_t on = __ballot(em != 0u);
+                const int total = __popcll(on);
+                if (em != 0u) {
+                    int* gr = a.rsrec + __popcll(on & ((1ull << lane) - 1ull)) * MJ_ROWS;
+                    const int cnt = __popc(em);
+                    int c = 0;
+#pragma unroll
+                    for (int r = 0; r < MJ_G5_FUSED_ROWS; ++r) {
+                        if ((em >> r) & 1u) {
+                            gr[c] = (r * k + (int)((er >> (3 * r)) & 7u)) |
+                                    (c == 0 ? lane << 16 : c == 1 ? cnt << 16 : 0);
+                            ++c;
+                        }
+                    }
+                    if (cnt == 1) gr[1] = 1 << 16;
+                }
+                if (lane >= total) {  // slots past the last routed expert: count 0
+                    a.rsrec[lane * MJ_ROWS] = 0;
+                    a.rsrec[lane * MJ_ROWS + 1] = 0;
+                }
+            }
+            // the row scratch is free for the weight tiles: every wave is past the barrier above
+        }
+    }
     {
-        const int ab = a.abort ? *a.abort : 0;
+        const int ab = !fused && a.abort ? *a.abort : 0;  // fused: checked with the logits
         if constexpr (PER) {
-            const int rec = a.srec[min(item / ncb, 63) * MJ_ROWS + lane];
+            const int rec = fused ? fused_rec(min(item / ncb, 63))
+                                  : a.srec[min(item / ncb, 63) * MJ_ROWS + lane];
             e = __builtin_amdgcn_readlane(rec, 0) >> 16;
             np = item / ncb < 64 ? __builtin_amdgcn_readlane(rec, 1) >> 16 : 0;
             lpair = rec & 0xFFFF;
@@ -169,7 +290,6 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         if (ab || np <= 0) return;  // whole block
     }
 
-    extern __shared__ __align__(16) char g5lds[];
     char* wreg = g5lds + (size_t)wv * S::WAVE_BYTES;      // this wave's weight tile
     char* wcode = wreg;
     uint16_t* wsc = (uint16_t*)(wreg + S::WCODE);          // [16][K/GS/KS] this K-slice
@@ -304,11 +424,16 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
             lds_barrier<G + NSB>();
         }
         // persistent mode: the next item's record, fetched behind this item's weights (one
-        // vector load younger than them: PF)
+        // vector load younger than them: PF).  With fused routing the record is formed from
+        // registers once the weights have landed; the load is then a stand-in that keeps the
+        // queue's count, and its value is consumed (times zero) so that it stays
         constexpr int PF = PER ? 1 : 0;
         if constexpr (PER) {
-            if (pb == 0)
-                rec_n = a.srec[min((item + (int)gridDim.x) / ncb, 63) * MJ_ROWS + lane];
+            if (pb == 0) {
+                const int* rp = fused ? (const int*)a.rlogits
+                                      : a.srec + min((item + (int)gridDim.x) / ncb, 63) * MJ_ROWS + lane;
+                rec_n = *rp;
+            }
         }
         wait_vmcnt<G + PF>();      // scales and biases have landed
         u4v sv[SCW], bv[SCW];
@@ -439,6 +564,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         int np_next = 0;
         if constexpr (PER) {
             const int nx = item + (int)gridDim.x;
+            if (fused) rec_n = fused_rec(min(nx / ncb, 63)) | (rec_n & (int)opaque(0u));
             np_next = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
             stage_next = pb + RA >= np && nx / ncb < 64 && np_next > 0;
             if (stage_next) issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16, nx % ncb);
@@ -553,8 +679,11 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     const int want = rows < 1 ? 1 : rows;
     int RA = want < S::R ? want : S::R;
     const bool expert = a.ecnt != nullptr || a.srec != nullptr;
+    // two blocks a CU for the expert products; static LDS: the pair lists (128 bytes) and, in
+    // the persistent up || gate kernels, the fused routing's records
+    const size_t stat = 256 + (PER && EPI == EPI_SWIGLU ? G5_FUSED_REC_BYTES : 0);
     const size_t limit =
-        (EPI == EPI_SWIGLU || EPI == EPI_STORE) && expert ? 80 * 1024 - 256 : G5_LDS_MAX;
+        (EPI == EPI_SWIGLU || EPI == EPI_STORE) && expert ? 80 * 1024 - stat : G5_LDS_MAX;
     while (RA > 1 && S::lds(RA, want > RA || PER) > limit) --RA;
     const bool multi = want > RA;
     int grid = n_buckets * ncb;
@@ -583,6 +712,12 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
     // expert products over routed-expert slot records (at most 64 experts): persistent
     const bool per = a.srec != nullptr;
     if (per && (n_buckets > 64 || (epi != EPI_SWIGLU && epi != EPI_STORE)))
+        return hipErrorInvalidValue;
+    // fused routing: the up || gate product ranks the router logits itself
+    if (a.rlogits != nullptr &&
+        (!per || epi != EPI_SWIGLU || a.rM < 1 || a.rM > MJ_G5_FUSED_ROWS || a.rE < 1 ||
+         a.rE > 64 || a.rk < 1 || a.rk > 8 || a.rk > a.rE || a.x_div != a.rk ||
+         a.rinds == nullptr || a.rscores == nullptr || a.rsrec == nullptr))
         return hipErrorInvalidValue;
     // row-alpha expert weights (scale alpha, bias -alpha in every group of a row): the
     // fold kernels read one alpha per row instead of the group scales and biases

@@ -110,7 +110,16 @@ struct GatherArgs {
     int K, N, gs;
     int x_div;              // x row of pair p = p / x_div
     const int* abort;
+    // persistent expert mode with fused routing (rlogits set, at most MJ_G5_FUSED_ROWS rows,
+    // E <= 64): every block ranks the router logits [rM][rE] itself and builds the slot records
+    // in LDS; block 0 writes inds / scores [rM][rk] and the records (rsrec) for the next product
+    const float* rlogits;
+    int rM, rE, rk;
+    int32_t* rinds;
+    float* rscores;
+    int* rsrec;
 };
+#define MJ_G5_FUSED_ROWS 16
 
 struct QmvArgs {
     const uint16_t* x;      // plain fp16 [rows_x][K]

@@ -110,10 +110,12 @@ def _moe_dev(mw):
     return d
 
 
-@pytest.mark.parametrize("M,flags", [(1, 0), (8, 0), (8, 3), (1, 3), (17, 3)])
+@pytest.mark.parametrize("M,flags", [(1, 0), (8, 0), (8, 3), (1, 3), (9, 3), (16, 3), (17, 3)])
 def test_moe_block(ctx, orc, M, flags):
     """Config 1 (M=1) and the K=8 verify rows of config 2 (M=8), and the pre-norm+residual form
-    used inside a layer: routing bit-exact, outputs within tolerance."""
+    used inside a layer: routing bit-exact, outputs within tolerance.  Up to 16 rows the up ||
+    gate product ranks the router logits itself (M = 16: two rows on every wave); 17 rows take
+    the separate top-k launch."""
     import torch
 
     print(f"case: moe M={M} flags={flags}", flush=True)
