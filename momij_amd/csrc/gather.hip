@@ -308,11 +308,26 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
 
     // ---- activation rows of a pass, straight into LDS: rows < npass only (the rest feed
     // MFMA output rows that are discarded).  Wave w stages rows w, w + WPB, ...
-    auto stage_load = [&](int pb, int npass, int b, int lp, int npp) {
+    // residual add over dense rows: the first pass's residual values (rows 4q .. 4q + 3 of
+    // output column n) are requested with the first rows, ahead of the weight stream, so the
+    // epilogue does not wait on a dependent load (older than the weights, they change no wait
+    // count)
+    constexpr bool RES_PF = EPI == EPI_ADD && !PER;
+    const bool res_pf = RES_PF && a.ecnt == nullptr && a.bk == nullptr && kh == 0;
+    uint32_t resv[4] = {0u, 0u, 0u, 0u};
+    auto stage_load = [&](int pb, int npass, int b, int lp, int npp, bool first = false) {
         uint16_t* xs = xs_of(b);
         float2* xsl = xsl_of(b);
         const int myr = min(pb + (lane < R ? lane : 0), npp - 1);
         const int prl = (PER || a.ecnt) ? __shfl(lp, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
+        if constexpr (RES_PF) {
+            // (after the pair list: the wait for a list load would cover these too)
+            if (first && res_pf) {
+                const int col = (cb * TPB + tt) * 16 + n;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) resv[r] = a.y[(size_t)min(4 * q + r, npass - 1) * a.N + col];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < R / WPB; ++j) {
             const int r = wv + WPB * j;
@@ -403,7 +418,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
   for (;;) {
     const int npass0 = min(RA, np);
     if (!early) {
-        stage_load(0, npass0, buf, lpair, np);  // ahead of the weights (loads return in order)
+        stage_load(0, npass0, buf, lpair, np, true);  // ahead of the weights (loads return in order)
         issue_weights(e, cb);
     }
     const UnpackK uk = {opaque(0x00C000C0u), opaque(0x03000300u), opaque(0x4C004C00u),
@@ -625,10 +640,12 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
                 const int i = 4 * q + r;
                 if (kh == 0 && i < npass) {
                     uint16_t* yp = a.y + (size_t)s_pair[buf][i] * a.N + col;
-                    if constexpr (EPI == EPI_ADD)
-                        *yp = f2h(h2f(*yp) + hround(acc[r]));
-                    else
+                    if constexpr (EPI == EPI_ADD) {
+                        const uint16_t res = res_pf && pb == 0 ? (uint16_t)resv[r] : *yp;
+                        *yp = f2h(h2f(res) + hround(acc[r]));
+                    } else {
                         *yp = f2h(acc[r]);
+                    }
                 }
             }
         }

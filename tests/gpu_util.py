@@ -33,5 +33,11 @@ def close_report(got, ref):
 def assert_close(got, ref, rel_tol=REL_NORM_TOL, abs_tol=ABS_TOL, what=""):
     rel, mx = close_report(got, ref)
     print(f"[{what}] rel_norm={rel:.3e} max_abs={mx:.3e}", flush=True)
+    if not (rel <= rel_tol and mx <= abs_tol) and np.ndim(got) == 2:
+        # which rows and columns are off, to tell a wrong row from scattered noise
+        d = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+        bad = d > abs_tol
+        print(f"[{what}] rows off: {np.nonzero(bad.any(axis=1))[0].tolist()}; columns off per "
+              f"row: {bad.sum(axis=1).tolist()}", flush=True)
     assert rel <= rel_tol and mx <= abs_tol, (what, rel, mx)
     return rel, mx
