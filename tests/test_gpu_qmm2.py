@@ -137,6 +137,37 @@ def test_moe_block(ctx, orc, M, flags):
     assert rel < 5e-3
 
 
+@pytest.mark.parametrize("M", [1, 9, 16])
+def test_moe_fused_routing_equals_separate_topk(ctx, M):
+    """Passes of at most 16 rows rank the router logits in the up gather's prologue (every block
+    builds the slot records in LDS); 17 rows take the separate top-k launch.  A row's routing
+    and output do not depend on the other rows of its pass, so an M-row pass equals the first M
+    rows of a 17-row pass bit for bit: expert ids, weights and outputs."""
+    import torch
+
+    print(f"case: moe fused routing M={M} vs 17 rows", flush=True)
+    rng = np.random.default_rng(500 + M)
+    E, H, I, gs, k = 64, 2048, 1024, 64, 8
+    mw = _moe_data(rng, E, H, I, gs)
+    dmw = _moe_dev(mw)
+    x = synth.normal_f16(rng, (17, H))
+
+    def run(rows):
+        dx = dev(np.ascontiguousarray(x[:rows]))
+        y = torch.empty_like(dx)
+        inds = torch.empty((rows, k), dtype=torch.int32, device="cuda")
+        scores = torch.empty((rows, k), dtype=torch.float32, device="cuda")
+        _run(ctx, lambda: ctx.moe_block(dmw, dx, y, rows, 3, inds, scores))
+        return host(y), host(inds), host(scores)
+
+    y17, i17, s17 = run(17)
+    ym, im, sm = run(M)
+    assert (im == i17[:M]).all()
+    assert (sm.view(np.uint32) == s17[:M].view(np.uint32)).all()
+    diff = ym.view(np.uint16) != y17[:M].view(np.uint16)
+    assert not diff.any(), f"rows differing: {np.nonzero(diff.any(axis=1))[0].tolist()}"
+
+
 def _row_alpha(mw):
     """Row-alpha form of the expert weights (WeightStore.swift:47-63): alpha = the row's first
     group scale, scales = alpha in every group, biases = -alpha."""
