@@ -398,7 +398,10 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
             if (vcls[j] >= 0)
                 *(u4v*)(a.vc + ((size_t)g * a.C + slot_of(L + vcls[j])) * HD + 8 * vd) = vv[j];
     }
-    __syncthreads();
+    // LDS-only barrier: the K / V appends above are read by later launches, not by this block
+    // (it holds the finished keys in LDS), so they complete behind the attention work instead of
+    // before it (__syncthreads would wait for the stores too)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     const float sc2 = a.scale * LOG2E;
     const int ln = lane & 15, lq = lane >> 4;
