@@ -226,7 +226,10 @@ __device__ __forceinline__ float u01(uint32_t x) { return (float)(x >> 8) * 0x1p
 // packed fp16 in hv), as k_rmsnorm_qx: out = half(x * (1 / sqrt(mean x^2 + eps)) * w), written
 // plain and / or in qx order with its block sums (NormOut).  Every thread of the block must
 // call it.
-__device__ __forceinline__ void norm_row_2048(const u4v hv, const NormOut& no, int row) {
+// RMSNorm of a 2048-wide row held as 8 halves a thread (256 threads), weights wv of this
+// thread's 8 dims already loaded; writes the plain and / or qx-ordered output
+__device__ __forceinline__ void norm_row_2048_w(const u4v hv, const u4v wv, const NormOut& no,
+                                                int row) {
     const int t = threadIdx.x, lane = t & 63;
     float ss = 0.0f;
 #pragma unroll
@@ -241,7 +244,6 @@ __device__ __forceinline__ void norm_row_2048(const u4v hv, const NormOut& no, i
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float inv = 1.0f / sqrtf(tot / 2048.0f + no.eps);
-    const u4v wv = *(const u4v*)(no.w + 8 * t);
     u4v o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -251,4 +253,7 @@ __device__ __forceinline__ void norm_row_2048(const u4v hv, const NormOut& no, i
     }
     if (no.plain) *(u4v*)(no.plain + (size_t)row * 2048 + 8 * t) = o;
     if (no.xperm) emit_qx(o, lane, no.xperm + (size_t)row * 2048, no.xsum + (size_t)row * 32, 8 * t);
+}
+__device__ __forceinline__ void norm_row_2048(const u4v hv, const NormOut& no, int row) {
+    norm_row_2048_w(hv, *(const u4v*)(no.w + 8 * threadIdx.x), no, row);
 }

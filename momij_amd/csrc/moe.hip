@@ -242,9 +242,58 @@ __global__ __launch_bounds__(256) void k_score_combine(const uint16_t* __restric
         y[i] = f2h(acc);
 }
 
+// The same combine, 8 elements a thread (H % 8 == 0, k <= 8) with every load issued before
+// the first wait: one memory round trip instead of one per expert.
+__global__ __launch_bounds__(256) void k_score_combine8(const uint16_t* __restrict__ down,
+                                                        const float* __restrict__ scores,
+                                                        const uint16_t* x_resid, uint16_t* y,
+                                                        int M, int k, int H, const int* abort) {
+    const int i = 8 * (blockIdx.x * 256 + threadIdx.x);
+    if (i >= M * H) return;
+    const int m = i / H, c = i % H;
+    u4v d[8];
+    float sc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int jj = min(j, k - 1);
+        d[j] = *(const u4v*)(down + ((size_t)m * k + jj) * H + c);
+        sc[j] = scores[m * k + jj];
+    }
+    const u4v xr = *(const u4v*)((x_resid ? x_resid : down) + (size_t)i);
+    if (aborted(abort)) return;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if (j < k) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[2 * q] += h2f(d[j][q] & 0xFFFFu) * sc[j];
+                acc[2 * q + 1] += h2f(d[j][q] >> 16) * sc[j];
+            }
+        }
+    }
+    u4v o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (x_resid)
+            o[q] = (uint32_t)f2h(h2f(xr[q] & 0xFFFFu) + hround(acc[2 * q])) |
+                   ((uint32_t)f2h(h2f(xr[q] >> 16) + hround(acc[2 * q + 1])) << 16);
+        else
+            o[q] = (uint32_t)f2h(acc[2 * q]) | ((uint32_t)f2h(acc[2 * q + 1]) << 16);
+    }
+    *(u4v*)(y + (size_t)i) = o;
+}
+
 hipError_t launch_score_combine(const uint16_t* down, const float* scores, const uint16_t* x_resid,
                                 uint16_t* y, int M, int k, int H, const int* abort,
                                 hipStream_t st) {
+    if (H % 8 == 0 && k >= 1 && k <= 8) {
+        hipLaunchKernelGGL(k_score_combine8, dim3((M * H / 8 + 255) / 256), dim3(256), 0, st, down,
+                           scores, x_resid, y, M, k, H, abort);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_score_combine, dim3((M * H + 255) / 256), dim3(256), 0, st, down, scores,
                        x_resid, y, M, k, H, abort);
     return hipGetLastError();
@@ -252,29 +301,43 @@ hipError_t launch_score_combine(const uint16_t* down, const float* scores, const
 
 // The expert combine of one row followed by the next RMSNorm (of the next layer's attention,
 // or the final norm), H = 2048: one 256-thread block per row, thread t owns elements
-// 8t .. 8t+7.  The combine is k_score_combine's arithmetic, the norm k_rmsnorm_qx's.
+// 8t .. 8t+7.  The combine is k_score_combine's arithmetic, the norm k_rmsnorm_qx's.  Every
+// load is issued before the first wait (the k <= 8 expert rows at clamped indices, their
+// weights, the residual, the norm weights and the abort word): one memory round trip, not one
+// per expert.
 __global__ __launch_bounds__(256) void k_combine_norm(const uint16_t* __restrict__ down,
                                                       const float* __restrict__ scores,
                                                       const uint16_t* x_resid, uint16_t* y, int k,
                                                       NormOut no, const int* abort) {
-    if (aborted(abort)) return;
     const int r = blockIdx.x, t = threadIdx.x;
     constexpr int H = 2048;
+    u4v d[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        d[j] = *(const u4v*)(down + ((size_t)r * k + min(j, k - 1)) * H + 8 * t);
+    // the weights as one vector load (lane j holds weight j), not eight scalar ones
+    const float scv = scores[r * k + min(t & 7, k - 1)];
+    const u4v xr = *(const u4v*)((x_resid ? x_resid : down) + (size_t)r * H + 8 * t);
+    const u4v wn = *(const u4v*)(no.w + 8 * t);
+    if (aborted(abort)) return;
+    float sc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sc[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scv), j));
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    for (int j = 0; j < k; ++j) {
-        const float sc = scores[r * k + j];
-        const u4v d = *(const u4v*)(down + ((size_t)r * k + j) * H + 8 * t);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            acc[2 * q] += h2f(d[q] & 0xFFFFu) * sc;
-            acc[2 * q + 1] += h2f(d[q] >> 16) * sc;
+    for (int j = 0; j < 8; ++j) {
+        if (j < k) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[2 * q] += h2f(d[j][q] & 0xFFFFu) * sc[j];
+                acc[2 * q + 1] += h2f(d[j][q] >> 16) * sc[j];
+            }
         }
     }
     u4v hv;
     if (x_resid) {
-        const u4v xr = *(const u4v*)(x_resid + (size_t)r * H + 8 * t);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             hv[q] = (uint32_t)f2h(h2f(xr[q] & 0xFFFFu) + hround(acc[2 * q])) |
@@ -285,13 +348,13 @@ __global__ __launch_bounds__(256) void k_combine_norm(const uint16_t* __restrict
             hv[q] = (uint32_t)f2h(acc[2 * q]) | ((uint32_t)f2h(acc[2 * q + 1]) << 16);
     }
     *(u4v*)(y + (size_t)r * H + 8 * t) = hv;
-    norm_row_2048(hv, no, r);
+    norm_row_2048_w(hv, wn, no, r);
 }
 
 hipError_t launch_combine_norm(const uint16_t* down, const float* scores, const uint16_t* x_resid,
                                uint16_t* y, int M, int k, int H, const NormOut& no,
                                const int* abort, hipStream_t st) {
-    if (H != 2048) return hipErrorInvalidValue;
+    if (H != 2048 || k < 1 || k > 8) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_combine_norm, dim3(M), dim3(256), 0, st, down, scores, x_resid, y, k, no,
                        abort);
     return hipGetLastError();
