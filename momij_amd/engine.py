@@ -99,6 +99,12 @@ class VerifyEngine:
             arr[i].attn = Context.attn_struct(lw["attn"])
             arr[i].moe = Context.moe_struct(lw["moe"])
         self._arr = arr
+        # per-call argument buffers, filled in place (building ctypes arrays every call costs
+        # more host time than the call itself)
+        self._rows = (C.c_int32 * _lib.MJ_MAX_ROWS)()
+        self._par = (C.c_int32 * _lib.MJ_MAX_ROWS)()
+        self._out = (C.c_int32 * _lib.MJ_MAX_ROWS)()
+        self._acc, self._tok = C.c_int32(), C.c_int32()
         h = C.c_void_p()
         c = cfg.to_c(lm_head_scales, lm_head_biases)
         ctx.check(self.lib.mj_model_create(ctx.h, C.byref(c), C.cast(arr, C.c_void_p), ptr(embed),
@@ -191,42 +197,46 @@ class VerifyEngine:
         self.ctx.check(self.lib.mj_step_chain_feeds(self.h, f, M, ev))
         return list(ev)
 
-    def verify_greedy(self, y: int, draft, parents=None) -> tuple[int, list[int]]:
+    def _draft_args(self, draft, parents=None):
         n = len(draft)
-        d = (C.c_int32 * max(n, 1))(*[int(t) for t in draft])
+        if n + 1 > _lib.MJ_MAX_ROWS:  # the library's own refusal (MJ_INVALID_ARG)
+            raise MomijError(4, f"draft of {n} nodes exceeds {_lib.MJ_MAX_ROWS - 1}")
+        self._rows[:n] = [int(t) for t in draft]
         par = None
         if parents is not None:
             assert len(parents) == n + 1
-            par = (C.c_int32 * (n + 1))(*[int(p) for p in parents])
-        acc = C.c_int32()
-        out = (C.c_int32 * (n + 1))()
-        self.ctx.check(self.lib.mj_verify_greedy(self.h, int(y), d, n, par, C.byref(acc), out))
-        return acc.value, list(out[: acc.value + 1])
+            self._par[: n + 1] = [int(p) for p in parents]
+            par = self._par
+        return n, par
+
+    def verify_greedy(self, y: int, draft, parents=None) -> tuple[int, list[int]]:
+        n, par = self._draft_args(draft, parents)
+        self.ctx.check(self.lib.mj_verify_greedy(self.h, int(y), self._rows, n, par,
+                                                 C.byref(self._acc), self._out))
+        acc = self._acc.value
+        return acc, list(self._out[: acc + 1])
 
     def verify_sampled(self, y: int, draft, temperature: float, q_mode: int, seed: int,
                        counter: int, q_point=None) -> tuple[int, int]:
-        n = len(draft)
-        d = (C.c_int32 * max(n, 1))(*[int(t) for t in draft])
+        n, _ = self._draft_args(draft)
         qp = None if q_point is None else (C.c_float * max(n, 1))(*[float(q) for q in q_point])
-        acc, tok = C.c_int32(), C.c_int32()
-        self.ctx.check(self.lib.mj_verify_sampled(self.h, int(y), d, n, temperature, q_mode, qp,
-                                                  seed, counter, C.byref(acc), C.byref(tok)))
-        return acc.value, tok.value
+        self.ctx.check(self.lib.mj_verify_sampled(self.h, int(y), self._rows, n, temperature,
+                                                  q_mode, qp, seed, counter, C.byref(self._acc),
+                                                  C.byref(self._tok)))
+        return self._acc.value, self._tok.value
 
     def verify_sampled_ex(self, y: int, draft, q_mode: int, seed: int, counter: int,
                           temperature: float, top_p=1.0, rep=1.0, pres=0.0, freq=0.0,
                           hist=None, q_point=None) -> tuple[int, int]:
         """mj_verify_sampled_ex: LogitsProcessor options; hist {token: count} or a pair of
         int32 arrays (tokens, counts)."""
-        n = len(draft)
-        d = (C.c_int32 * max(n, 1))(*[int(t) for t in draft])
+        n, _ = self._draft_args(draft)
         qp = None if q_point is None else (C.c_float * max(n, 1))(*[float(q) for q in q_point])
         sp, keep = _lib.sampling(temperature, top_p, rep, pres, freq, hist)
-        acc, tok = C.c_int32(), C.c_int32()
-        self.ctx.check(self.lib.mj_verify_sampled_ex(self.h, int(y), d, n, C.byref(sp), q_mode,
-                                                     qp, seed, counter, C.byref(acc),
-                                                     C.byref(tok)))
-        return acc.value, tok.value
+        self.ctx.check(self.lib.mj_verify_sampled_ex(self.h, int(y), self._rows, n, C.byref(sp),
+                                                     q_mode, qp, seed, counter,
+                                                     C.byref(self._acc), C.byref(self._tok)))
+        return self._acc.value, self._tok.value
 
 
 def random_model(cfg: MapleLikeConfig, seed: int = 0, device: str = "cuda",
