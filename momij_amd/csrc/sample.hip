@@ -25,7 +25,7 @@
 #define BLK 64
 #define MAX_CHUNKS 12288  // V <= 196608
 #define RMB 32            // blocks a row's maximum is split over
-#define DEC_STAGE 8192    // block sums the decision kernel stages in LDS (the rest it reads)
+#define DEC_STAGE (MJ_ROWS * (MAX_CHUNKS / BLK))  // every row's block sums, in LDS
 
 // Hand-off from the accept decisions to the residual walk: phase 1 = row fr was rejected and
 // its residual still has to be summed (k_resid_sums) and walked (k_resid_walk).
@@ -131,30 +131,137 @@ __device__ __forceinline__ void row_uniforms(const SampleArgs& a, int row, float
     u1 = u01(c[1]);
 }
 
-__device__ __forceinline__ float e_at(const SampleArgs& a, int row, int v, float mxs) {
-    const float s = a.logits[(size_t)row * a.V + v] * a.invT;
+__device__ __forceinline__ float e_of(const SampleArgs& a, float x, float mxs) {
+    const float s = x * a.invT;
     return canon_expf(s - mxs);
 }
 
-// residual mass at v of row `row` (p_v = e_v / Z)
-__device__ __forceinline__ float r_at(const SampleArgs& a, int row, int v, float mxs, float Z,
-                                      float q, int d) {
-    const float pv = __fdiv_rn(e_at(a, row, v, mxs), Z);
+__device__ __forceinline__ float e_at(const SampleArgs& a, int row, int v, float mxs) {
+    return e_of(a, a.logits[(size_t)row * a.V + v], mxs);
+}
+
+// residual mass at v given e_v (p_v = e_v / Z)
+__device__ __forceinline__ float r_of(const SampleArgs& a, float e, int v, float Z, float q,
+                                      int d) {
+    const float pv = __fdiv_rn(e, Z);
     if (a.q_mode == 1) return fmaxf(pv - q, 0.0f);
     if (v == d && q > 0.0f) return fmaxf(0.0f, pv - q);
     return pv;
 }
 
+// Rows of 16-byte aligned logits (float4 requests) or not (one float a request).
+__device__ __forceinline__ bool rows_aligned(const SampleArgs& a) {
+    return ((a.V & 3) | ((uintptr_t)a.logits & 15)) == 0;
+}
+
+// The CH logits of chunk c of a row, requested together; indices past the row's end clamp to
+// its last element (callers use only those below V).
+__device__ __forceinline__ void chunk_logits(const SampleArgs& a, int row, int c, float x[CH]) {
+    const float* rp = a.logits + (size_t)row * a.V;
+    if (rows_aligned(a)) {
+        const float4* p4 = (const float4*)rp;
+        const int last = (a.V >> 2) - 1;
+#pragma unroll
+        for (int k = 0; k < CH / 4; ++k) {
+            const float4 f = p4[min(c * (CH / 4) + k, last)];
+            x[4 * k] = f.x;
+            x[4 * k + 1] = f.y;
+            x[4 * k + 2] = f.z;
+            x[4 * k + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) x[k] = rp[min(c * CH + k, a.V - 1)];
+    }
+}
+
+// Chunk c's element values -- e, or the residual (resid) -- into x, and their sum in element
+// order.
+__device__ __forceinline__ float chunk_vals(const SampleArgs& a, int row, int c, bool resid,
+                                            float mxs, float Z, float q, int d, float x[CH]) {
+    chunk_logits(a, row, c, x);
+    const int v0 = c * CH;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+        float e = e_of(a, x[k], mxs);
+        if (resid) e = r_of(a, e, v0 + k, Z, q, d);
+        x[k] = e;
+        if (v0 + k < a.V) s = s + e;
+    }
+    return s;
+}
+
+// n >= 1 floats from src into LDS by nt threads, eight requests a thread in flight.
+__device__ __forceinline__ void stage_lds(float* dst, const float* src, int n, int t, int nt) {
+    for (int base = t; base < n; base += nt * 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = src[min(base + nt * k, n - 1)];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (base + nt * k < n) dst[base + nt * k] = v[k];
+    }
+}
+
+// One thread: p[0..n) (n >= 1) replaced by its running totals in order, p[b] = ((p_0 + p_1) +
+// ...) + p_b from 0.0f; returns the total.
+__device__ __forceinline__ float running_totals(float* p, int n) {
+    float z = 0.0f;
+    for (int b0 = 0; b0 < n; b0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = p[min(b0 + k, n - 1)];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (b0 + k < n) {
+                z = z + v[k];
+                p[b0 + k] = z;
+            }
+    }
+    return z;
+}
+
+// First lane of the (whole, converged) wave whose `hit` holds, or -1.
+__device__ __forceinline__ int wave_first(bool hit) {
+    const uint64_t m = __ballot(hit);
+    return m ? __ffsll((unsigned long long)m) - 1 : -1;
+}
+
 // Row maxima in RMB slices a row (a maximum is exact in any order): block (row, j) writes the
-// maximum of its slice; the sums kernel folds the RMB partials.
+// maximum of its slice; the sums kernel folds the RMB partials.  A thread requests its whole
+// share of the slice at once (indices clamp to the slice's last element, and a repeated element
+// leaves a maximum unchanged).
+#define RM_UNROLL 6  // float4 requests a thread: a slice of V / RMB <= 6144 floats in one round
 __global__ __launch_bounds__(256) void k_rowmax(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
     const int row = blockIdx.x / RMB, j = blockIdx.x % RMB, t = threadIdx.x;
-    const int span = (a.V + RMB - 1) / RMB;
-    const int v0 = j * span, v1 = min(a.V, v0 + span);
+    const float* rp = a.logits + (size_t)row * a.V;
     float m = -INFINITY;
-    for (int v = v0 + t; v < v1; v += 256) m = fmaxf(m, a.logits[(size_t)row * a.V + v]);
+    if (rows_aligned(a)) {
+        const int V4 = a.V >> 2, span = (V4 + RMB - 1) / RMB;
+        const int v0 = j * span, v1 = min(V4, v0 + span);
+        const float4* p4 = (const float4*)rp;
+        for (int v = v0 + t; v < v1; v += 256 * RM_UNROLL) {
+            float4 f[RM_UNROLL];
+#pragma unroll
+            for (int k = 0; k < RM_UNROLL; ++k) f[k] = p4[min(v + 256 * k, v1 - 1)];
+#pragma unroll
+            for (int k = 0; k < RM_UNROLL; ++k)
+                m = fmaxf(m, fmaxf(fmaxf(f[k].x, f[k].y), fmaxf(f[k].z, f[k].w)));
+        }
+    } else {
+        const int span = (a.V + RMB - 1) / RMB;
+        const int v0 = j * span, v1 = min(a.V, v0 + span);
+        for (int v = v0 + t; v < v1; v += 256 * 8) {
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) f[k] = rp[min(v + 256 * k, v1 - 1)];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) m = fmaxf(m, f[k]);
+        }
+    }
     m = wave_max(m);
     __shared__ float sm[4];
     if ((t & 63) == 0) sm[t >> 6] = m;
@@ -162,7 +269,9 @@ __global__ __launch_bounds__(256) void k_rowmax(SampleArgs a) {
     if (t == 0) a.mpart[row * RMB + j] = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
 }
 
-// Block sums of e_v: one 64-thread block per (row, 1024-element block), lane = chunk.
+// Block sums of e_v: one 64-thread block per (row, 1024-element block), lane = chunk.  The
+// partial maxima and the chunk's logits are requested together (clamped indices: every lane
+// loads, lanes past the end contribute nothing).
 __global__ __launch_bounds__(64) void k_sample_sums(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
@@ -170,17 +279,21 @@ __global__ __launch_bounds__(64) void k_sample_sums(SampleArgs a) {
     const int lane = threadIdx.x;
     const int nch = (a.V + CH - 1) / CH;
     const int chunk = b * BLK + lane;
-    float mx = lane < RMB ? a.mpart[row * RMB + lane] : -INFINITY;
+    float mx = a.mpart[row * RMB + (lane & (RMB - 1))];
+    float x[CH];
+    chunk_logits(a, row, min(chunk, nch - 1), x);
     mx = wave_max(mx);
     if (b == 0 && lane == 0) a.rowmax[row] = mx;
     const float mxs = mx * a.invT;
+    const int v0 = chunk * CH;
     float cs = 0.0f;
-    if (chunk < nch) {
-        const int e = min(chunk * CH + CH, a.V);
-        for (int v = chunk * CH; v < e; ++v) cs = cs + e_at(a, row, v, mxs);
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+        const float e = e_of(a, x[k], mxs);
+        if (v0 + k < a.V) cs = cs + e;
     }
     __shared__ float s[BLK];
-    s[lane] = cs;
+    s[lane] = chunk < nch ? cs : 0.0f;
     __syncthreads();
     if (lane == 0) {
         float bs = 0.0f;
@@ -204,145 +317,114 @@ __device__ __forceinline__ void write_result(const SampleArgs& a, int acc, int t
     }
 }
 
-// Walk of row `row` to tgt over its mass -- the residual (walk_resid: block sums in rbs) or e
-// (block sums in bsum) -- block, then chunk (the chosen block's 64 chunk sums recomputed in the
-// same order), then element; writes (fr, token).  Whole block (>= 64 threads).
-__device__ void walk_write(const SampleArgs& a, int row, int fr, bool walk_resid, float tgt,
-                           float mxs, float Zr, float q, int d) {
+// Walk of row `row` to tgt over its mass -- the residual (resid) or e -- given the running
+// totals of its block sums (pref[b] = ((s_0 + s_1) + ...) + s_b, the totals a sequential walk
+// forms): the first block whose running total reaches tgt (the last element if none), in it the
+// first chunk (the block's 64 chunk sums recomputed in the same order, running on from the total
+// before the block; the block's last element if none), then the first element of that chunk;
+// writes (fr, token).  Block of 256 threads; the block's chunk sums and element values are
+// computed once, and the running totals of a level are formed redundantly by every lane of
+// wave 0 so that the first lane reaching tgt is found by one ballot.
+__device__ void walk_write(const SampleArgs& a, int row, int fr, bool resid, float tgt,
+                           const float* pref, float mxs, float Zr, float q, int d) {
     const int t = threadIdx.x;
-    const int nch = (a.V + CH - 1) / CH;
-    __shared__ float sbs[MAX_CHUNKS / BLK];
-    __shared__ float cs[BLK];
-    __shared__ float ev[CH];
-    __shared__ int s_bidx, s_cidx, s_tok;
-    __shared__ float s_P, s_Q;
-    // the row's block sums, requested together
-    for (int b = t; b < a.nblocks; b += blockDim.x)
-        sbs[b] = walk_resid ? a.rbs[b] : a.bsum[(size_t)row * a.nblocks + b];
+    const int nch = (a.V + CH - 1) / CH, nb = a.nblocks;
+    __shared__ __align__(16) float cs[BLK];
+    __shared__ __align__(16) float ev[BLK][CH + 4];
+    __shared__ int s_blk;
+    if (t == 0) s_blk = nb;
     __syncthreads();
-    if (t == 0) {
-        float P = 0.0f;
-        int blk = -1;
-        for (int b = 0; b < a.nblocks; ++b) {
-            const float Pn = P + sbs[b];
-            if (tgt <= Pn) {
-                blk = b;
-                break;
-            }
-            P = Pn;
-        }
-        s_bidx = blk;
-        s_P = P;
-        s_tok = a.V - 1;
+    if (t < nb && tgt <= pref[t]) atomicMin(&s_blk, t);  // nb <= MAX_CHUNKS / BLK <= 256
+    __syncthreads();
+    const int blk = s_blk;
+    if (blk == nb) {  // block-uniform
+        if (t == 0) write_result(a, fr, a.V - 1);
+        return;
+    }
+    const int c0 = blk * BLK, n = min(BLK, nch - c0);
+    const float P = blk > 0 ? pref[blk - 1] : 0.0f;
+    if (t < BLK) {
+        float x[CH];
+        const float s = chunk_vals(a, row, min(c0 + t, nch - 1), resid, mxs, Zr, q, d, x);
+        cs[t] = s;
+        float4* e4 = (float4*)ev[t];
+#pragma unroll
+        for (int k = 0; k < CH / 4; ++k)
+            e4[k] = make_float4(x[4 * k], x[4 * k + 1], x[4 * k + 2], x[4 * k + 3]);
     }
     __syncthreads();
-    const int blk = s_bidx;
-    if (blk >= 0) {
-        if (t < BLK) {
-            const int c = blk * BLK + t;
-            float sum = 0.0f;
-            if (c < nch) {
-                const int e = min(c * CH + CH, a.V);
-                for (int v = c * CH; v < e; ++v)
-                    sum = sum + (walk_resid ? r_at(a, row, v, mxs, Zr, q, d) : e_at(a, row, v, mxs));
-            }
-            cs[t] = sum;
-        }
-        __syncthreads();
-        if (t == 0) {
-            const int c0 = blk * BLK, c1 = min(c0 + BLK, nch);
-            float Q = s_P;
-            int cc = -1;
-            for (int c = c0; c < c1; ++c) {
-                const float Qn = Q + cs[c - c0];
-                if (tgt <= Qn) {
-                    cc = c;
-                    break;
-                }
-                Q = Qn;
-            }
-            s_cidx = cc;
-            s_Q = Q;
-            if (cc < 0) s_tok = min(c1 * CH, a.V) - 1;
-        }
-        __syncthreads();
-        const int cc = s_cidx;
-        if (cc >= 0) {
-            // the chunk's element values, each computed once, then the running total in order
-            const int e = min(cc * CH + CH, a.V);
-            if (t < CH && cc * CH + t < e) {
-                const int v = cc * CH + t;
-                ev[t] = walk_resid ? r_at(a, row, v, mxs, Zr, q, d) : e_at(a, row, v, mxs);
-            }
-            __syncthreads();
-            if (t == 0) {
-                float R = s_Q;
-                int tok = e - 1;
-                for (int v = cc * CH; v < e; ++v) {
-                    R = R + ev[v - cc * CH];
-                    if (tgt <= R) {
-                        tok = v;
-                        break;
-                    }
-                }
-                s_tok = tok;
-            }
-            __syncthreads();
-        }
+    if (t >= 64) return;  // wave 0 finishes (wave-uniform)
+    // chunk level: lane k keeps the running total after chunk k
+    float Q = P, Qk = 0.0f;
+#pragma unroll
+    for (int k = 0; k < BLK; ++k) {
+        Q = Q + cs[k];
+        Qk = t == k ? Q : Qk;
     }
-    if (t == 0) write_result(a, fr, s_tok);
+    const int ci = wave_first(t < n && tgt <= Qk);
+    int tok;
+    if (ci < 0) {
+        tok = min((c0 + n) * CH, a.V) - 1;
+    } else {
+        const int cc = c0 + ci;
+        const int ne = min(CH, a.V - cc * CH);
+        float R = ci > 0 ? __shfl(Qk, ci - 1) : P, Rk = 0.0f;
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            R = R + ev[ci][k];
+            Rk = t == k ? R : Rk;
+        }
+        const int ei = wave_first(t < ne && tgt <= Rk);
+        tok = cc * CH + (ei < 0 ? ne - 1 : ei);
+    }
+    if (t == 0) write_result(a, fr, tok);
 }
 
-// Single block: row totals and the sequential accept decisions.  A full accept samples the bonus
-// here (or leaves it to the nucleus kernels); a reject hands row fr to k_resid_sums /
+// Single block: row totals (with their running totals kept for a walk) and the accept
+// decisions, one row a lane; the first rejected row ends the chain.  A full accept samples the
+// bonus here (or leaves it to the nucleus kernels); a reject hands row fr to k_resid_sums /
 // k_resid_walk through the state.
-__global__ __launch_bounds__(64) void k_sample_decide(SampleArgs a) {
+__global__ __launch_bounds__(256) void k_sample_decide(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
     const int t = threadIdx.x;
     const int D = a.rows - 1;
-    __shared__ float Z[MJ_ROWS];
-    __shared__ float ed[MJ_ROWS];
-    __shared__ float sbs[DEC_STAGE];
-    __shared__ int s_fr;
-    // every row's block sums and the drafts' e values, requested together; then each row's
-    // total in block order
     const int per = a.nblocks;
-    const int nst = min(a.rows * per, DEC_STAGE);
-    for (int idx = t; idx < nst; idx += blockDim.x) sbs[idx] = a.bsum[idx];
+    __shared__ float Z[MJ_ROWS];
+    __shared__ float pref[DEC_STAGE];  // row r's block sums at r * per, then their running totals
+    __shared__ int s_fr;
+    // the drafts' e values and every row's block sums, requested together
+    int d = -1;
+    float ed = 0.0f;
     if (t < D) {
-        const int d = a.draft[t];
-        ed[t] = (d >= 0 && d < a.V) ? e_at(a, t, d, a.rowmax[t] * a.invT) : 0.0f;
+        d = a.draft[t];
+        if (d >= 0 && d < a.V)
+            ed = e_of(a, a.logits[(size_t)t * a.V + d], a.rowmax[t] * a.invT);
     }
+    stage_lds(pref, a.bsum, a.rows * per, t, 256);
     __syncthreads();
-    if (t < a.rows) {
-        float z = 0.0f;
-        for (int b = 0; b < per; ++b) {
-            const int idx = t * per + b;
-            z = z + (idx < DEC_STAGE ? sbs[idx] : a.bsum[idx]);
-        }
-        Z[t] = z;
-    }
+    if (t < a.rows) Z[t] = running_totals(pref + t * per, per);
     __syncthreads();
-    if (t == 0) {
-        int fr = D;
-        for (int i = 0; i < D; ++i) {
-            const int d = a.draft[i];
-            const float p = (d >= 0 && d < a.V) ? __fdiv_rn(ed[i], Z[i]) : 0.0f;
-            float q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[i] : 1.0f);
+    if (t < 64) {  // wave 0: one draft a lane (D < MJ_ROWS == 64)
+        bool rej = false;
+        if (t < D) {
+            const float p = (d >= 0 && d < a.V) ? __fdiv_rn(ed, Z[t]) : 0.0f;
+            float q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[t] : 1.0f);
             q = fmaxf(0.0f, q);
             float u0, u1;
-            row_uniforms(a, i, u0, u1);
-            if (q > 0.0f && p > 0.0f && u0 <= fminf(1.0f, __fdiv_rn(p, q))) continue;
-            fr = i;
-            break;
+            row_uniforms(a, t, u0, u1);
+            rej = !(q > 0.0f && p > 0.0f && u0 <= fminf(1.0f, __fdiv_rn(p, q)));
         }
-        s_fr = fr;
-        if (fr < D) {
-            float q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[fr] : 1.0f);
-            *a.state = SampleState{1, fr, a.draft[fr], 0, fmaxf(0.0f, q), Z[fr], 0.0f, 0.0f};
-        } else {
-            *a.state = SampleState{0, fr, -1, 0, 0.0f, Z[fr], 0.0f, 0.0f};
+        const int f = wave_first(rej);
+        const int fr = f < 0 ? D : f;
+        if (t == 0) {
+            s_fr = fr;
+            if (fr < D) {
+                float q = a.q_mode == 1 ? a.q_uniform : (a.q_point ? a.q_point[fr] : 1.0f);
+                *a.state = SampleState{1, fr, a.draft[fr], 0, fmaxf(0.0f, q), Z[fr], 0.0f, 0.0f};
+            } else {
+                *a.state = SampleState{0, fr, -1, 0, 0.0f, Z[fr], 0.0f, 0.0f};
+            }
         }
     }
     __syncthreads();
@@ -356,7 +438,8 @@ __global__ __launch_bounds__(64) void k_sample_decide(SampleArgs a) {
         return;  // block-uniform
     }
     if (t == 0 && a.nb.st) a.nb.st->need = 0;
-    walk_write(a, fr, fr, false, u0 * Z[fr], a.rowmax[fr] * a.invT, Z[fr], 0.0f, -1);
+    walk_write(a, fr, fr, false, u0 * Z[fr], pref + fr * per, a.rowmax[fr] * a.invT, Z[fr],
+               0.0f, -1);
 }
 
 // Residual block sums of the rejected row (same chunk / block order as the e sums): one 64-thread
@@ -370,13 +453,10 @@ __global__ __launch_bounds__(64) void k_resid_sums(SampleArgs a) {
     const int nch = (a.V + CH - 1) / CH;
     const int chunk = b * BLK + lane;
     const float mxs = a.rowmax[st.fr] * a.invT;
-    float cs = 0.0f;
-    if (chunk < nch) {
-        const int e = min(chunk * CH + CH, a.V);
-        for (int v = chunk * CH; v < e; ++v) cs = cs + r_at(a, st.fr, v, mxs, st.Zr, st.q, st.d);
-    }
+    float x[CH];
+    const float cs = chunk_vals(a, st.fr, min(chunk, nch - 1), true, mxs, st.Zr, st.q, st.d, x);
     __shared__ float sc[BLK];
-    sc[lane] = cs;
+    sc[lane] = chunk < nch ? cs : 0.0f;
     __syncthreads();
     if (lane == 0) {
         float bs = 0.0f;
@@ -387,22 +467,19 @@ __global__ __launch_bounds__(64) void k_resid_sums(SampleArgs a) {
 }
 
 // The rejected row's sample: the residual total S, then a walk to u1 * S over the residual, or,
-// with no residual mass, samplePrepared of the row (nucleus kernels, or a walk to u1 * Z over e).
-__global__ __launch_bounds__(64) void k_resid_walk(SampleArgs a) {
+// with no residual mass, samplePrepared of the row (nucleus kernels, or a walk to u1 * Z over e
+// with the row's block sums).
+__global__ __launch_bounds__(256) void k_resid_walk(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
     const SampleState st = *a.state;
     if (st.phase != 1) return;
     const int t = threadIdx.x;
     __shared__ float s_S;
-    __shared__ float srb[MAX_CHUNKS / BLK];
-    for (int b = t; b < a.nblocks; b += blockDim.x) srb[b] = a.rbs[b];
+    __shared__ float pref[MAX_CHUNKS / BLK];
+    stage_lds(pref, a.rbs, a.nblocks, t, 256);
     __syncthreads();
-    if (t == 0) {
-        float S = 0.0f;
-        for (int b = 0; b < a.nblocks; ++b) S = S + srb[b];
-        s_S = S;
-    }
+    if (t == 0) s_S = running_totals(pref, a.nblocks);
     __syncthreads();
     const float S = s_S;
     float u0, u1;
@@ -413,7 +490,13 @@ __global__ __launch_bounds__(64) void k_resid_walk(SampleArgs a) {
         return;  // block-uniform
     }
     if (t == 0 && a.nb.st) a.nb.st->need = 0;
-    walk_write(a, st.fr, st.fr, walk_resid, walk_resid ? u1 * S : u1 * st.Zr,
+    if (!walk_resid) {  // block-uniform: the row's e block sums instead
+        stage_lds(pref, a.bsum + (size_t)st.fr * a.nblocks, a.nblocks, t, 256);
+        __syncthreads();
+        if (t == 0) running_totals(pref, a.nblocks);
+        __syncthreads();
+    }
+    walk_write(a, st.fr, st.fr, walk_resid, walk_resid ? u1 * S : u1 * st.Zr, pref,
                a.rowmax[st.fr] * a.invT, st.Zr, st.q, st.d);
 }
 
@@ -595,13 +678,13 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
     hipLaunchKernelGGL(k_sample_sums, dim3(rows * a.nblocks), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_sample_decide, dim3(1), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(k_sample_decide, dim3(1), dim3(256), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_resid_sums, dim3(a.nblocks), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_resid_walk, dim3(1), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(k_resid_walk, dim3(1), dim3(256), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess || !nb) return e;
     hipLaunchKernelGGL(k_nucleus_keys, dim3((V + 255) / 256), dim3(256), 0, st, a);

@@ -290,3 +290,52 @@ def test_accept_sampled_ex_bit_exact(ctx, head_case, orc, opts):
         seen[ref[0]] = seen.get(ref[0], 0) + 1
     assert (host(logits).view(np.uint32) == lh.view(np.uint32)).all()
     print("accepted-count histogram", opts, seen, flush=True)
+
+
+@pytest.mark.parametrize("Vs,off,opts", [
+    (151923, 0, None),                 # rows not 16-byte aligned, last chunk and block partial
+    (1001, 0, None),                   # one block of 63 chunks, the last partial
+    (V, 1, None),                      # aligned width, base pointer one float off
+    (151923, 0, dict(top_p=0.5, rep=1.3, pres=0.4, freq=0.25)),
+])
+def test_accept_sampled_unaligned_rows_bit_exact(ctx, head_case, orc, Vs, off, opts):
+    """Rows the kernels cannot read as float4 (width not a multiple of 4, or a base address off
+    16 bytes) take the one-float-a-request path; partial chunks and blocks end the row.  Bit for
+    bit against the oracle on the same logits and uniforms."""
+    import torch
+
+    logits = head_case["logits"]
+    buf = torch.empty(M * Vs + off, dtype=torch.float32, device="cuda")
+    lv = buf[off:].view(M, Vs)
+    lv.copy_(logits[:, :Vs])
+    torch.cuda.synchronize()
+    lh = host(lv)
+    am = lh.argmax(1).astype(np.int32)
+    rng = np.random.default_rng(Vs + off)
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    seen = {}
+    for trial in range(10):
+        draft = am[:M - 1].copy()
+        for i in range(5, M - 1):
+            draft[i] = rng.integers(0, Vs)
+        if trial % 3 == 0:
+            draft[int(rng.integers(0, 5))] = rng.integers(0, Vs)  # early reject
+        q_mode = trial % 2
+        dd = dev(draft.astype(np.int32))
+        torch.cuda.synchronize()
+        u = orc.verify_uniforms(2025, trial, M)
+        if opts is None:
+            ctx.accept_sampled(lv, M, Vs, dd, 0.7, q_mode, 2025, trial, out)
+            ref = orc.accept_sampled(lh, draft, 0.7, q_mode, u)
+        else:
+            hist = {int(t): int(c) for t, c in zip(rng.integers(0, Vs, 50), rng.integers(0, 4, 50))}
+            ctx.accept_sampled_ex(lv, M, Vs, dd, q_mode, 2025, trial, out, 0.7, hist=hist, **opts)
+            ht = np.array(list(hist.keys()), np.int32)
+            hc = np.array([hist[t] for t in ht.tolist()], np.int32)
+            ref = orc.accept_sampled_ex(lh, draft, 0.7, q_mode, u, hist_tok=ht, hist_cnt=hc,
+                                        **opts)
+        ctx.sync()
+        got = tuple(int(v) for v in host(out))
+        assert got == ref, (Vs, off, trial, got, ref)
+        seen[ref[0]] = seen.get(ref[0], 0) + 1
+    print("accepted-count histogram", Vs, off, seen, flush=True)
