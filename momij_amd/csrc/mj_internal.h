@@ -248,12 +248,14 @@ size_t nucleus_bytes(int V);
 void nucleus_layout(void* base, int V, NucleusBuf& nb);
 // Full-vocabulary sampled acceptance.  With sd the temperature, q, uniforms' seed / counter,
 // the drafts and the options' scalars come from the step descriptor (hist arrays from o).
+// head_max: the exact maxima of the rows as given (the lm_head's), for a call without
+// penalties only (the caller knows): the penalty and row-maximum launches are then left out.
 hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* draft,
                                  float temperature, int q_mode, const float* q_point,
                                  uint64_t seed, uint64_t counter, const SampleOpts& o,
                                  const NucleusBuf* nb, float* rowmax, float* bsum, int32_t* out,
                                  StepResult* res, const StepDesc* sd, const int* abort,
-                                 hipStream_t st);
+                                 hipStream_t st, const float* head_max = nullptr);
 int sample_nblocks(int V);
 size_t sample_scratch_floats(int rows, int V);  // the bsum buffer of launch_accept_sampled
 

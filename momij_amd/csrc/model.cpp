@@ -19,14 +19,21 @@
 #include "mj_abi_internal.h"
 #include "mj_internal.h"
 
-// PASS_SAMPLED_NUC: a sampled pass whose bonus (or zero-mass residual) takes a nucleus
+// PASS_SAMPLED_NUC: a sampled pass whose bonus (or zero-mass residual) takes a nucleus.
+// PASS_PEN marks a sampled pass with penalties: the logits are rewritten, so the row maxima are
+// recomputed; without it the lm_head's maxima are used and those launches are left out.
 enum PassKind {
     PASS_PREFILL = 0,
     PASS_CHAIN = 1,
     PASS_GREEDY = 2,
     PASS_SAMPLED = 3,
-    PASS_SAMPLED_NUC = 4
+    PASS_SAMPLED_NUC = 4,
+    PASS_PEN = 8
 };
+
+static bool sampled_pass(int kind) {
+    return (kind & ~PASS_PEN) == PASS_SAMPLED || (kind & ~PASS_PEN) == PASS_SAMPLED_NUC;
+}
 
 struct mj_model {
     mj_ctx* ctx = nullptr;
@@ -256,7 +263,7 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
             if (s != MJ_OK) return s;
         }
         float* logits =
-            (kind == PASS_SAMPLED || kind == PASS_SAMPLED_NUC || m->cap.logits) ? m->logits : nullptr;
+            (sampled_pass(kind) || m->cap.logits) ? m->logits : nullptr;
         if (m->profiling) m->prof.begin(PROF_HEAD, st);
         if (c.head_bits == 4)
             s = mj_hip(ctx,
@@ -278,15 +285,16 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                            hipMemcpyDeviceToDevice, st), "capture");
             if (s != MJ_OK) return s;
         }
-        if (kind == PASS_SAMPLED || kind == PASS_SAMPLED_NUC) {
+        if (sampled_pass(kind)) {
             SampleOpts o{};
             o.hist_tok = m->hist_tok;
             o.hist_cnt = m->hist_cnt;
+            const bool nuc = (kind & ~PASS_PEN) == PASS_SAMPLED_NUC;
             s = mj_hip(ctx, launch_accept_sampled(m->logits, M, c.vocab, nullptr, 1.0f, 0, nullptr,
-                                                  0, 0, o,
-                                                  kind == PASS_SAMPLED_NUC ? &m->nuc : nullptr,
-                                                  m->rowmax, m->bsum, nullptr, m->res_dev,
-                                                  m->sd_dev, ab, st), "sampled accept");
+                                                  0, 0, o, nuc ? &m->nuc : nullptr, m->rowmax,
+                                                  m->bsum, nullptr, m->res_dev, m->sd_dev, ab, st,
+                                                  (kind & PASS_PEN) ? nullptr : m->maxv),
+                       "sampled accept");
         } else {
             const int32_t* toks = (const int32_t*)((char*)m->sd_dev + offsetof(StepDesc, tokens));
             const int32_t* pars = (const int32_t*)((char*)m->sd_dev + offsetof(StepDesc, parents));
@@ -294,7 +302,7 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                                  st), "greedy accept");
         }
         if (s != MJ_OK) return s;
-        if (kind == PASS_GREEDY || kind == PASS_SAMPLED || kind == PASS_SAMPLED_NUC) {
+        if (kind == PASS_GREEDY || sampled_pass(kind)) {
             s = mj_hip(ctx, launch_kv_commit(m->kv, m->layer_stride, c.n_layers, c.kv_capacity,
                                              c.n_kv_heads, m->sd_dev, m->res_dev, ab, st),
                        "kv commit");
@@ -773,7 +781,10 @@ mj_status mj_verify_sampled_ex(mj_model* m, int32_t y, const int32_t* draft, int
     int32_t rows[MJ_MAX_ROWS];
     rows[0] = y;
     for (int i = 0; i < n_draft; ++i) rows[i + 1] = draft[i];
-    s = feed_rows(m, rows, nullptr, M, o.top_p < 1.0f - 1e-6f ? PASS_SAMPLED_NUC : PASS_SAMPLED);
+    const bool pen = (std::fabs(o.rep - 1.0f) > 1e-6f && o.rep > 0.0f) || o.pres != 0.0f ||
+                     o.freq != 0.0f;
+    s = feed_rows(m, rows, nullptr, M,
+                  (o.top_p < 1.0f - 1e-6f ? PASS_SAMPLED_NUC : PASS_SAMPLED) | (pen ? PASS_PEN : 0));
     if (s != MJ_OK) return s;
     const StepResult* r = m->res_host;
     m->offset += r->accepted + 1;

@@ -48,6 +48,7 @@ struct SampleArgs {
     float* bsum;           // [rows][nblocks] block sums of e
     int nblocks;
     float* mpart;          // [rows][RMB] partial row maxima
+    const float* head_max; // [rows] row maxima already known (no penalties), or nullptr
     float* rbs;            // [nblocks] block sums of the residual of the rejected row
     struct SampleState* state;
     int32_t* out;          // [2] or nullptr
@@ -270,8 +271,8 @@ __global__ __launch_bounds__(256) void k_rowmax(SampleArgs a) {
 }
 
 // Block sums of e_v: one 64-thread block per (row, 1024-element block), lane = chunk.  The
-// partial maxima and the chunk's logits are requested together (clamped indices: every lane
-// loads, lanes past the end contribute nothing).
+// row maximum (the lm_head's, or folded from the partial maxima) and the chunk's logits are
+// requested together (clamped indices: every lane loads, lanes past the end contribute nothing).
 __global__ __launch_bounds__(64) void k_sample_sums(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
@@ -279,10 +280,13 @@ __global__ __launch_bounds__(64) void k_sample_sums(SampleArgs a) {
     const int lane = threadIdx.x;
     const int nch = (a.V + CH - 1) / CH;
     const int chunk = b * BLK + lane;
-    float mx = a.mpart[row * RMB + (lane & (RMB - 1))];
     float x[CH];
     chunk_logits(a, row, min(chunk, nch - 1), x);
-    mx = wave_max(mx);
+    float mx;
+    if (a.head_max)
+        mx = a.head_max[row];
+    else
+        mx = wave_max(a.mpart[row * RMB + (lane & (RMB - 1))]);
     if (b == 0 && lane == 0) a.rowmax[row] = mx;
     const float mxs = mx * a.invT;
     const int v0 = chunk * CH;
@@ -642,7 +646,7 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
                                  uint64_t seed, uint64_t counter, const SampleOpts& o,
                                  const NucleusBuf* nb, float* rowmax, float* bsum, int32_t* out,
                                  StepResult* res, const StepDesc* sd, const int* abort,
-                                 hipStream_t st) {
+                                 hipStream_t st, const float* head_max) {
     SampleArgs a{};
     a.sd = sd;
     a.logits = logits;
@@ -668,13 +672,17 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
     a.abort = abort;
     a.o = o;
     if (nb) a.nb = *nb;
+    a.head_max = head_max;
     if (V > MAX_CHUNKS * CH || rows > MJ_ROWS) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_penalize, dim3(rows), dim3(256), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_rowmax, dim3(rows * RMB), dim3(256), 0, st, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e = hipSuccess;
+    if (!head_max) {
+        hipLaunchKernelGGL(k_penalize, dim3(rows), dim3(256), 0, st, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_rowmax, dim3(rows * RMB), dim3(256), 0, st, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(k_sample_sums, dim3(rows * a.nblocks), dim3(64), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
