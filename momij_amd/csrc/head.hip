@@ -556,16 +556,15 @@ __global__ __launch_bounds__(512) void k_lm_head_q4(HeadQ4Args a) {
 }
 
 // One wave per row: fold the block partials (value, lowest id on ties; log-sum-exp pairs).
-__global__ __launch_bounds__(64) void k_head_final(const float* pval, const int* pidx, int nblk,
-                                                   int M, int32_t* out_idx, float* out_max,
-                                                   HeadLse lse, const int* abort) {
-    if (aborted(abort)) return;
-    const int m = blockIdx.x, lane = threadIdx.x;
-    if (m >= M) return;
+// Row m's fold by one wave: its nblk partials, eight a lane requested together.  Every lane
+// returns the row's argmax id; lane 0 writes out_idx / out_max / the log-sum-exp.
+__device__ __forceinline__ int head_fold_row(const float* pval, const int* pidx, int nblk, int m,
+                                             int lane, int32_t* out_idx, float* out_max,
+                                             const HeadLse& lse) {
     float b = -INFINITY;
     int i = 0x7fffffff;
     float lm = -INFINITY, ls = 0.0f;
-    for (int k0 = 0; k0 < nblk; k0 += 8 * 64) {  // eight partials a lane requested together
+    for (int k0 = 0; k0 < nblk; k0 += 8 * 64) {
         float v[8];
         int j[8];
 #pragma unroll
@@ -600,6 +599,98 @@ __global__ __launch_bounds__(64) void k_head_final(const float* pval, const int*
         // ln sum_v exp(logit_v / T) = ln 2 * (m + log2 s); -inf when every id is banned
         if (lse.out) lse.out[m] = lm == -INFINITY ? -INFINITY : 0.69314718f * (lm + __log2f(ls));
     }
+    return i;
+}
+
+__global__ __launch_bounds__(64) void k_head_final(const float* pval, const int* pidx, int nblk,
+                                                   int M, int32_t* out_idx, float* out_max,
+                                                   HeadLse lse, const int* abort) {
+    if (aborted(abort)) return;
+    const int m = blockIdx.x;
+    if (m >= M) return;
+    head_fold_row(pval, pidx, nblk, m, threadIdx.x, out_idx, out_max, lse);
+}
+
+// Greedy acceptance by one wave, lane c = row c < n (n <= 64): tok / par / am are row c's token,
+// parent and argmax.  verifyDraftChain's longest-prefix rule walked over the draft tree: from
+// row 0, the lowest-index child whose token equals the current row's argmax, while one exists
+// (a ballot a level).  Writes res (path, emit, argmax) and / or out_flat ([acc, token,
+// path[0..n), emit[0..n)]).
+__device__ __forceinline__ void accept_greedy_wave(int tok, int par, int am, int n,
+                                                   StepResult* res, int32_t* out_flat) {
+    const int lane = threadIdx.x & 63;
+    int cur = 0, acc = 0, my_path = 0, my_emit = 0;
+    for (;;) {
+        const int amc = __shfl(am, cur);
+        const uint64_t kids = __ballot(lane < n && par == cur && tok == amc);
+        if (!kids) break;
+        const int next = __ffsll((unsigned long long)kids) - 1;
+        const int tn = __shfl(tok, next);
+        if (lane == acc) my_emit = tn;
+        ++acc;
+        if (lane == acc) my_path = next;
+        cur = next;
+    }
+    const int fin = __shfl(am, cur);
+    if (lane == acc) my_emit = fin;
+    if (res) {
+        if (lane == 0) {
+            res->accepted = acc;
+            res->token = fin;
+        }
+        if (lane <= acc) {
+            res->path[lane] = my_path;
+            res->emit[lane] = my_emit;
+        }
+        if (lane < n) res->argmax[lane] = am;
+    }
+    if (out_flat) {
+        if (lane == 0) {
+            out_flat[0] = acc;
+            out_flat[1] = fin;
+        }
+        if (lane <= acc) {
+            out_flat[2 + lane] = my_path;
+            out_flat[2 + n + lane] = my_emit;
+        }
+    }
+}
+
+// k_head_final over every row of one launch group (M <= 32, a wave a row), then the greedy
+// acceptance from the argmax ids it just formed: one launch where there were two.
+__global__ __launch_bounds__(1024) void k_head_final_accept(const float* pval, const int* pidx,
+                                                            int nblk, int M, int32_t* out_idx,
+                                                            float* out_max, HeadLse lse,
+                                                            const int* abort, GreedyAccept ga) {
+    if (aborted(abort)) return;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    __shared__ int s_am[32];
+    // the accept's per-row inputs, requested before the fold
+    const int tok = lane < M ? ga.tokens[lane] : -1;
+    const int par = lane < M ? ga.parents[lane] : -2;
+    for (int m = wv; m < M; m += (int)(blockDim.x >> 6)) {
+        const int i = head_fold_row(pval, pidx, nblk, m, lane, out_idx, out_max, lse);
+        if (lane == 0) s_am[m] = i;
+    }
+    __syncthreads();
+    if (wv == 0) accept_greedy_wave(tok, par, lane < M ? s_am[lane] : -1, M, ga.res, nullptr);
+}
+
+// The fold of rows m0 .. m0 + mg of M.  With ga the greedy acceptance follows: in the same
+// launch when the rows are one group (M <= 32), else after the last group's fold.
+static hipError_t launch_head_final(const float* pval, const int* pidx, int nb, int M, int m0,
+                                    int mg, int32_t* out_idx, float* out_max, const HeadLse& gl,
+                                    const int* abort, hipStream_t st, const GreedyAccept* ga) {
+    if (ga && M <= 32) {
+        hipLaunchKernelGGL(k_head_final_accept, dim3(1), dim3(64 * (mg < 16 ? mg : 16)), 0, st,
+                           pval, pidx, nb, mg, out_idx, out_max, gl, abort, *ga);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg, out_idx + m0,
+                       out_max ? out_max + m0 : nullptr, gl, abort);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !ga || m0 + mg < M) return e;
+    return launch_accept_greedy(ga->tokens, ga->parents, out_idx, M, ga->res, nullptr, abort, st);
 }
 
 // two 512-thread blocks per CU (the staged rows take at most 66 KB of LDS each)
@@ -620,7 +711,7 @@ int head_blocks() {
 hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, int V,
                           const int32_t* banned, int n_banned, float* logits, float* pval,
                           int* pidx, int32_t* out_idx, float* out_max, HeadLse lse,
-                          const int* abort, hipStream_t st) {
+                          const int* abort, hipStream_t st, const GreedyAccept* ga) {
     if (K % 256 != 0 || M < 1 || n_banned > MJ_HEAD_MAX_BANNED)  // halves of 128-k multiples
         return hipErrorInvalidValue;
     for (int m0 = 0; m0 < M; m0 += 32) {
@@ -649,9 +740,7 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg,
-                           out_idx + m0, out_max ? out_max + m0 : nullptr, gl, abort);
-        e = hipGetLastError();
+        e = launch_head_final(pval, pidx, nb, M, m0, mg, out_idx, out_max, gl, abort, st, ga);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -659,47 +748,19 @@ hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, in
 
 // ---------------------------------------------------------------------------------------
 // Greedy acceptance over rows 0..n-1 (row 0 = the fed token y).  tokens/parents from the
-// step descriptor (or explicit arrays), argmax per row.  Single thread: n <= 64.
+// step descriptor (or explicit arrays), argmax per row.  One wave: n <= 64.
 // ---------------------------------------------------------------------------------------
-__global__ void k_accept_greedy(const int32_t* tokens, const int32_t* parents,
-                                const int32_t* argmax, int n, StepResult* res,
-                                int32_t* out_flat, const int* abort) {
+__global__ __launch_bounds__(64) void k_accept_greedy(const int32_t* tokens,
+                                                      const int32_t* parents,
+                                                      const int32_t* argmax, int n,
+                                                      StepResult* res, int32_t* out_flat,
+                                                      const int* abort) {
     if (aborted(abort)) return;
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    int cur = 0, acc = 0;
-    int path[MJ_ROWS], emit[MJ_ROWS];
-    path[0] = 0;
-    for (;;) {
-        int next = -1;
-        for (int c = cur + 1; c < n; ++c)
-            if (parents[c] == cur && tokens[c] == argmax[cur]) {
-                next = c;
-                break;
-            }
-        if (next < 0) break;
-        emit[acc] = tokens[next];
-        ++acc;
-        path[acc] = next;
-        cur = next;
-    }
-    emit[acc] = argmax[cur];
-    if (res) {
-        res->accepted = acc;
-        res->token = argmax[cur];
-        for (int i = 0; i <= acc; ++i) {
-            res->path[i] = path[i];
-            res->emit[i] = emit[i];
-        }
-        for (int i = 0; i < n; ++i) res->argmax[i] = argmax[i];
-    }
-    if (out_flat) {
-        out_flat[0] = acc;
-        out_flat[1] = argmax[cur];
-        for (int i = 0; i <= acc; ++i) {
-            out_flat[2 + i] = path[i];
-            out_flat[2 + n + i] = emit[i];
-        }
-    }
+    const int lane = threadIdx.x;
+    const int tok = lane < n ? tokens[lane] : -1;
+    const int par = lane < n ? parents[lane] : -2;
+    const int am = lane < n ? argmax[lane] : -1;
+    accept_greedy_wave(tok, par, am, n, res, out_flat);
 }
 
 hipError_t launch_accept_greedy(const int32_t* tokens, const int32_t* parents,
@@ -856,7 +917,7 @@ hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_
                              const uint16_t* b, int M, int K, int V, const int32_t* banned,
                              int n_banned, float* logits, float* pval, int* pidx,
                              int32_t* out_idx, float* out_max, HeadLse lse, const int* abort,
-                             hipStream_t st) {
+                             hipStream_t st, const GreedyAccept* ga) {
     if (K % 512 != 0 || K > 4096 || M < 1 || n_banned > MJ_HEAD_MAX_BANNED)
         return hipErrorInvalidValue;
     const bool pl4 = (K / 128) % 8 == 0;  // half strip of K / 128 groups: 8-group pieces
@@ -881,9 +942,7 @@ hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_
             launch_timed(k_lm_head_q4<2, 2>, dim3(nb), dim3(512), lds, st, qa);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg,
-                           out_idx + m0, out_max ? out_max + m0 : nullptr, gl, abort);
-        e = hipGetLastError();
+        e = launch_head_final(pval, pidx, nb, M, m0, mg, out_idx, out_max, gl, abort, st, ga);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

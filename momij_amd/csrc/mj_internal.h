@@ -188,10 +188,17 @@ struct HeadLse {
     float* ps;
     float* out;
 };
+// Greedy acceptance of a verify pass over the head's argmax ids (tokens / parents: the step
+// descriptor's rows), folded into the head's final launch.
+struct GreedyAccept {
+    const int32_t* tokens;
+    const int32_t* parents;
+    StepResult* res;
+};
 hipError_t launch_lm_head(const uint16_t* x, const uint16_t* w, int M, int K, int V,
                           const int32_t* banned, int n_banned, float* logits, float* pval,
                           int* pidx, int32_t* out_idx, float* out_max, HeadLse lse,
-                          const int* abort, hipStream_t st);
+                          const int* abort, hipStream_t st, const GreedyAccept* ga = nullptr);
 // Banned ids the 4-bit head stages in LDS (the reference passes at most 16,
 // SeedlessDecodeEngine.swift:470, 496).
 #define MJ_HEAD_MAX_BANNED 64
@@ -199,7 +206,7 @@ hipError_t launch_lm_head_q4(const uint16_t* x, const uint32_t* w, const uint16_
                              const uint16_t* b, int M, int K, int V, const int32_t* banned,
                              int n_banned, float* logits, float* pval, int* pidx,
                              int32_t* out_idx, float* out_max, HeadLse lse, const int* abort,
-                             hipStream_t st);
+                             hipStream_t st, const GreedyAccept* ga = nullptr);
 int head_blocks();
 hipError_t launch_accept_greedy(const int32_t* tokens, const int32_t* parents,
                                 const int32_t* argmax, int n, StepResult* res, int32_t* out_flat,

@@ -4,8 +4,8 @@
 // SeedlessDecodeEngine.swift:194-327, 516-545, 1541-1603): caller-owned weights, a KV ring per
 // layer ([2][n_kv][C][128] fp16, committed position p at slot p % C), scratch sized for
 // MJ_MAX_ROWS rows, an absolute offset (committed tokens).  A verify pass is one stream of
-// kernels (embed -> layers -> final norm -> lm_head -> acceptance -> KV commit -> result copy)
-// with a single host wait.  Per-pass parameters live in a device StepDesc so the pass can be
+// kernels (embed -> layers -> final norm -> lm_head (+ greedy acceptance in its final launch)
+// -> sampled acceptance -> KV commit for a tree -> result copy) with a single host wait.  Per-pass parameters live in a device StepDesc so the pass can be
 // captured once per (kind, rows) into a HIP graph and replayed.
 #include <hip/hip_runtime.h>
 
@@ -22,13 +22,16 @@
 // PASS_SAMPLED_NUC: a sampled pass whose bonus (or zero-mass residual) takes a nucleus.
 // PASS_PEN marks a sampled pass with penalties: the logits are rewritten, so the row maxima are
 // recomputed; without it the lm_head's maxima are used and those launches are left out.
+// PASS_TREE marks a greedy pass over a draft tree that is not a chain: only then can the
+// accepted path leave the rows' KV out of place (path[i] != i), so only then is it compacted.
 enum PassKind {
     PASS_PREFILL = 0,
     PASS_CHAIN = 1,
     PASS_GREEDY = 2,
     PASS_SAMPLED = 3,
     PASS_SAMPLED_NUC = 4,
-    PASS_PEN = 8
+    PASS_PEN = 8,
+    PASS_TREE = 16
 };
 
 static bool sampled_pass(int kind) {
@@ -264,6 +267,11 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
         }
         float* logits =
             (sampled_pass(kind) || m->cap.logits) ? m->logits : nullptr;
+        // a greedy pass's acceptance runs in the head's final launch
+        const int32_t* toks = (const int32_t*)((char*)m->sd_dev + offsetof(StepDesc, tokens));
+        const int32_t* pars = (const int32_t*)((char*)m->sd_dev + offsetof(StepDesc, parents));
+        const GreedyAccept ga{toks, pars, m->res_dev};
+        const GreedyAccept* gap = sampled_pass(kind) ? nullptr : &ga;
         if (m->profiling) m->prof.begin(PROF_HEAD, st);
         if (c.head_bits == 4)
             s = mj_hip(ctx,
@@ -271,12 +279,12 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                          (const uint16_t*)c.lm_head_scales,
                                          (const uint16_t*)c.lm_head_biases, M, H, c.vocab, nullptr,
                                          0, logits, m->pval, m->pidx, m->argmax, m->maxv,
-                                         HeadLse{}, ab, st),
+                                         HeadLse{}, ab, st, gap),
                        "lm_head q4");
         else
             s = mj_hip(ctx, launch_lm_head(m->xf, m->lm_head, M, H, c.vocab, nullptr, 0, logits,
                                            m->pval, m->pidx, m->argmax, m->maxv, HeadLse{}, ab,
-                                           st),
+                                           st, gap),
                        "lm_head");
         if (m->profiling) m->prof.end(st);
         if (s != MJ_OK) return s;
@@ -295,14 +303,9 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
                                                   m->bsum, nullptr, m->res_dev, m->sd_dev, ab, st,
                                                   (kind & PASS_PEN) ? nullptr : m->maxv),
                        "sampled accept");
-        } else {
-            const int32_t* toks = (const int32_t*)((char*)m->sd_dev + offsetof(StepDesc, tokens));
-            const int32_t* pars = (const int32_t*)((char*)m->sd_dev + offsetof(StepDesc, parents));
-            s = mj_hip(ctx, launch_accept_greedy(toks, pars, m->argmax, M, m->res_dev, nullptr, ab,
-                                                 st), "greedy accept");
         }
         if (s != MJ_OK) return s;
-        if (kind == PASS_GREEDY || sampled_pass(kind)) {
+        if (kind & PASS_TREE) {
             s = mj_hip(ctx, launch_kv_commit(m->kv, m->layer_stride, c.n_layers, c.kv_capacity,
                                              c.n_kv_heads, m->sd_dev, m->res_dev, ab, st),
                        "kv commit");
@@ -648,6 +651,7 @@ static mj_status feed_rows(mj_model* m, const int32_t* tokens, const int32_t* pa
     }
     s = fill_tree(m->ctx, sd, parents, M);
     if (s != MJ_OK) return s;
+    if (kind == PASS_GREEDY && !sd->chain) kind |= PASS_TREE;
     return run_pass(m, kind, M);
 }
 

@@ -307,17 +307,23 @@ __global__ __launch_bounds__(64) void k_sample_sums(SampleArgs a) {
     }
 }
 
+// The outcome (acc drafts accepted, then tok), written by the 64 lanes of one wave: lane i
+// writes path[i] and emit[i] (the accepted drafts are read together).
 __device__ __forceinline__ void write_result(const SampleArgs& a, int acc, int tok) {
-    if (a.out) {
+    const int i = threadIdx.x & 63;
+    if (a.out && i == 0) {
         a.out[0] = acc;
         a.out[1] = tok;
     }
     if (a.res) {
-        a.res->accepted = acc;
-        a.res->token = tok;
-        for (int i = 0; i <= acc; ++i) a.res->path[i] = i;
-        for (int i = 0; i < acc; ++i) a.res->emit[i] = a.draft[i];
-        a.res->emit[acc] = tok;
+        if (i == 0) {
+            a.res->accepted = acc;
+            a.res->token = tok;
+        }
+        if (i <= acc) {
+            a.res->path[i] = i;
+            a.res->emit[i] = i < acc ? a.draft[i] : tok;
+        }
     }
 }
 
@@ -342,7 +348,7 @@ __device__ void walk_write(const SampleArgs& a, int row, int fr, bool resid, flo
     __syncthreads();
     const int blk = s_blk;
     if (blk == nb) {  // block-uniform
-        if (t == 0) write_result(a, fr, a.V - 1);
+        if (t < 64) write_result(a, fr, a.V - 1);
         return;
     }
     const int c0 = blk * BLK, n = min(BLK, nch - c0);
@@ -381,7 +387,7 @@ __device__ void walk_write(const SampleArgs& a, int row, int fr, bool resid, flo
         const int ei = wave_first(t < ne && tgt <= Rk);
         tok = cc * CH + (ei < 0 ? ne - 1 : ei);
     }
-    if (t == 0) write_result(a, fr, tok);
+    write_result(a, fr, tok);  // wave 0
 }
 
 // Single block: row totals (with their running totals kept for a walk) and the accept
@@ -612,7 +618,7 @@ __global__ __launch_bounds__(1024) void k_nucleus_pick(SampleArgs a) {
     };
     const float S = blk_sum(kept, a.V, cs, bs, &s_f);
     const int tok = S > 0.0f ? blk_walk(kept, a.V, st.u * S, cs, bs, &s_i) : a.nb.ids_s[0];
-    if (threadIdx.x == 0) write_result(a, st.acc, tok);
+    if (threadIdx.x < 64) write_result(a, st.acc, tok);
 }
 
 static size_t sort_tmp_bytes(int V) {
