@@ -499,29 +499,38 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnArgs a) {
     const int cs = (int)(((int64_t)wv - cg.c0) & 3);  // this wave's first chunk
     const float2* ml = a.mlpart + (size_t)g * a.max_chunks * nq16 + qv;
     const float* op = a.opart + ((size_t)g * a.max_chunks * nq16 + qv) * HD + 2 * lane;
-    float mx = -INFINITY;
-    for (int c = lane; c < nch; c += 64) mx = fmaxf(mx, ml[(size_t)c * nq16].x);
+    // this wave's chunks cb + 4j, j < 4, requested at clamped indices (every lane loads; chunks
+    // past the end are skipped below); two rounds (32 chunks) at once
+    float2 m4[2][4], p4[2][4];
+    const int clast = nch > 0 ? nch - 1 : 0;
+    auto request = [&](int cb, float2* mm, float2* pp) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = min(cb + 4 * j, clast);
+            mm[j] = ml[(size_t)c * nq16];
+            pp[j] = *(const float2*)(op + (size_t)c * nq16 * HD);
+        }
+    };
+    // the first two rounds, together with the chunk maxima (they do not need them)
+    request(cs, m4[0], p4[0]);
+    request(cs + 16, m4[1], p4[1]);
+    // the maximum over the chunks (clamped indices: a repeated chunk leaves it unchanged)
+    float mx = ml[(size_t)min(lane, clast) * nq16].x;
+    for (int c = lane + 64; c < nch; c += 64) mx = fmaxf(mx, ml[(size_t)c * nq16].x);
     mx = wave_max(mx);
     float o0 = 0.0f, o1 = 0.0f, ls = 0.0f;
-    for (int cb = cs; cb < nch; cb += 16) {
-        float2 m4[4], p4[4];
+    for (int cb = cs, rd = 0; cb < nch; cb += 16, ++rd) {
+        if (rd >= 2) request(cb, m4[0], p4[0]);
+        const float2* mm = rd == 1 ? m4[1] : m4[0];
+        const float2* pp = rd == 1 ? p4[1] : p4[0];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int c = cb + 4 * j;
-            m4[j] = make_float2(-INFINITY, 0.0f);
-            p4[j] = make_float2(0.0f, 0.0f);
-            if (c < nch) {
-                m4[j] = ml[(size_t)c * nq16];
-                p4[j] = *(const float2*)(op + (size_t)c * nq16 * HD);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
+            if (cb + 4 * j >= nch) break;
             // log2 units
-            const float w = m4[j].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m4[j].x - mx);
-            ls += m4[j].y * w;
-            o0 += w * p4[j].x;
-            o1 += w * p4[j].y;
+            const float w = mm[j].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mm[j].x - mx);
+            ls += mm[j].y * w;
+            o0 += w * pp[j].x;
+            o1 += w * pp[j].y;
         }
     }
     __shared__ float s_o[4][HD];
