@@ -656,34 +656,87 @@ __device__ __forceinline__ void accept_greedy_wave(int tok, int par, int am, int
     }
 }
 
-// k_head_final over every row of one launch group (M <= 32, a wave a row), then the greedy
-// acceptance from the argmax ids it just formed: one launch where there were two.
-__global__ __launch_bounds__(1024) void k_head_final_accept(const float* pval, const int* pidx,
-                                                            int nblk, int M, int32_t* out_idx,
-                                                            float* out_max, HeadLse lse,
-                                                            const int* abort, GreedyAccept ga) {
+// k_head_final over every row of one launch group (M <= 32; no log-sum-exp), then the greedy
+// acceptance from the argmax ids it just formed: one launch where there were two.  512
+// threads read the partials contiguously: float4 f = t + 512 i of the [nblk][32] arrays is
+// rows 4 (t % 8) .. + 3 of partial block f / 8, so a thread keeps four rows over nblk / 64
+// blocks (one round of requests for nblk <= 512); lanes of one row group meet by shuffles (xor 8, 16, 32), the eight waves in LDS.
+// Highest value, lowest id among equal values: the same pick in any order.
+__device__ __forceinline__ void argmax_merge(float& b, int& i, float v, int j) {
+    if (v > b || (v == b && j < i)) {
+        b = v;
+        i = j;
+    }
+}
+
+__global__ __launch_bounds__(512) void k_head_final_accept(const float* pval, const int* pidx,
+                                                           int nblk, int M, int32_t* out_idx,
+                                                           float* out_max, const int* abort,
+                                                           GreedyAccept ga) {
     if (aborted(abort)) return;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    __shared__ int s_am[32];
-    // the accept's per-row inputs, requested before the fold
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int g = t & 7;                 // row group: rows 4g .. 4g + 3
+    const int ng = (M + 3) >> 2;         // row groups in use
+    __shared__ float s_v[8][32];
+    __shared__ int s_i[8][32];
+    // the accept's per-row inputs, requested with the partials
     const int tok = lane < M ? ga.tokens[lane] : -1;
     const int par = lane < M ? ga.parents[lane] : -2;
-    for (int m = wv; m < M; m += (int)(blockDim.x >> 6)) {
-        const int i = head_fold_row(pval, pidx, nblk, m, lane, out_idx, out_max, lse);
-        if (lane == 0) s_am[m] = i;
+    float b[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    int bi[4] = {0x7fffffff, 0x7fffffff, 0x7fffffff, 0x7fffffff};
+    if (g < ng) {
+        const f4* pv4 = (const f4*)pval;
+        const u4v* pi4 = (const u4v*)pidx;
+        const int F = nblk * 8;  // float4s of each array
+        for (int f0 = t; f0 < F; f0 += 512 * 8) {  // one round for nblk <= 512
+            f4 v[8];
+            u4v j[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int f = min(f0 + 512 * u, F - 8 + g);  // clamped: a repeat changes no pick
+                v[u] = pv4[f];
+                j[u] = pi4[f];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) argmax_merge(b[c], bi[c], v[u][c], (int)j[u][c]);
+        }
+    }
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            argmax_merge(b[c], bi[c], __shfl_xor(b[c], o, MJ_WAVE), __shfl_xor(bi[c], o, MJ_WAVE));
+    if (lane < 8) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            s_v[wv][4 * lane + c] = b[c];
+            s_i[wv][4 * lane + c] = bi[c];
+        }
     }
     __syncthreads();
-    if (wv == 0) accept_greedy_wave(tok, par, lane < M ? s_am[lane] : -1, M, ga.res, nullptr);
+    if (wv != 0) return;
+    float bm = -INFINITY;
+    int im = 0x7fffffff;
+    if (lane < M)
+#pragma unroll
+        for (int w = 0; w < 8; ++w) argmax_merge(bm, im, s_v[w][lane], s_i[w][lane]);
+    if (lane < M) {
+        out_idx[lane] = im;
+        if (out_max) out_max[lane] = bm;
+    }
+    accept_greedy_wave(tok, par, lane < M ? im : -1, M, ga.res, nullptr);
 }
 
 // The fold of rows m0 .. m0 + mg of M.  With ga the greedy acceptance follows: in the same
-// launch when the rows are one group (M <= 32), else after the last group's fold.
+// launch when the rows are one group (M <= 32, no log-sum-exp), else after the last fold.
 static hipError_t launch_head_final(const float* pval, const int* pidx, int nb, int M, int m0,
                                     int mg, int32_t* out_idx, float* out_max, const HeadLse& gl,
                                     const int* abort, hipStream_t st, const GreedyAccept* ga) {
-    if (ga && M <= 32) {
-        hipLaunchKernelGGL(k_head_final_accept, dim3(1), dim3(64 * (mg < 16 ? mg : 16)), 0, st,
-                           pval, pidx, nb, mg, out_idx, out_max, gl, abort, *ga);
+    if (ga && M <= 32 && !gl.out) {
+        hipLaunchKernelGGL(k_head_final_accept, dim3(1), dim3(512), 0, st, pval, pidx, nb, mg,
+                           out_idx, out_max, abort, *ga);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_head_final, dim3(mg), dim3(64), 0, st, pval, pidx, nb, mg, out_idx + m0,
