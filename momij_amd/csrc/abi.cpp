@@ -86,14 +86,9 @@ void* Arena::take(size_t bytes) {
     return p;
 }
 
+// After a synchronisation: the abort word's state from its host copy (no device read).
 mj_status mj_check_abort(mj_ctx* ctx) {
-    int v = 0;
-    mj_status s = mj_hip(ctx, hipMemcpyAsync(&v, ctx->abort_dev, sizeof v, hipMemcpyDeviceToHost,
-                                             ctx->stream), "abort read");
-    if (s != MJ_OK) return s;
-    s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "abort sync");
-    if (s != MJ_OK) return s;
-    return v ? mj_fail(ctx, MJ_ABORTED, "aborted by the abort word") : MJ_OK;
+    return ctx->abort_host.load() ? mj_fail(ctx, MJ_ABORTED, "aborted by the abort word") : MJ_OK;
 }
 
 extern "C" {
@@ -167,7 +162,9 @@ mj_status mj_set_abort(mj_ctx* ctx, int flag) {
     mj_status s = mj_hip(ctx, hipMemcpyAsync(ctx->abort_dev, &v, sizeof v, hipMemcpyHostToDevice,
                                              ctx->stream), "set abort");
     if (s != MJ_OK) return s;
-    return mj_hip(ctx, hipStreamSynchronize(ctx->stream), "set abort sync");
+    s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "set abort sync");
+    if (s == MJ_OK) ctx->abort_host.store(v);
+    return s;
 }
 
 mj_status mj_sync(mj_ctx* ctx) {
