@@ -831,18 +831,20 @@ __global__ __launch_bounds__(256) void k_kv_commit(uint16_t* kv, int64_t layer_s
                                                    int64_t C, int nKV, const StepDesc* sd,
                                                    const StepResult* res, const int* abort) {
     if (aborted(abort)) return;
+    const int t = threadIdx.x;
+    // the accepted count and path (one entry a thread) requested together
     const int acc = res->accepted;
+    const int pv = res->path[t & (MJ_ROWS - 1)];
     const int layer = blockIdx.x / (2 * nKV), rest = blockIdx.x % (2 * nKV);
     uint16_t* base = kv + layer * layer_stride + (int64_t)rest * C * 128;  // K heads then V heads
     const int64_t L = sd->L;
     __shared__ u4v rows[MJ_ROWS][16];
-    const int t = threadIdx.x;
-    bool moved = false;
-    for (int i = 1; i <= acc; ++i) moved |= res->path[i] != i;
-    if (!moved) return;
+    __shared__ int s_path[MJ_ROWS];
+    if (t < MJ_ROWS) s_path[t] = pv;
+    if (!__syncthreads_or(t >= 1 && t <= acc && t < MJ_ROWS && pv != t)) return;  // in place
     for (int idx = t; idx < (acc + 1) * 16; idx += 256) {
         const int i = idx >> 4, part = idx & 15;
-        const int64_t src = (L + res->path[i]) % C;
+        const int64_t src = (L + s_path[i]) % C;
         rows[i][part] = *(const u4v*)(base + src * 128 + 8 * part);
     }
     __syncthreads();
