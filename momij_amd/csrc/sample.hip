@@ -92,7 +92,10 @@ __device__ __forceinline__ float penalize1(float x, int count, float rep, float 
 
 // Row i's penalties: every history token, then every draft d < i that is neither earlier among
 // the drafts nor in the history, each once with its total count (history count + occurrences
-// among drafts 0 .. i-1).  One block per row; each token is written by one thread.
+// among drafts 0 .. i-1).  One block per row; each token is written by one thread.  The drafts
+// sit in LDS; a history entry counts its matches there and marks the drafts it equals (so a
+// draft learns whether the history holds it without searching it); history entries and their
+// logits are requested eight a thread at a time.
 __global__ __launch_bounds__(256) void k_penalize(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
@@ -100,27 +103,45 @@ __global__ __launch_bounds__(256) void k_penalize(SampleArgs a) {
     if (!rep_on && a.o.pres == 0.0f && a.o.freq == 0.0f) return;
     const int i = blockIdx.x, t = threadIdx.x;
     float* l = a.logits + (size_t)i * a.V;
-    for (int j = t; j < a.o.n_hist; j += 256) {
-        const int tok = a.o.hist_tok[j];
-        if (tok < 0 || tok >= a.V) continue;
-        int c = a.o.hist_cnt[j];
-        for (int d = 0; d < i; ++d) c += a.draft[d] == tok;
-        l[tok] = penalize1(l[tok], c, a.o.rep, a.o.pres, a.o.freq);
-    }
-    for (int d = t; d < i; d += 256) {
-        const int tok = a.draft[d];
-        if (tok < 0 || tok >= a.V) continue;
-        bool first = true;
-        for (int e = 0; e < d; ++e) first = first && a.draft[e] != tok;
-        int lo = 0, hi = a.o.n_hist;  // binary search of the ascending history
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (a.o.hist_tok[mid] < tok) lo = mid + 1; else hi = mid;
+    __shared__ int s_draft[MJ_ROWS];
+    __shared__ int s_inh[MJ_ROWS];  // draft d equals a history token
+    if (t < i) s_draft[t] = a.draft[t];
+    if (t < MJ_ROWS) s_inh[t] = 0;
+    __syncthreads();
+    const int nh = a.o.n_hist;
+    for (int j0 = t; j0 < nh; j0 += 256 * 8) {
+        int tok[8], cnt[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = min(j0 + 256 * u, nh - 1);
+            tok[u] = a.o.hist_tok[j];
+            cnt[u] = a.o.hist_cnt[j];
         }
-        const bool in_hist = lo < a.o.n_hist && a.o.hist_tok[lo] == tok;
-        if (!first || in_hist) continue;
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const bool ok = j0 + 256 * u < nh && tok[u] >= 0 && tok[u] < a.V;
+            x[u] = ok ? l[tok[u]] : 0.0f;
+            for (int d = 0; d < i; ++d)
+                if (s_draft[d] == tok[u] && j0 + 256 * u < nh) {
+                    ++cnt[u];
+                    s_inh[d] = 1;
+                }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (j0 + 256 * u < nh && tok[u] >= 0 && tok[u] < a.V)
+                l[tok[u]] = penalize1(x[u], cnt[u], a.o.rep, a.o.pres, a.o.freq);
+    }
+    __syncthreads();
+    for (int d = t; d < i; d += 256) {
+        const int tok = s_draft[d];
+        if (tok < 0 || tok >= a.V || s_inh[d]) continue;
+        bool first = true;
+        for (int e = 0; e < d; ++e) first = first && s_draft[e] != tok;
+        if (!first) continue;
         int c = 0;
-        for (int e = 0; e < i; ++e) c += a.draft[e] == tok;
+        for (int e = 0; e < i; ++e) c += s_draft[e] == tok;
         l[tok] = penalize1(l[tok], c, a.o.rep, a.o.pres, a.o.freq);
     }
 }
