@@ -159,11 +159,14 @@ void* mj_get_stream(const mj_ctx* ctx) { return ctx ? (void*)ctx->stream : nullp
 mj_status mj_set_abort(mj_ctx* ctx, int flag) {
     if (!ctx) return MJ_INVALID_ARG;
     const int v = flag ? 1 : 0;
+    // the host copy is set before the device word can be, and cleared only once the device word
+    // is: a pass whose kernels saw the word set is always reported aborted
+    if (v) ctx->abort_host.store(1);
     mj_status s = mj_hip(ctx, hipMemcpyAsync(ctx->abort_dev, &v, sizeof v, hipMemcpyHostToDevice,
                                              ctx->stream), "set abort");
     if (s != MJ_OK) return s;
     s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "set abort sync");
-    if (s == MJ_OK) ctx->abort_host.store(v);
+    if (s == MJ_OK && !v) ctx->abort_host.store(0);
     return s;
 }
 

@@ -13,8 +13,8 @@ struct mj_ctx {
     hipStream_t own = nullptr;     // the context's own stream (default priority)
     hipStream_t stream = nullptr;  // stream in use (own, or a caller's)
     int* abort_dev = nullptr;      // device abort word (stopBuf)
-    // its host copy: mj_set_abort is the word's only writer and returns once the device word
-    // holds the value, so this mirrors it for every call that could observe it
+    // its host copy, kept by the word's only writer (mj_set_abort): set before the device word,
+    // cleared after it, so a synchronised call never misses an abort its kernels saw
     std::atomic<int> abort_host{0};
     void* scratch = nullptr;       // op-level scratch arena
     size_t scratch_bytes = 0;
