@@ -54,11 +54,19 @@ int mj_abi_version(void);
 /* Use an external hipStream_t (e.g. the caller's current stream); NULL restores the own one. */
 mj_status mj_set_stream(mj_ctx* ctx, void* hip_stream);
 void* mj_get_stream(const mj_ctx* ctx);
-/* Device abort word (stopBuf): non-zero makes every kernel of this context return early and
- * the next synchronising call report MJ_ABORTED.  Cleared with flag = 0. */
+/* Abort word (stopBuf, SeedlessMetal.swift:60, 69-70): non-zero makes every kernel of this
+ * context that starts after the call return early.  Safe from any thread at any time, also
+ * while the owning thread's pass is queued, running or being captured into a graph: the word is
+ * written by a copy on a stream of the context's own that no pass uses, and mj_set_abort waits
+ * for that copy only.  A synchronising call (mj_sync, mj_prefill's chunks, the verify and step
+ * calls) reports MJ_ABORTED when the word is set at its entry (then nothing is queued) or at its
+ * end, or was set at any time in between -- whenever some of its kernels may have skipped their
+ * work -- and its results are then void (a model's offset does not advance).  Cleared with
+ * flag = 0; the next call runs normally. */
 mj_status mj_set_abort(mj_ctx* ctx, int flag);
 /* One wait for everything queued (cb.commit + waitUntilCompleted,
- * SeedlessDecodeEngine.swift:324-325).  Reports MJ_ABORTED if the abort word was set. */
+ * SeedlessDecodeEngine.swift:324-325).  Reports MJ_ABORTED if the abort word is set or was set
+ * since the previous synchronising call. */
 mj_status mj_sync(mj_ctx* ctx);
 
 /* ---------------------------------------------------------------- memory ----- */
@@ -126,7 +134,10 @@ mj_status mj_moe_block(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void
  * exceed it (M rows x top_k x (I + H) halves dominate: H <= 2048 fits any I <= 4096 at
  * M = 64) is refused with MJ_CAPACITY before any work is queued.  Every call on one GPU shares
  * that GPU's array, which keeps the last call's contents: calls that overlap on one GPU (from
- * several contexts or streams) race. */
+ * several contexts, or one context whose stream mj_set_stream changed between calls) race, so
+ * the caller must order them -- issue them on one stream, or make each stream wait for the
+ * previous call's completion event.  No synchronisation is added here: a wait on an event
+ * recorded outside a graph capture would break the capture this entry point exists for. */
 #define MJ_MOE_NOALLOC_BYTES (8u << 20)
 mj_status mj_moe_block_noalloc(mj_ctx* ctx, const mj_moe_weights* w, const void* x, void* y,
                                int M, int flags, int32_t* out_inds, float* out_scores);
@@ -205,7 +216,9 @@ mj_status mj_accept_greedy(mj_ctx* ctx, const int32_t* tokens, const int32_t* pa
  * (SpeculativeSampling.swift:27-99) with LogitsProcessor.probabilities / samplePrepared
  * (LogitsProcessor.swift:116-189), no penalties.  logits fp32 [rows][V] device (row i = target
  * after feed i), draft int32 [rows-1] device.  q_mode MJ_Q_POINT: q = q_point[i] at the draft
- * token (q_point device nullable = 1, the reference default); MJ_Q_UNIFORM: q = 1/V.
+ * token (q_point: a DEVICE float array [rows-1], read by the kernels; NULL = 1 on every draft, the
+ * reference default); MJ_Q_UNIFORM: q = 1/V.  q < 0 counts as 0 (max(0, draftQ)): such a
+ * draft is rejected without a uniform and the residual is the target itself.
  * Uniforms: Philox4x32-10, key = seed, counter = (row, counter lo, counter hi, 0x6d6a6a76),
  * u0 = accept test, u1 = residual walk (row rows-1: u0 = bonus).  Sums and walks use a fixed
  * blocked order (16-element chunks, 64-chunk blocks) so results are reproducible bit for bit.
@@ -305,7 +318,10 @@ mj_status mj_verify_greedy(mj_model* model, int32_t y, const int32_t* draft, int
 
 /* verifyDraftSampled (SeedlessDecodeEngine.swift:1541-1571) over the exact fp16 head and the
  * full vocabulary (chain drafts): one pass, device-side sampled acceptance (mj_accept_sampled
- * rules), commit accepted + 1 rows.  out_token = resampled token or bonus. */
+ * rules), commit accepted + 1 rows.  out_token = resampled token or bonus.  Unlike
+ * mj_accept_sampled, draft and q_point are HOST arrays here: q_point float [n_draft] holds
+ * draftQ (qAlong's q on draft i, mergedDraftQ at SeedlessDecodeEngine.swift:1530-1538) and is
+ * copied into the pass's descriptor; NULL = 1 on every draft. */
 mj_status mj_verify_sampled(mj_model* model, int32_t y, const int32_t* draft, int n_draft,
                             float temperature, int q_mode, const float* q_point, uint64_t seed,
                             uint64_t counter, int32_t* out_accepted, int32_t* out_token);

@@ -86,9 +86,20 @@ void* Arena::take(size_t bytes) {
     return p;
 }
 
-// After a synchronisation: the abort word's state from its host copy (no device read).
-mj_status mj_check_abort(mj_ctx* ctx) {
-    return ctx->abort_host.load() ? mj_fail(ctx, MJ_ABORTED, "aborted by the abort word") : MJ_OK;
+// Both report each set once to the owning thread: the generation they have seen becomes the
+// reference of the next mj_sync.
+mj_status mj_abort_begin(mj_ctx* ctx, unsigned* gen) {
+    *gen = ctx->abort_gen.load();
+    if (!ctx->abort_host.load()) return MJ_OK;
+    ctx->synced_gen = *gen;
+    return mj_fail(ctx, MJ_ABORTED, "aborted by the abort word");
+}
+
+mj_status mj_abort_end(mj_ctx* ctx, unsigned gen) {
+    const unsigned now = ctx->abort_gen.load();
+    const bool ab = ctx->abort_host.load() || now != gen;
+    ctx->synced_gen = now;
+    return ab ? mj_fail(ctx, MJ_ABORTED, "aborted by the abort word") : MJ_OK;
 }
 
 extern "C" {
@@ -124,12 +135,16 @@ mj_status mj_init(int device, mj_ctx** out) {
     mj_ctx* c = new mj_ctx();
     c->device = device;
     if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&c->ctl, hipStreamNonBlocking) != hipSuccess ||
+        hipHostMalloc(&c->abort_src, 2 * sizeof(int), hipHostMallocDefault) != hipSuccess ||
         hipMalloc(&c->abort_dev, sizeof(int)) != hipSuccess ||
         hipMemset(c->abort_dev, 0, sizeof(int)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
-        delete c;
+        mj_destroy(c);
         return MJ_HIP_ERROR;
     }
+    c->abort_src[0] = 0;
+    c->abort_src[1] = 1;
     c->stream = c->own;
     *out = c;
     return MJ_OK;
@@ -139,9 +154,12 @@ mj_status mj_destroy(mj_ctx* ctx) {
     if (!ctx) return MJ_INVALID_ARG;
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
+    if (ctx->ctl) hipStreamSynchronize(ctx->ctl);
     if (ctx->scratch) hipFree(ctx->scratch);
     if (ctx->abort_dev) hipFree(ctx->abort_dev);
+    if (ctx->abort_src) hipHostFree(ctx->abort_src);
     if (ctx->own) hipStreamDestroy(ctx->own);
+    if (ctx->ctl) hipStreamDestroy(ctx->ctl);
     delete ctx;
     return MJ_OK;
 }
@@ -156,25 +174,37 @@ mj_status mj_set_stream(mj_ctx* ctx, void* s) {
 
 void* mj_get_stream(const mj_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
 
+// Any thread, at any time: the word is written by a copy on the context's control stream,
+// never on the stream passes run (or are captured) on.  Errors of the copy are returned, not
+// recorded in the context's message (the owning thread may be reading it).
 mj_status mj_set_abort(mj_ctx* ctx, int flag) {
     if (!ctx) return MJ_INVALID_ARG;
     const int v = flag ? 1 : 0;
-    // the host copy is set before the device word can be, and cleared only once the device word
-    // is: a pass whose kernels saw the word set is always reported aborted
-    if (v) ctx->abort_host.store(1);
-    mj_status s = mj_hip(ctx, hipMemcpyAsync(ctx->abort_dev, &v, sizeof v, hipMemcpyHostToDevice,
-                                             ctx->stream), "set abort");
-    if (s != MJ_OK) return s;
-    s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "set abort sync");
-    if (s == MJ_OK && !v) ctx->abort_host.store(0);
-    return s;
+    std::lock_guard<std::mutex> lock(ctx->abort_mu);
+    int prev = -1;
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (hipSetDevice(ctx->device) != hipSuccess) return MJ_HIP_ERROR;
+    // set: the generation and the host mirror move before the device word can; clear: the
+    // mirror follows the device word
+    if (v) {
+        ctx->abort_gen.fetch_add(1);
+        ctx->abort_host.store(1);
+    }
+    hipError_t e = hipMemcpyAsync(ctx->abort_dev, ctx->abort_src + v, sizeof(int),
+                                  hipMemcpyHostToDevice, ctx->ctl);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->ctl);
+    if (e == hipSuccess && !v) ctx->abort_host.store(0);
+    if (prev >= 0) hipSetDevice(prev);
+    return e == hipSuccess ? MJ_OK : MJ_HIP_ERROR;
 }
 
+// Reports MJ_ABORTED when the word is set, or was set since the previous synchronising call:
+// the work queued in between may have been skipped.
 mj_status mj_sync(mj_ctx* ctx) {
     if (!ctx) return MJ_INVALID_ARG;
     mj_status s = mj_hip(ctx, hipStreamSynchronize(ctx->stream), "sync");
     if (s != MJ_OK) return s;
-    return mj_check_abort(ctx);
+    return mj_abort_end(ctx, ctx->synced_gen);
 }
 
 mj_status mj_alloc(mj_ctx* ctx, size_t bytes, void** out) {

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/momij_hip.h"
@@ -12,10 +13,20 @@ struct mj_ctx {
     int device = 0;
     hipStream_t own = nullptr;     // the context's own stream (default priority)
     hipStream_t stream = nullptr;  // stream in use (own, or a caller's)
-    int* abort_dev = nullptr;      // device abort word (stopBuf)
-    // its host copy, kept by the word's only writer (mj_set_abort): set before the device word,
-    // cleared after it, so a synchronised call never misses an abort its kernels saw
+    // Abort word (stopBuf).  abort_dev is what kernels read; only mj_set_abort writes it, with a
+    // copy on `ctl`, a stream of its own that no pass runs or is captured on, so any thread may
+    // set it while a pass is queued, running or being captured, and kernels that start after
+    // the copy see it.  abort_host mirrors it (set before the device word, cleared after it);
+    // abort_gen counts the sets.  A call reports MJ_ABORTED when the word was set at its entry
+    // or at its end, or was set in between (the generation moved): whenever its kernels may
+    // have seen the word set.
+    int* abort_dev = nullptr;
+    hipStream_t ctl = nullptr;
+    int* abort_src = nullptr;      // pinned {0, 1}: the copies' sources
     std::atomic<int> abort_host{0};
+    std::atomic<unsigned> abort_gen{0};
+    unsigned synced_gen = 0;       // abort_gen the owning thread's last synchronising call saw
+    std::mutex abort_mu;           // one set or clear at a time
     void* scratch = nullptr;       // op-level scratch arena
     size_t scratch_bytes = 0;
     std::string err;
@@ -75,7 +86,10 @@ struct Prof {
 mj_status mj_fail(mj_ctx* ctx, mj_status st, const char* fmt, ...);
 mj_status mj_hip(mj_ctx* ctx, hipError_t e, const char* what);
 mj_status mj_scratch_reserve(mj_ctx* ctx, size_t bytes);
-mj_status mj_check_abort(mj_ctx* ctx);
+// The abort word around one synchronising call: begin at its entry (MJ_ABORTED, and nothing
+// queued, if the word is set; *gen receives the generation), end after its wait.
+mj_status mj_abort_begin(mj_ctx* ctx, unsigned* gen);
+mj_status mj_abort_end(mj_ctx* ctx, unsigned gen);
 // Scratch of an MoE block call laid out over an arena (base nullptr: size counting only).
 void moe_scratch_layout(Arena& a, int H, int I, int E, int k, int M, MoeScratch& ms);
 mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms);

@@ -321,9 +321,12 @@ static mj_status enqueue_pass(mj_model* m, int kind, int M, hipStream_t st) {
 static mj_status run_pass(mj_model* m, int kind, int M) {
     mj_ctx* ctx = m->ctx;
     hipStream_t st = ctx->stream;
+    unsigned gen = 0;
+    mj_status s = mj_abort_begin(ctx, &gen);  // set: nothing is queued
+    if (s != MJ_OK) return s;
     hipSetDevice(ctx->device);
-    mj_status s = mj_hip(ctx, hipMemcpyAsync(m->sd_dev, m->sd_host, sizeof(StepDesc),
-                                             hipMemcpyHostToDevice, st), "descriptor upload");
+    s = mj_hip(ctx, hipMemcpyAsync(m->sd_dev, m->sd_host, sizeof(StepDesc),
+                                   hipMemcpyHostToDevice, st), "descriptor upload");
     if (s != MJ_OK) return s;
     const mj_capture& cp = m->cap;
     const bool capturing = cp.h || cp.inds || cp.logits || cp.attn_out || cp.moe_in ||
@@ -381,7 +384,7 @@ static mj_status run_pass(mj_model* m, int kind, int M) {
             }
         }
     }
-    return mj_check_abort(ctx);
+    return mj_abort_end(ctx, gen);
 }
 
 static mj_status check_rows(mj_model* m, int M) {

@@ -192,11 +192,6 @@ void or_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, int
     }
 }
 
-/* resid_add -- SeedlessMetal.swift:2528-2539: h = half(h + delta) */
-void or_resid_add(uint16_t* h, const uint16_t* delta, int M, int H) {
-    for (size_t i = 0; i < (size_t)M * H; ++i) h[i] = or_f2h(or_h2f(h[i]) + or_h2f(delta[i]));
-}
-
 /* Router logits -- SeedlessMetal.swift:2574-2595: y[m,e] = sum_k W[e,k] * x[m,k] (fp32 out) */
 void or_router_logits(const uint16_t* W, const uint16_t* x, float* logits, int M, int E, int H) {
     for (int m = 0; m < M; ++m)

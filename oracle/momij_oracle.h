@@ -58,7 +58,6 @@ void or_score_resid(const uint16_t* down, const float* scores, uint16_t* h,
 
 /* ---- a4: norm / router ---------------------------------------------------- */
 void or_rms_norm(const uint16_t* x, const uint16_t* w, uint16_t* out, int M, int H, float eps);
-void or_resid_add(uint16_t* h, const uint16_t* delta, int M, int H);
 void or_router_logits(const uint16_t* W, const uint16_t* x, float* logits, int M, int E, int H);
 void or_route_topk(const float* logits, int32_t* inds, float* scores, int M, int E, int k);
 

@@ -41,3 +41,29 @@ def assert_close(got, ref, rel_tol=REL_NORM_TOL, abs_tol=ABS_TOL, what=""):
               f"row: {bad.sum(axis=1).tolist()}", flush=True)
     assert rel <= rel_tol and mx <= abs_tol, (what, rel, mx)
     return rel, mx
+
+
+def draft_q_values(rng, logits, draft, T):
+    """Draft densities q_i as a suffix-tree draft source gives them (qAlong: child count over
+    sibling mass, floored at 1e-6, 1 past the matched path), mixed with q = 0 (always rejected),
+    and q near the target's own p on the draft (accept probability strictly inside (0, 1))."""
+    q = np.empty(len(draft), np.float32)
+    for i, d in enumerate(draft):
+        l = logits[i].astype(np.float64) / T
+        p = np.exp(l - l.max())
+        pd = p[d] / p.sum()
+        kind = int(rng.integers(0, 6))
+        if kind == 0:
+            q[i] = 0.0
+        elif kind == 1:
+            q[i] = 1e-6
+        elif kind == 2:
+            b = int(rng.integers(2, 8))
+            q[i] = float(rng.integers(1, b + 1)) / b
+        elif kind == 3:
+            q[i] = min(1.0, pd * rng.uniform(0.4, 3.0))
+        elif kind == 4:
+            q[i] = 1.0
+        else:
+            q[i] = rng.uniform(0.0, 1.0)
+    return q

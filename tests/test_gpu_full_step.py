@@ -69,7 +69,8 @@ def full():
     w = dict(layers={l: host_layer(layers[l]) for l in LAYERS},
              routers=[host(layers[l]["moe"]["router_w"]) for l in range(cfg.n_layers)],
              head=host(head))
-    yield dict(ctx=ctx, cfg=cfg, eng=eng, y=y, rng=rng, w=w, cont=_greedy(eng, y, 8))
+    yield dict(ctx=ctx, cfg=cfg, eng=eng, y=y, rng=rng, w=w, cont=_greedy(eng, y, 8),
+               prompt=prompt)
     eng.close()
     ctx.close()
 
@@ -172,3 +173,46 @@ def test_full_tree16_commit_and_next_pass(full, orc):
     oacc, _, oemit = orc.accept_greedy([y2] + draft, None, am)
     assert oacc == acc2 and list(oemit) == toks2
     eng.rewind(L0)
+
+
+def test_abort_from_another_thread_during_prefill(full):
+    """stopBuf from a cancelling thread (SeedlessMetal.swift:60, 69-70): a second host thread
+    sets the abort word while mj_prefill of the 2048-token prompt runs (32 chunks of 64 rows).
+    The call returns MJ_ABORTED with no HIP error and the offset at a whole chunk before the
+    end; every kernel of the pass in flight exits normally (the next calls succeed); after the
+    word is cleared a prefill from the start gives the same next token and greedy continuation
+    as the uninterrupted one."""
+    import threading
+    import time
+
+    from momij_amd._lib import MomijError
+
+    ctx, eng = full["ctx"], full["eng"]
+    eng.rewind(0)
+    t0 = time.perf_counter()
+    y = eng.prefill(full["prompt"], chunk=64)
+    t_full = time.perf_counter() - t0
+    assert y == full["y"]
+    eng.rewind(0)
+    delay = max(0.2 * t_full, 0.002)
+    timer = threading.Timer(delay, lambda: ctx.set_abort(True))
+    timer.start()
+    try:
+        with pytest.raises(MomijError) as e:
+            eng.prefill(full["prompt"], chunk=64)
+    finally:
+        timer.join()
+    print(f"prefill {t_full * 1e3:.1f} ms, abort after {delay * 1e3:.1f} ms: offset "
+          f"{eng.offset}", flush=True)
+    assert e.value.status == 5, e.value
+    assert eng.offset % 64 == 0 and eng.offset < 2048
+    # still set: the next call queues nothing and reports the abort
+    with pytest.raises(MomijError) as e2:
+        eng.step_chain_feeds([y])
+    assert e2.value.status == 5
+    ctx.set_abort(False)
+    ctx.sync()
+    eng.rewind(0)
+    assert eng.prefill(full["prompt"], chunk=64) == full["y"]
+    assert eng.offset == 2048
+    assert _greedy(eng, full["y"], 3) == full["cont"][:3]

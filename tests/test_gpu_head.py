@@ -9,7 +9,7 @@ checked to exceed the fp32 accumulation error bound, so the match is not luck.
 import numpy as np
 import pytest
 
-from tests.gpu_util import assert_close, dev, host
+from tests.gpu_util import assert_close, dev, draft_q_values, host
 
 pytestmark = pytest.mark.gpu
 
@@ -290,6 +290,46 @@ def test_accept_sampled_ex_bit_exact(ctx, head_case, orc, opts):
         seen[ref[0]] = seen.get(ref[0], 0) + 1
     assert (host(logits).view(np.uint32) == lh.view(np.uint32)).all()
     print("accepted-count histogram", opts, seen, flush=True)
+
+
+@pytest.mark.parametrize("opts", [None, dict(top_p=0.6, rep=1.3, pres=0.4, freq=0.25)])
+def test_accept_sampled_point_q_bit_exact(ctx, head_case, orc, opts):
+    """Fractional draft densities (qAlong-like count ratios, 1e-6, q = 0, q near p) passed as a
+    device array q_point to mj_accept_sampled(_ex): accept count and emitted token bit for bit
+    against the oracle on the same logits, q and uniforms, over the full 151936-token head."""
+    import torch
+
+    am = head_case["am"]
+    logits = head_case["logits"]
+    lh = host(logits)
+    rng = np.random.default_rng(57 if opts is None else 58)
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    seen = {}
+    for trial in range(16):
+        draft = am[:M - 1].copy()
+        for i in range(6, M - 1):
+            draft[i] = rng.integers(0, V)
+        qp = draft_q_values(rng, lh, draft, 0.7)
+        dd, dq = dev(draft.astype(np.int32)), dev(qp)
+        u = orc.verify_uniforms(4049, trial, M)
+        torch.cuda.synchronize()
+        if opts is None:
+            ctx.accept_sampled(logits, M, V, dd, 0.7, 0, 4049, trial, out, q_point=dq)
+            ref = orc.accept_sampled(lh, draft, 0.7, 0, u, q_point=qp)
+        else:
+            hist = {int(t): int(c) for t, c in zip(rng.integers(0, V, 100), rng.integers(0, 4, 100))}
+            ctx.accept_sampled_ex(logits, M, V, dd, 0, 4049, trial, out, 0.7, hist=hist,
+                                  q_point=dq, **opts)
+            ht = np.array(list(hist.keys()), np.int32)
+            hc = np.array([hist[t] for t in ht.tolist()], np.int32)
+            ref = orc.accept_sampled_ex(lh, draft, 0.7, 0, u, q_point=qp, hist_tok=ht,
+                                        hist_cnt=hc, **opts)
+        ctx.sync()
+        got = tuple(int(v) for v in host(out))
+        assert got == ref, (trial, qp.tolist(), got, ref)
+        seen[ref[0]] = seen.get(ref[0], 0) + 1
+    print("accepted-count histogram (point q)", opts, seen, flush=True)
+    assert len(seen) >= 2
 
 
 @pytest.mark.parametrize("Vs,off,opts", [

@@ -18,7 +18,7 @@ vocabulary and window so the oracle can replay everything) is checked end to end
 import numpy as np
 import pytest
 
-from tests.gpu_util import assert_close, host
+from tests.gpu_util import assert_close, draft_q_values, host
 from tests.teacher import capture_pass, check_head, check_layer
 
 pytestmark = pytest.mark.gpu
@@ -327,6 +327,78 @@ def test_sampled_verify_ex_bit_exact(model, orc, q_mode):
             eng.rewind(L0)
             assert eng.verify_sampled_ex(y, draft, q_mode, 123, trial, 0.7, hist=hh,
                                          **o) == (acc, tok)
+
+
+@pytest.mark.parametrize("ex", [False, True])
+def test_sampled_verify_point_q_bit_exact(model, orc, ex):
+    """mj_verify_sampled(_ex) with a host array q_point of draft densities: from a suffix index
+    over the prompt (qAlong, the draftQ of verifyDraftSampled, SeedlessDecodeEngine.swift:
+    1530-1559) on even trials, from the mixed generator (0, 1e-6, count ratios, q near p) on odd
+    ones.  Decisions bit for bit against the oracle on the pass's own logits; a graph replay of
+    the same inputs decides the same."""
+    import torch
+
+    from momij_amd.drafts import SuffixDraftIndex
+
+    eng, cfg = model["eng"], model["cfg"]
+    rng = np.random.default_rng(70 + ex)
+    eng.rewind(0)
+    prompt = rng.integers(0, cfg.vocab, 60).tolist()
+    y = eng.prefill(prompt)
+    cont = greedy_continuation(eng, y, 8)
+    L0 = eng.offset
+    cap = torch.empty((64, cfg.vocab), dtype=torch.float32, device="cuda")
+    idx = SuffixDraftIndex(16)
+    # the prompt and continuations that share its last five tokens and leave the greedy path
+    # after 2, 1, 1 and 0 tokens: qAlong from that five-token context gives count ratios
+    # (4/5, 1/2, 1/2, then 1 along the prompt's own path)
+    idx.insert(prompt + [y] + cont)
+    tail = prompt[-4:] + [y]
+    for pre in (cont[:2], cont[:1], cont[:1], []):
+        idx.insert(tail + pre + [int(t) for t in rng.integers(0, cfg.vocab, 3)])
+    ctx_hist = [(prompt[-5] + 1) % cfg.vocab] + tail  # longest matched suffix: the five tokens
+    o = dict(top_p=0.7, rep=1.2, pres=0.3, freq=0.2) if ex else {}
+    hist = {int(t): 1 for t in prompt[-20:]} if ex else None
+    seen = {}
+    for trial in range(8):
+        draft = cont[:5] + [int(t) for t in rng.integers(0, cfg.vocab, 3)]
+        eng.rewind(L0)
+        if trial % 2 == 0:
+            qp = np.array(idx.q_along(ctx_hist, draft), np.float32)
+            assert (qp[:3] < 1).all(), qp
+        else:
+            eng.set_capture(logits=cap)
+            eng.verify_greedy(y, draft)  # this pass's logits, to place q near p
+            eng.set_capture()
+            eng.rewind(L0)
+            qp = draft_q_values(rng, host(cap)[:8], draft, 0.7)
+        eng.set_capture(logits=cap)
+        if ex:
+            acc, tok = eng.verify_sampled_ex(y, draft, 0, 321, trial, 0.7, hist=hist, q_point=qp,
+                                             **o)
+        else:
+            acc, tok = eng.verify_sampled(y, draft, 0.7, 0, seed=321, counter=trial, q_point=qp)
+        eng.set_capture()
+        lg = host(cap)[:9]
+        u = orc.verify_uniforms(321, trial, 9)
+        if ex:
+            ht = np.array(list(hist.keys()), np.int32)
+            hc = np.array([hist[t] for t in ht.tolist()], np.int32)
+            ref = orc.accept_sampled_ex(lg, np.array(draft, np.int32), 0.7, 0, u, q_point=qp,
+                                        hist_tok=ht, hist_cnt=hc, **o)
+        else:
+            ref = orc.accept_sampled(lg, np.array(draft, np.int32), 0.7, 0, u, q_point=qp)
+        assert (acc, tok) == ref, (trial, qp.tolist(), acc, tok, ref)
+        assert eng.offset == L0 + acc + 1
+        eng.rewind(L0)
+        if ex:
+            again = eng.verify_sampled_ex(y, draft, 0, 321, trial, 0.7, hist=hist, q_point=qp, **o)
+        else:
+            again = eng.verify_sampled(y, draft, 0.7, 0, seed=321, counter=trial, q_point=qp)
+        assert again == (acc, tok), (trial, again, acc, tok)
+        seen[acc] = seen.get(acc, 0) + 1
+    print("sampled (point q) accepted histogram", ex, seen, flush=True)
+    assert len(seen) >= 2
 
 
 def test_graph_replays_equal_eager(model):

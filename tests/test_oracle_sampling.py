@@ -17,6 +17,8 @@ or_accept_sampled_ex.
 import numpy as np
 import pytest
 
+from tests.gpu_util import draft_q_values as _q_values
+
 
 # ---------------------------------------------------------------- float64 statement ------
 def _penalize64(l, hist, extra, rep, pres, freq, order="rpf"):
@@ -65,11 +67,24 @@ def _nucleus64(e, top_p, u, short=False):
     return tok, min(near, near_cut)
 
 
-def _accept64(logits, draft, T, q_mode, u, top_p, rep, pres, freq, hist, plant=None):
+def _accept64(logits, draft, T, q_mode, u, top_p, rep, pres, freq, hist, plant=None,
+              q_point=None):
+    """tryAccept / walkDraft in float64.  q_point (point mode): the draft density q_i on draft i
+    (qAlong), max(0, q_i); None = 1 on every draft.  Plants: "q_row" reads q from the previous
+    row, "q_one" ignores q_point, "q_resid" leaves the draft's mass in the residual."""
     rows, V = logits.shape
     D = rows - 1
     nuc = top_p < 1 - 1e-6
     near = 1.0
+
+    def q_of(i):
+        if q_mode == 1:
+            return 1.0 / V
+        if q_point is None or plant == "q_one":
+            return 1.0
+        j = (i - 1) % D if plant == "q_row" else i
+        return max(0.0, float(np.float32(q_point[j])))
+
     for i in range(rows):
         extra = [] if plant == "no_drafts" else list(draft[:i])
         order = "prf" if plant == "order" else "rpf"
@@ -84,13 +99,14 @@ def _accept64(logits, draft, T, q_mode, u, top_p, rep, pres, freq, hist, plant=N
             return D, tok, min(near, n2)
         p = e / Z
         d = draft[i]
-        q = 1.0 / V if q_mode == 1 else 1.0
-        if p[d] > 0 and u[i, 0] <= min(1.0, p[d] / q):
-            near = min(near, abs(u[i, 0] - min(1.0, p[d] / q)))
-            continue
-        near = min(near, abs(u[i, 0] - min(1.0, p[d] / q)))
+        q = q_of(i)
+        if q > 0 and p[d] > 0:
+            edge = abs(u[i, 0] - min(1.0, p[d] / q))
+            near = min(near, edge)
+            if u[i, 0] <= min(1.0, p[d] / q):
+                continue
         r = np.maximum(p - q, 0) if q_mode == 1 else p.copy()
-        if q_mode == 0:
+        if q_mode == 0 and q > 0 and plant != "q_resid":
             r[d] = max(0.0, r[d] - q)
         if r.sum() > 0:
             tok, n2 = _walk64(r, u[i, 1] * r.sum())
@@ -242,3 +258,61 @@ def test_nucleus_vs_float64(orc):
         stok, _ = _nucleus64(e.astype(np.float64), top_p, u, short=True)
         short_miss += stok != tok
     assert ambiguous <= 3 and short_miss >= 10
+
+
+# ---------------------------------------------------------------- fractional draft q ----
+@pytest.mark.parametrize("ex", [False, True])
+@pytest.mark.parametrize("gen", ["random", "sharp"])
+def test_accept_sampled_point_q_vs_float64(orc, gen, ex):
+    """tryAccept with the draft density of a draft source (draftQ from qAlong,
+    SeedlessDecodeEngine.swift:1530-1559; SpeculativeSampling.swift:27-59): accept iff q > 0,
+    p > 0 and u <= min(1, p / q), else the residual p with the draft's mass reduced by q.  The
+    oracle agrees with the float64 statement on the same uniforms; planted mistakes -- q taken
+    from the previous row, q ignored (1 everywhere), the draft's mass left in the residual --
+    disagree on several of the same cases."""
+    T = 0.8
+    ambiguous = agree = 0
+    planted_miss = {"q_row": 0, "q_one": 0, "q_resid": 0}
+    cases = _cases(80 + ex, 80) if gen == "random" else _sharp_cases(90 + ex, 80)
+    for trial, logits, draft, ht, hc, opts in cases:
+        rng = np.random.default_rng(1000 + trial)
+        qp = _q_values(rng, logits, draft, T)
+        u = orc.verify_uniforms(700 + trial, 5, logits.shape[0])
+        if ex:
+            acc, tok = orc.accept_sampled_ex(logits, draft, T, 0, u, q_point=qp, hist_tok=ht,
+                                             hist_cnt=hc, **opts)
+            hist = dict(zip(ht.tolist(), hc.tolist()))
+            o = (opts["top_p"], opts["rep"], opts["pres"], opts["freq"], hist)
+        else:
+            acc, tok = orc.accept_sampled(logits, draft, T, 0, u, q_point=qp)
+            o = (1.0, 1.0, 0.0, 0.0, {})
+        racc, rtok, near = _accept64(logits, draft, T, 0, u, *o, q_point=qp)
+        if (acc, tok) != (racc, rtok):
+            ambiguous += 1
+            assert near < 1e-5, (trial, acc, tok, racc, rtok, near)
+            continue
+        agree += 1
+        for plant in planted_miss:
+            pacc, ptok, _ = _accept64(logits, draft, T, 0, u, *o, plant=plant, q_point=qp)
+            planted_miss[plant] += (pacc, ptok) != (acc, tok)
+    assert ambiguous <= 3 and agree >= 70
+    print(gen, ex, "agree", agree, "ambiguous", ambiguous, "planted", planted_miss)
+    assert all(v >= 3 for v in planted_miss.values()), planted_miss
+
+
+def test_point_q_extremes(orc):
+    """q = 0 rejects every draft (no uniform can accept it) and samples the target itself;
+    q below p accepts with certainty; q = 1 is the reference default (q_point NULL)."""
+    rng = np.random.default_rng(12)
+    V, rows = 300, 4
+    for trial in range(30):
+        logits = (rng.standard_normal((rows, V)) * 3).astype(np.float32)
+        draft = logits[:-1].argmax(1).astype(np.int32)
+        u = orc.verify_uniforms(11, trial, rows)
+        acc0, _ = orc.accept_sampled(logits, draft, 1.0, 0, u, q_point=np.zeros(rows - 1, np.float32))
+        assert acc0 == 0
+        acc_lo, _ = orc.accept_sampled(logits, draft, 1.0, 0, u,
+                                       q_point=np.full(rows - 1, 1e-6, np.float32))
+        assert acc_lo == rows - 1
+        assert orc.accept_sampled(logits, draft, 1.0, 0, u, q_point=np.ones(rows - 1, np.float32)) \
+            == orc.accept_sampled(logits, draft, 1.0, 0, u)
