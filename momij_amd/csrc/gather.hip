@@ -323,9 +323,13 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         if constexpr (RES_PF) {
             // (after the pair list: the wait for a list load would cover these too)
             if (first && res_pf) {
+                // rows of the lane's outputs: q (a pass of at most 4 rows), else 4q .. 4q+3
                 const int col = (cb * TPB + tt) * 16 + n;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) resv[r] = a.y[(size_t)min(4 * q + r, npass - 1) * a.N + col];
+                for (int r = 0; r < 4; ++r) {
+                    const int i = npass <= 4 ? q : 4 * q + r;
+                    resv[r] = a.y[(size_t)min(i, npass - 1) * a.N + col];
+                }
             }
         }
 #pragma unroll
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     // qx pair (x_i, x_{i+8}) of a 16-block, i = (4c + j) % 8: base of code i
-                    const float base = ((4 * c + j) & 1) ? 4.0f : 16.0f;
+                    const float base = code_base(4 * c + j);
                     const float lo = h2f((uint16_t)v[j]), hi = h2f((uint16_t)(v[j] >> 16));
                     X += lo + hi;
                     Bx += base * (lo + hi);
@@ -421,12 +425,19 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         stage_load(0, npass0, buf, lpair, np, true);  // ahead of the weights (loads return in order)
         issue_weights(e, cb);
     }
-    const UnpackK uk = {opaque(0x00C000C0u), opaque(0x03000300u), opaque(0x4C004C00u),
-                        opaque(0x44004400u)};
+    const UnpackK uk = unpack_consts();
     const int xrow = min(n, RA - 1);
     const uint32_t* wq = (const uint32_t*)wcode + 16 * n + q;  // B: word q of row n's chunks
 
-    auto run_pass = [&](int pb, int npass) {
+    // NR activation rows a lane's MFMA outputs hold.  A pass of at most 4 rows (NR = 1) places
+    // staged row i at MFMA rows 4i .. 4i+3 (lane n reads row n / 4), so lane (n, q) holds row q
+    // in each of its four outputs and scales and finishes one of them; more rows (NR = 4) sit at
+    // MFMA rows 0 .. 15, lane (n, q) holding rows 4q .. 4q+3.  Each output is the same sum of the
+    // same products either way.
+    auto run_pass = [&](auto nr_t, int pb, int npass) {
+        constexpr int NR = decltype(nr_t)::value;
+        static_assert(NR == 1 || NR == 4, "rows a lane");
+        const int xr = NR == 1 ? min(n >> 2, RA - 1) : xrow;
         constexpr int G = KBW / 4;  // code column groups, issued after the scale loads
         constexpr int NSB = ROWA ? 1 : 2;  // scale / bias loads of a tile
         // every wave's staged rows visible (this wave's were issued before its weights)
@@ -473,7 +484,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
         for (int c = 0; c < 4; ++c) corr[c] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
         const float* xcs =
-            (const float*)(xsl_of(buf) + xrow * S::SS + kh * KBW + (q >> 1)) + (q & 1);
+            (const float*)(xsl_of(buf) + xr * S::SS + kh * KBW + (q >> 1)) + (q & 1);
         // this lane's B values: the biases (term 0) or the negated scales (term 1), taken from
         // the fp16 half of block 2i + q/2's group (the sign flipped in the fp16 bits)
         const uint32_t sgn = (q & 1) ? 0x8000u : 0u;
@@ -503,13 +514,13 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        // A: activation row xrow, quarter q, of this K-slice
-        const uint16_t* xak = xs_of(buf) + xrow * XS + 16 * q + 64 * kh * KBW;
+        // A: activation row xr, quarter q, of this K-slice
+        const uint16_t* xak = xs_of(buf) + xr * XS + 16 * q + 64 * kh * KBW;
         // the correction chain's sum starts the accumulator (its four partial chains are
-        // then free)
-        float acc[4];
+        // then free); outputs r >= NR stay unused
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = (corr[0][r] + corr[1][r]) + (corr[2][r] + corr[3][r]);
+        for (int r = 0; r < NR; ++r) acc[r] = (corr[0][r] + corr[1][r]) + (corr[2][r] + corr[3][r]);
         // row-alpha weights: every block has scale alpha, so the MFMA sums chain over the whole
         // slice and alpha scales them once
         f4 dacc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};  // even / odd blocks
@@ -562,16 +573,16 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
                     const uint32_t sw = opaque(sv[g / 8][(g % 8) / 2]);
                     const float sc = h2f((uint16_t)(sw >> (16 * (g & 1))));
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[r] += sc * d[r];
+                    for (int r = 0; r < NR; ++r) acc[r] += sc * d[r];
                 }
               }
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pin(acc[r]);
+            for (int r = 0; r < NR; ++r) pin(acc[r]);
         }
         if constexpr (ROWA) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += alpha_n * (dacc[0][r] + dacc[1][r]);
+            for (int r = 0; r < NR; ++r) acc[r] += alpha_n * (dacc[0][r] + dacc[1][r]);
         }
         // persistent mode, last pass of the item: this wave's tile is free, start the next
         // item's weights; its rows follow once every wave is done with the current ones
@@ -602,7 +613,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
                 for (int k2 = 1; k2 < KS; ++k2) {
                     const f4 o = *slot(k2);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[r] += o[r];
+                    for (int r = 0; r < NR; ++r) acc[r] += o[r];
                 }
             }
         }
@@ -613,31 +624,39 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
                 stage_load(0, min(RA, np_next), buf ^ 1, rec_n & 0xFFFF, np_next);
             }
         }
-        // lane (n, q) now holds the outputs of activation rows 4q .. 4q+3 for weight row n
+        // lane (n, q) now holds the outputs of activation rows 4q .. 4q+3 (NR = 4) or row q
+        // (NR = 1) for weight row n
         if constexpr (EPI == EPI_SWIGLU) {
-            // up row n < 8 pairs with gate row n + 8: lanes n < 8 finish rows 4q, 4q + 1 and
-            // lanes n + 8 rows 4q + 2, 4q + 3, each taking the other half of its pair by a swap
+            // up row n < 8 pairs with gate row n + 8.  NR = 4: lanes n < 8 finish rows 4q, 4q + 1
+            // and lanes n + 8 rows 4q + 2, 4q + 3, each taking the other half of its pair by a
+            // swap; NR = 1: lanes n < 8 finish row q
+            auto finish = [&](float up, float g, int i) {
+                up = hround(up);
+                g = hround(g);
+                g = fminf(g, 7.0f);
+                up = fminf(fmaxf(up, -7.0f), 7.0f);
+                const float act = hround(g / (1.0f + expf(-g)) * up);
+                const int j = (cb * TPB + tt) * 8 + (n & 7);
+                a.y[(size_t)s_pair[buf][i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
+            };
+            if constexpr (NR == 1) {
+                const float recv = __shfl_xor(acc[0], 8, MJ_WAVE);
+                if (kh == 0 && n < 8 && q < npass) finish(acc[0], recv, q);
+            } else {
 #pragma unroll
-            for (int rr = 0; rr < 2; ++rr) {
-                const bool lo = n < 8;
-                const float recv = __shfl_xor(lo ? acc[rr + 2] : acc[rr], 8, MJ_WAVE);
-                const int r = lo ? rr : rr + 2;
-                const int i = 4 * q + r;
-                if (kh == 0 && i < npass) {
-                    float up = hround(lo ? acc[rr] : recv);
-                    float g = hround(lo ? recv : acc[rr + 2]);
-                    g = fminf(g, 7.0f);
-                    up = fminf(fmaxf(up, -7.0f), 7.0f);
-                    const float act = hround(g / (1.0f + expf(-g)) * up);
-                    const int j = (cb * TPB + tt) * 8 + (n & 7);
-                    a.y[(size_t)s_pair[buf][i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
+                for (int rr = 0; rr < 2; ++rr) {
+                    const bool lo = n < 8;
+                    const float recv = __shfl_xor(lo ? acc[rr + 2] : acc[rr], 8, MJ_WAVE);
+                    const int r = lo ? rr : rr + 2;
+                    const int i = 4 * q + r;
+                    if (kh == 0 && i < npass) finish(lo ? acc[rr] : recv, lo ? recv : acc[rr + 2], i);
                 }
             }
         } else {
             const int col = (cb * TPB + tt) * 16 + n;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = 4 * q + r;
+            for (int r = 0; r < NR; ++r) {
+                const int i = NR == 1 ? q : 4 * q + r;
                 if (kh == 0 && i < npass) {
                     uint16_t* yp = a.y + (size_t)s_pair[buf][i] * a.N + col;
                     if constexpr (EPI == EPI_ADD) {
@@ -650,13 +669,17 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
             }
         }
     };
-
-    run_pass(0, npass0);
+    // a first pass of at most 4 rows (nearly every expert of a verify pass) takes the
+    // one-row-a-lane form; later passes of a bucket with more rows than fit the general one
+    if (npass0 <= 4)
+        run_pass(std::integral_constant<int, 1>{}, 0, npass0);
+    else
+        run_pass(std::integral_constant<int, 4>{}, 0, npass0);
     for (int pb = RA; pb < np; pb += RA) {
         __syncthreads();  // the previous pass is done with LDS
         const int npass = min(RA, np - pb);
         stage_load(pb, npass, buf, lpair, np);
-        run_pass(pb, npass);
+        run_pass(std::integral_constant<int, 4>{}, pb, npass);
     }
     if constexpr (!PER) break;
     item += gridDim.x;

@@ -2,13 +2,15 @@
 //
 // 2-bit code expansion.  A uint32 word of the MLX layout holds codes c0..c15 (code i in bits
 // [2i, 2i+1]).  unpack16() turns it into eight fp16 pairs without a per-code shift:
-//     v[i] = (base_i + c_i, base_i + c_{i+8}),  base_i = 16 (i even) or 4 (i odd),
-// by masking two code positions straight into the fp16 mantissa of a constant whose ulp is
-// 1: 0x4C00 = 16.0 (mantissa bits 6-7 carry c) and 0x4400 = 4.0 (bits 8-9).  Four shifted
-// copies of the word cover all 16 codes: 12 VALU ops per 16 weights.  The constant part is
-// removed exactly after the dot product: sum_k (base_k + c_k) x_k - sum_k base_k x_k, with
-// Bx = sum_k base_k x_k precomputed once per 64-element block of x.  Small bases keep the
-// fp32 partial sums within ~100x of the result, so the subtraction costs < 1e-5 relative.
+//     v[i] = (base_i + c_i, base_i + c_{i+8}),  base_i = 256, 64, 16, 4 for i % 4 = 0, 1, 2, 3,
+// by masking two code positions straight into the fp16 mantissa of a constant whose ulp makes
+// them count 1: 0x5C00 = 256.0 (code in mantissa bits 2-3), 0x5400 = 64.0 (bits 4-5), 0x4C00 =
+// 16.0 (bits 6-7) and 0x4400 = 4.0 (bits 8-9).  Two shifted copies of the word (w << 2: codes
+// 0-3 and 8-11; w >> 6: codes 4-7 and 12-15) cover all 16 codes: 10 VALU ops per 16 weights.
+// The constant part is removed exactly after the dot product: sum_k (base_k + c_k) x_k -
+// sum_k base_k x_k, with Bx = sum_k base_k x_k precomputed once per 64-element block of x.  The
+// bases stay small enough (the fp32 partial sums within ~200x of the result) that the
+// subtraction costs < 1e-4 relative.
 //
 // Activations feeding a 2-bit product are stored "permuted": inside each 16-element block
 // the order is x0 x8 x1 x9 x2 x10 x3 x11 x4 x12 x5 x13 x6 x14 x7 x15, i.e. fp16 pair i is
@@ -32,33 +34,40 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 __device__ __forceinline__ float hround(float f) { return (float)(_Float16)f; }
 
 __device__ __forceinline__ void unpack16(uint32_t w, uint32_t v[8]) {
-    const uint32_t s1 = w << 6, s2 = w << 2, s3 = w >> 2, s4 = w >> 6;
-    v[0] = (s1 & 0x00C000C0u) | 0x4C004C00u;
-    v[1] = (s1 & 0x03000300u) | 0x44004400u;
-    v[2] = (s2 & 0x00C000C0u) | 0x4C004C00u;
-    v[3] = (s2 & 0x03000300u) | 0x44004400u;
-    v[4] = (s3 & 0x00C000C0u) | 0x4C004C00u;
-    v[5] = (s3 & 0x03000300u) | 0x44004400u;
-    v[6] = (s4 & 0x00C000C0u) | 0x4C004C00u;
-    v[7] = (s4 & 0x03000300u) | 0x44004400u;
+    const uint32_t s1 = w << 2, s2 = w >> 6;
+    v[0] = (s1 & 0x000C000Cu) | 0x5C005C00u;
+    v[1] = (s1 & 0x00300030u) | 0x54005400u;
+    v[2] = (s1 & 0x00C000C0u) | 0x4C004C00u;
+    v[3] = (s1 & 0x03000300u) | 0x44004400u;
+    v[4] = (s2 & 0x000C000Cu) | 0x5C005C00u;
+    v[5] = (s2 & 0x00300030u) | 0x54005400u;
+    v[6] = (s2 & 0x00C000C0u) | 0x4C004C00u;
+    v[7] = (s2 & 0x03000300u) | 0x44004400u;
 }
 
 // unpack16 with its masks and magic constants held in VGPRs (an AND-OR with a VGPR constant
 // is one v_and_or_b32; with inline literals it is two instructions on this target).
 struct UnpackK {
-    uint32_t m1, m2, c1, c2;
+    uint32_t m[4], c[4];
 };
 __device__ __forceinline__ void unpack16k(uint32_t w, uint32_t v[8], const UnpackK& k) {
-    const uint32_t s1 = w << 6, s2 = w << 2, s3 = w >> 2, s4 = w >> 6;
-    v[0] = (s1 & k.m1) | k.c1;
-    v[1] = (s1 & k.m2) | k.c2;
-    v[2] = (s2 & k.m1) | k.c1;
-    v[3] = (s2 & k.m2) | k.c2;
-    v[4] = (s3 & k.m1) | k.c1;
-    v[5] = (s3 & k.m2) | k.c2;
-    v[6] = (s4 & k.m1) | k.c1;
-    v[7] = (s4 & k.m2) | k.c2;
+    const uint32_t s1 = w << 2, s2 = w >> 6;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = (s1 & k.m[i]) | k.c[i];
+        v[i + 4] = (s2 & k.m[i]) | k.c[i];
+    }
 }
+
+// base of qx pair i (i = 0..7 inside its 16-element block), as a float and as an fp16 pair
+__device__ __forceinline__ float code_base(int i) { return (float)(256 >> (2 * (i & 3))); }
+__device__ __forceinline__ uint32_t code_base2(int i) {
+    constexpr uint32_t b2[4] = {0x5C005C00u, 0x54005400u, 0x4C004C00u, 0x44004400u};
+    return b2[i & 3];
+}
+// bases of the plain pair (x_{2j}, x_{2j+1}) of an 8-aligned run of a row: (256, 64) for even
+// j, (16, 4) for odd j
+__device__ __forceinline__ uint32_t plain_base2(int j) { return (j & 1) ? 0x44004C00u : 0x54005C00u; }
 
 // Value the optimiser cannot see through: keeps loop-invariant code expansion from being
 // hoisted out of a loop (and held live across it) when registers are the scarce resource.
@@ -71,8 +80,19 @@ __device__ __forceinline__ uint32_t opaque(uint32_t x) {
 // (keeps unrolled accumulation chains from being deferred until every operand is live).
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
-// base of permuted pair i (16 for even code index, 4 for odd)
-__device__ __forceinline__ float code_base(int i) { return (i & 1) ? 4.0f : 16.0f; }
+// A wave-uniform value held in an SGPR the optimiser cannot see through.
+__device__ __forceinline__ uint32_t opaque_s(uint32_t x) {
+    asm volatile("" : "+s"(x));
+    return x;
+}
+
+// the masks (SGPRs) and constants (VGPRs) of unpack16k: a v_and_or_b32 may read one SGPR, so
+// each AND-OR stays one instruction while only the four constants take vector registers
+__device__ __forceinline__ UnpackK unpack_consts() {
+    return UnpackK{{opaque_s(0x000C000Cu), opaque_s(0x00300030u), opaque_s(0x00C000C0u),
+                    opaque_s(0x03000300u)},
+                   {opaque(0x5C005C00u), opaque(0x54005400u), opaque(0x4C004C00u), opaque(0x44004400u)}};
+}
 
 // fp16 pair (lo, hi) from two raw fp16 bit patterns
 __device__ __forceinline__ uint32_t pack2(uint32_t lo16, uint32_t hi16) {
@@ -123,10 +143,10 @@ __device__ __forceinline__ void emit_qx(const u4v v, int lane, uint16_t* xperm_r
     X = dot2(v.y, 0x3C003C00u, X);
     X = dot2(v.z, 0x3C003C00u, X);
     X = dot2(v.w, 0x3C003C00u, X);
-    Bx = dot2(v.x, 0x44004C00u, Bx);
-    Bx = dot2(v.y, 0x44004C00u, Bx);
-    Bx = dot2(v.z, 0x44004C00u, Bx);
-    Bx = dot2(v.w, 0x44004C00u, Bx);
+    Bx = dot2(v.x, plain_base2(0), Bx);
+    Bx = dot2(v.y, plain_base2(1), Bx);
+    Bx = dot2(v.z, plain_base2(2), Bx);
+    Bx = dot2(v.w, plain_base2(3), Bx);
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) {
         X += __shfl_xor(X, m, MJ_WAVE);

@@ -53,11 +53,11 @@ __global__ __launch_bounds__(256) void k_qx_prep(const uint16_t* __restrict__ x,
     X = dot2(v.y, 0x3C003C00u, X);
     X = dot2(v.z, 0x3C003C00u, X);
     X = dot2(v.w, 0x3C003C00u, X);
-    // plain pair (x_even, x_odd): bases (16, 4)
-    Bx = dot2(v.x, 0x44004C00u, Bx);
-    Bx = dot2(v.y, 0x44004C00u, Bx);
-    Bx = dot2(v.z, 0x44004C00u, Bx);
-    Bx = dot2(v.w, 0x44004C00u, Bx);
+    // plain pairs (x_2j, x_2j+1): bases (256, 64) and (16, 4)
+    Bx = dot2(v.x, plain_base2(0), Bx);
+    Bx = dot2(v.y, plain_base2(1), Bx);
+    Bx = dot2(v.z, plain_base2(2), Bx);
+    Bx = dot2(v.w, plain_base2(3), Bx);
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) {
         X += __shfl_xor(X, m, MJ_WAVE);
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void k_qx_sums(const uint16_t* __restrict__ xp
     for (int c = 0; c < 8; ++c) {
         const u4v v = *(const u4v*)(xr + 8 * c);
         for (int j = 0; j < 4; ++j) {
-            const float base = ((4 * c + j) & 1) ? 4.0f : 16.0f;  // pair (x_i, x_{i+8}), i = (4c+j)%8
+            const float base = code_base(4 * c + j);  // pair (x_i, x_{i+8}), i = (4c+j)%8
             const float lo = h2f((uint16_t)v[j]), hi = h2f((uint16_t)(v[j] >> 16));
             X += lo + hi;
             Bx += base * (lo + hi);
@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256) void k_qmv2(QmvArgs a) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
         X = dot2(xp[i], 0x3C003C00u, X);
-        Bx = dot2(xp[i], (i & 1) ? 0x44004400u : 0x4C004C00u, Bx);
+        Bx = dot2(xp[i], code_base2(i), Bx);
     }
 
     for (int o0 = wb; o0 < wend; o0 += OUT_PER_IT) {
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(EPI == EPI_SWIGLU ? 512 : 256) void k_gather(Gather
             for (int c = 0; c < 64; ++c) {
                 const float v = act_lds[i * 65 + c];
                 X += v;
-                Bx += ((c & 1) ? 4.0f : 16.0f) * v;
+                Bx += code_base(c % 8) * v;  // plain element c: the base of its qx pair
             }
             const int pr = bk ? bk->pair[p0 + i] : i;
             a.ysum[(size_t)pr * (I / 64) + kbo] = make_float2(X, Bx);
