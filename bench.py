@@ -132,6 +132,50 @@ def expert_bytes(cfg, inds_layers, M):
     return np.array(up), np.array(dn), np.array(uniq)
 
 
+def kernel_profile(eng, cfg, y, draft, parents, L0, steps):
+    """Per-kernel-class times of eager verify passes of (draft, parents) from HIP events, less
+    the timer's own cost, and the HBM rates of the expert gathers and the head from the pass's
+    own routing (unique experts per layer counted once)."""
+    import torch
+
+    M = len(draft) + 1
+    icap = torch.empty((cfg.n_layers, 64, cfg.top_k), dtype=torch.int32, device="cuda")
+    eng.rewind(L0)
+    eng.set_capture(inds=icap)
+    eng.verify_greedy(y, draft, parents)
+    eng.set_capture()
+    inds = icap.cpu().numpy()
+    up_b, dn_b, uniq = expert_bytes(cfg, inds, M)
+    eng.profile(True)
+    for _ in range(steps):
+        eng.rewind(L0)
+        eng.verify_greedy(y, draft, parents)
+    km = eng.kernel_ms()
+    eng.profile(False)
+    # each bracketed time is kernel + timer cost; brackets around a 20 us wall-clock hold in
+    # the same passes give that cost, which is taken off every launch
+    ev_ms, ev_n = km.pop("timer")
+    ev_each = max(ev_ms / max(ev_n, 1) - TIMER_HOLD_MS, 0.0)
+    km = {name: (ms - n * ev_each, n) for name, (ms, n) in km.items()}
+    up_ms, up_n = km["expert_up"]
+    dn_ms, dn_n = km["expert_down"]
+    hd_ms, hd_n = km["lm_head"]
+    up_gbs = up_b.sum() * steps / (up_ms * 1e-3) / 1e9
+    dn_gbs = dn_b.sum() * steps / (dn_ms * 1e-3) / 1e9
+    head_bytes = cfg.vocab * cfg.H * 2 + M * cfg.H * 2
+    hd_gbs = head_bytes * hd_n / (hd_ms * 1e-3) / 1e9
+    kernels = {name: dict(ms_per_launch=round(ms / max(n, 1), 5), launches=n)
+               for name, (ms, n) in km.items()}
+    kernels["expert_up"]["GBps"] = round(up_gbs, 1)
+    kernels["expert_up"]["bytes_per_launch"] = int(up_b.mean())
+    kernels["expert_down"]["GBps"] = round(dn_gbs, 1)
+    kernels["expert_down"]["bytes_per_launch"] = int(dn_b.mean())
+    kernels["lm_head"]["GBps"] = round(hd_gbs, 1)
+    kernels["lm_head"]["bytes_per_launch"] = int(head_bytes)
+    return dict(kernels=kernels, up_gbs=up_gbs, dn_gbs=dn_gbs, hd_gbs=hd_gbs, up_ms=up_ms,
+                up_n=up_n, timer_ms=ev_each, up_b=up_b, uniq=uniq)
+
+
 def cpu_baseline(eng, cfg, weights, y, draft, L0, reps=5):
     """Oracle restatement timed on the host: layers 0-1 of the verify pass (from the GPU's own
     layer inputs and KV cache) + the full fp16 lm_head for the 9 rows; scaled to 24 layers.
@@ -268,41 +312,19 @@ def main():
                                  pres=0.1, freq=0.1, hist=hist)
     log(f"sampled: {sampled}; top-p + penalties: {sampled_opts}")
 
-    # per-kernel times from HIP events (eager passes) and the routing of the pass
-    icap = torch.empty((cfg.n_layers, 64, cfg.top_k), dtype=torch.int32, device="cuda")
-    eng.rewind(L0)
-    eng.set_capture(inds=icap)
-    eng.verify_greedy(y, draft)
-    eng.set_capture()
-    inds = icap.cpu().numpy()
-    M = len(draft) + 1
-    up_b, dn_b, uniq = expert_bytes(cfg, inds, M)
+    # per-kernel times from HIP events (eager passes) and the routing of the pass: the K=8
+    # chain (the headline) and the 16-node tree (config 4's own pass, 17 rows)
     prof_steps = max(5, min(args.steps, 20))
-    eng.profile(True)
-    for _ in range(prof_steps):
-        eng.rewind(L0)
-        eng.verify_greedy(y, draft)
-    km = eng.kernel_ms()
-    eng.profile(False)
-    # each bracketed time is kernel + timer cost; brackets around a 20 us wall-clock hold in
-    # the same passes give that cost, which is taken off every launch
-    ev_ms, ev_n = km.pop("timer")
-    ev_each = max(ev_ms / max(ev_n, 1) - TIMER_HOLD_MS, 0.0)
-    km = {name: (ms - n * ev_each, n) for name, (ms, n) in km.items()}
-    up_ms, up_n = km["expert_up"]
-    dn_ms, dn_n = km["expert_down"]
-    hd_ms, hd_n = km["lm_head"]
-    up_gbs = up_b.sum() * prof_steps / (up_ms * 1e-3) / 1e9
-    dn_gbs = dn_b.sum() * prof_steps / (dn_ms * 1e-3) / 1e9
-    head_bytes = cfg.vocab * cfg.H * 2 + M * cfg.H * 2
-    hd_gbs = head_bytes * hd_n / (hd_ms * 1e-3) / 1e9
-    kernels = {name: dict(ms_per_launch=round(ms / max(n, 1), 5), launches=n)
-               for name, (ms, n) in km.items()}
-    kernels["expert_up"]["GBps"] = round(up_gbs, 1)
-    kernels["expert_down"]["GBps"] = round(dn_gbs, 1)
-    kernels["lm_head"]["GBps"] = round(hd_gbs, 1)
-    log(f"expert up {up_gbs:.0f} GB/s, down {dn_gbs:.0f} GB/s, head {hd_gbs:.0f} GB/s, "
-        f"unique experts/layer {uniq.mean():.1f}")
+    kp = kernel_profile(eng, cfg, y, draft, None, L0, prof_steps)
+    kt = kernel_profile(eng, cfg, y, tdraft, TREE16, L0, prof_steps)
+    kernels, up_gbs, up_ms, up_n, ev_each, up_b, uniq = (
+        kp["kernels"], kp["up_gbs"], kp["up_ms"], kp["up_n"], kp["timer_ms"], kp["up_b"],
+        kp["uniq"])
+    M = len(draft) + 1
+    log(f"expert up {kp['up_gbs']:.0f} GB/s, down {kp['dn_gbs']:.0f} GB/s, head "
+        f"{kp['hd_gbs']:.0f} GB/s, unique experts/layer {uniq.mean():.1f}")
+    log(f"tree16 (17 rows): expert up {kt['up_gbs']:.0f} GB/s, down {kt['dn_gbs']:.0f} GB/s, "
+        f"head {kt['hd_gbs']:.0f} GB/s, unique experts/layer {kt['uniq'].mean():.1f}")
 
     # HBM bytes per launch of the same kernel, from the FETCH_SIZE / WRITE_SIZE collections
     # summarised under profiles/ (counter runs cannot share a process with this timing)
@@ -355,7 +377,9 @@ def main():
         },
         "cpu_baseline": cpu,
         "tree": {"tokens_per_s": round(ttoks / tdt, 3), "ms_per_step": round(tdt / args.steps * 1e3, 4),
-                 "accepted": tacc, "rows": len(TREE16), "device_ms_per_step": round(tdev, 4)},
+                 "accepted": tacc, "rows": len(TREE16), "device_ms_per_step": round(tdev, 4),
+                 "kernels": kt["kernels"],
+                 "unique_experts_per_layer": round(float(kt["uniq"].mean()), 2)},
         "sampled": dict(sampled, temperature=0.7, q="uniform 1/V"),
         "sampled_top_p_penalties": dict(sampled_opts, temperature=0.7, top_p=0.9,
                                         repetition=1.1, presence=0.1, frequency=0.1),

@@ -8,6 +8,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -30,14 +31,37 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
 
 
+# Kernels whose waits count their own outstanding vector-memory requests (s_waitcnt vmcnt(N)
+# with N > 0): a register spill would add scratch requests to that count, so none may spill.
+COUNTED_WAIT_KERNELS = ("k_gather5", "k_lm_head")
+
+
+def _spills(stderr: str) -> list:
+    """(kernel, VGPR spill count) of the counted-wait kernels that spill, from the resource
+    remarks of one compile."""
+    out, cur = [], None
+    for line in stderr.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            cur = m.group(1)
+            continue
+        m = re.search(r"VGPRs Spill: (\d+)", line)
+        if m and cur and int(m.group(1)) > 0 and any(k in cur for k in COUNTED_WAIT_KERNELS):
+            out.append((cur, int(m.group(1))))
+    return out
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd = [HIPCC, "-x", "hip", *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
+    bad = _spills(r.stderr)
+    if bad:
+        raise RuntimeError(f"{src}: kernels with counted waits spill registers: {bad}")
     return obj
 
 
