@@ -240,15 +240,14 @@ struct NucState {
     int need, row, acc;
     float u, Z;
 };
-// Scratch of a nucleus sample over one row of V: the row's keys (e bits) and ids, their
-// descending order, the sort's temporary storage and the deferred decision.
+// Scratch of a nucleus sample over one row of V: the row's keys (e bits), the selection's four
+// rounds of digit histograms (counts [4][256], exact masses [4][256]), the last round's counts
+// per block [blocks][256], and the deferred decision.
 struct NucleusBuf {
     uint32_t* keys;
-    int32_t* ids;
-    uint32_t* keys_s;
-    int32_t* ids_s;
-    void* tmp;
-    size_t tmp_bytes;
+    uint32_t* hcnt;
+    uint64_t* hmass;
+    uint32_t* hblk;
     NucState* st;
 };
 size_t nucleus_bytes(int V);

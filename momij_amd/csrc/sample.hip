@@ -10,14 +10,13 @@
 // seen set and counts growing with the drafts accepted before it (walkDraft 86-87);
 // samplePrepared's nucleus (137-154) for the bonus and for a residual of zero mass: tokens
 // ranked by e descending, the lower id first on ties, kept up to the first ranked prefix whose
-// blocked prefix sum reaches top_p * Z, sampled in id order (the ranking is a radix sort of
-// the row's e bits).
+// mass reaches top_p * Z, sampled in id order.  The masses are summed exactly, as integers
+// trunc(e * 2^40), so no order is needed: the cut is found by a radix selection over the e bits
+// (four 8-bit digit rounds of histograms of counts and masses), not by sorting the row.
 // Every float operation below happens in a fixed order (chunks of 16 summed sequentially,
 // blocks of 64 chunks summed sequentially, block totals summed sequentially; exp evaluated by
 // canon_expf; IEEE divisions) so the CPU oracle reproduces each decision bit for bit.
 #pragma clang fp contract(off)
-#include <hipcub/hipcub.hpp>
-
 #include "mj_device.h"
 #include "mj_internal.h"
 
@@ -504,8 +503,13 @@ __global__ __launch_bounds__(256) void k_resid_walk(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
     const SampleState st = *a.state;
-    if (st.phase != 1) return;
     const int t = threadIdx.x;
+    // the nucleus selection's first histogram starts empty (its kernel adds to it next)
+    if (a.nb.st) {
+        a.nb.hcnt[t] = 0u;
+        a.nb.hmass[t] = 0ull;
+    }
+    if (st.phase != 1) return;
     __shared__ float s_S;
     __shared__ float pref[MAX_CHUNKS / BLK];
     stage_lds(pref, a.rbs, a.nblocks, t, 256);
@@ -602,20 +606,100 @@ __device__ int blk_walk(F f, int n, float tgt, const float* cs, const float* bs,
     return *s_out;
 }
 
-// e bits and ids of the nucleus row (e >= 0: its bits order as the values do)
-__global__ __launch_bounds__(256) void k_nucleus_keys(SampleArgs a) {
-    if (aborted(a.abort)) return;
-    a = resolve(a);
-    const NucState st = *a.nb.st;
-    if (!st.need) return;
-    const int v = blockIdx.x * 256 + threadIdx.x;
-    if (v >= a.V) return;
-    a.nb.keys[v] = __float_as_uint(e_at(a, st.row, v, a.rowmax[st.row] * a.invT));
-    a.nb.ids[v] = v;
+// ---- nucleus cut by radix selection -------------------------------------------------------
+// The e of the nucleus row are non-negative floats, so their bits order as their values.  Round
+// r (0..3) histograms digit r (bits 31 - 8r .. 24 - 8r) of the keys that match the digits
+// already chosen: a count and an exact mass (sum of trunc(e * 2^40)) per digit value.  Scanning a
+// round's digits from the top, the cut lies in the first digit whose mass, added to the mass
+// of the keys above it, reaches the target; after four rounds the cut key is known exactly,
+// and among the keys equal to it (ties, taken in id order) the cut is the j-th, j the fewest
+// that reach the target.  NUC_BLOCKS blocks of 256 threads cover up to NUC_BLOCKS * 2048 ids,
+// block b ids [2048 b, 2048 b + 2048); the last round also keeps each block's digit counts so
+// the j-th tie is found without another pass.
+#define NUC_BLOCKS 96
+#define NUC_PER_BLOCK 2048
+
+__device__ __forceinline__ uint64_t nuc_fixed(float e) {
+    return (uint64_t)(e * 0x1p40f);  // exact scaling, then truncation (e <= 1)
 }
 
-// After the ranking (ids_s / keys_s: e descending, lower id first among equal e): the kept
-// prefix, its mass in id order, and the sample.
+// The selection state after rounds 0 .. r - 1: the chosen digits (prefix) and the mass of the
+// keys ranked above them; false when the target exceeds the row's whole mass (every key kept).
+__device__ bool nuc_prefix(const NucleusBuf& nb, int r, uint64_t F, uint32_t& prefix,
+                           uint64_t& above) {
+    prefix = 0u;
+    above = 0ull;
+    for (int rr = 0; rr < r; ++rr) {
+        const uint32_t* cnt = nb.hcnt + 256 * rr;
+        const uint64_t* mass = nb.hmass + 256 * rr;
+        int d = 255;
+        for (; d >= 0; --d) {
+            if (cnt[d] == 0u) continue;
+            if (above + mass[d] >= F) break;
+            above += mass[d];
+        }
+        if (d < 0) return false;
+        prefix = (prefix << 8) | (uint32_t)d;
+    }
+    return true;
+}
+
+__device__ __forceinline__ uint64_t nuc_target(const SampleArgs& a, float Z) {
+    const float tp = a.o.top_p < 0.0f ? 0.0f : (a.o.top_p > 1.0f ? 1.0f : a.o.top_p);
+    return nuc_fixed(tp * Z);
+}
+
+// Round R of the selection; round 0 also computes the row's keys (e bits).
+template <int R>
+__global__ __launch_bounds__(256) void k_nucleus_round(SampleArgs a) {
+    if (aborted(a.abort)) return;
+    a = resolve(a);
+    const int t = threadIdx.x, b = blockIdx.x;
+    // the next round's histogram starts empty
+    if constexpr (R < 3) {
+        if (b == 0) {
+            a.nb.hcnt[256 * (R + 1) + t] = 0u;
+            a.nb.hmass[256 * (R + 1) + t] = 0ull;
+        }
+    }
+    const NucState st = *a.nb.st;
+    if (!st.need) return;
+    __shared__ uint32_t s_cnt[256];
+    __shared__ unsigned long long s_mass[256];
+    s_cnt[t] = 0u;
+    s_mass[t] = 0ull;
+    uint32_t prefix = 0u;
+    uint64_t above = 0ull;
+    bool some = true;
+    if constexpr (R > 0) some = nuc_prefix(a.nb, R, nuc_target(a, st.Z), prefix, above);
+    __syncthreads();
+    if (!some) return;  // block-uniform: every key is kept
+    const float mxs = a.rowmax[st.row] * a.invT;
+#pragma unroll
+    for (int i = 0; i < NUC_PER_BLOCK / 256; ++i) {
+        const int v = b * NUC_PER_BLOCK + 256 * i + t;
+        if (v >= a.V) break;
+        uint32_t key;
+        if constexpr (R == 0) {
+            key = __float_as_uint(e_at(a, st.row, v, mxs));
+            a.nb.keys[v] = key;
+        } else {
+            key = a.nb.keys[v];
+            if ((key >> (32 - 8 * R)) != prefix) continue;
+        }
+        const int d = (key >> (24 - 8 * R)) & 255;
+        atomicAdd(&s_cnt[d], 1u);
+        atomicAdd(&s_mass[d], (unsigned long long)nuc_fixed(__uint_as_float(key)));
+    }
+    __syncthreads();
+    if (s_cnt[t] != 0u) {
+        atomicAdd(a.nb.hcnt + 256 * R + t, s_cnt[t]);
+        atomicAdd((unsigned long long*)(a.nb.hmass + 256 * R + t), s_mass[t]);
+    }
+    if constexpr (R == 3) a.nb.hblk[256 * b + t] = s_cnt[t];
+}
+
+// The cut (key and id), the kept mass in id order and the sample.
 __global__ __launch_bounds__(1024) void k_nucleus_pick(SampleArgs a) {
     if (aborted(a.abort)) return;
     a = resolve(a);
@@ -625,47 +709,111 @@ __global__ __launch_bounds__(1024) void k_nucleus_pick(SampleArgs a) {
     __shared__ float bs[MAX_CHUNKS / BLK];
     __shared__ float s_f;
     __shared__ int s_i;
+    __shared__ int s_wsum[16];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    uint32_t ck = 0u;   // the cut key
+    int cid = a.V - 1;  // the cut id: with every key kept, the last
+    uint64_t above = 0ull;
+    const uint64_t F = nuc_target(a, st.Z);
+    if (nuc_prefix(a.nb, 4, F, ck, above)) {
+        // ties of the cut key, in id order: j of them reach the target (at least one)
+        const uint64_t m = nuc_fixed(__uint_as_float(ck));
+        const uint64_t need = F > above ? F - above : 0ull;
+        const int j = need == 0ull ? 1 : (int)((need + m - 1) / m);
+        // the block holding the j-th tie, and its rank there (every thread scans the counts)
+        const int d = ck & 255;
+        int b = 0, before = 0;
+        for (; b < NUC_BLOCKS; ++b) {
+            const int c = (int)a.nb.hblk[256 * b + d];
+            if (before + c >= j) break;
+            before += c;
+        }
+        const int jl = j - before;
+        // two ids a thread of that block's range, counted by a block-wide prefix
+        const int v0 = b * NUC_PER_BLOCK + 2 * t;
+        const bool h0 = v0 < a.V && a.nb.keys[v0] == ck;
+        const bool h1 = v0 + 1 < a.V && a.nb.keys[v0 + 1] == ck;
+        const int c = (int)h0 + (int)h1;
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, MJ_WAVE);
+            if (lane >= o) incl += y;
+        }
+        if (lane == 63) s_wsum[wv] = incl;
+        __syncthreads();
+        int off = 0;
+        for (int w = 0; w < wv; ++w) off += s_wsum[w];
+        const int ex = off + incl - c;
+        if (c > 0 && ex < jl && jl <= ex + c) s_i = (h0 && ex + 1 == jl) ? v0 : v0 + 1;
+        __syncthreads();
+        cid = s_i;
+    }
     const float mxs = a.rowmax[st.row] * a.invT;
-    const float tp = a.o.top_p < 0.0f ? 0.0f : (a.o.top_p > 1.0f ? 1.0f : a.o.top_p);
-    const uint32_t* ks = a.nb.keys_s;
-    const auto ranked = [&](int i) { return __uint_as_float(ks[i]); };
-    blk_sum(ranked, a.V, cs, bs, &s_f);
-    const int k = blk_walk(ranked, a.V, tp * st.Z, cs, bs, &s_i);
-    const float es = ranked(k);
-    const int is = a.nb.ids_s[k];
+    const uint32_t* keys = a.nb.keys;
     const auto kept = [&](int v) {
-        const float e = e_at(a, st.row, v, mxs);
-        return (e > es || (e == es && v <= is)) ? e : 0.0f;
+        const uint32_t k = keys[v];
+        return (k > ck || (k == ck && v <= cid)) ? __uint_as_float(k) : 0.0f;
     };
     const float S = blk_sum(kept, a.V, cs, bs, &s_f);
-    const int tok = S > 0.0f ? blk_walk(kept, a.V, st.u * S, cs, bs, &s_i) : a.nb.ids_s[0];
-    if (threadIdx.x < 64) write_result(a, st.acc, tok);
-}
-
-static size_t sort_tmp_bytes(int V) {
-    size_t b = 0;
-    hipError_t e = hipcub::DeviceRadixSort::SortPairsDescending(
-        nullptr, b, (const uint32_t*)nullptr, (uint32_t*)nullptr, (const int32_t*)nullptr,
-        (int32_t*)nullptr, V, 0, 32, (hipStream_t)0);
-    return e == hipSuccess ? b : 0;
+    int tok;
+    if (S > 0.0f) {
+        tok = blk_walk(kept, a.V, st.u * S, cs, bs, &s_i);
+    } else {  // the top-ranked token: the largest key, the lowest id among equal keys
+        uint32_t bk = 0u;
+        int bi = a.V;
+        for (int v = t; v < a.V; v += 1024) {
+            const uint32_t k = keys[v];
+            if (k > bk || (k == bk && v < bi)) {
+                bk = k;
+                bi = v;
+            }
+        }
+        if (t == 0) s_i = a.V;
+        __syncthreads();
+        for (int w = 0; w < 16; ++w) {  // fixed order: wave by wave through LDS
+            __syncthreads();
+            if (wv == w) {
+#pragma unroll
+                for (int o = 32; o > 0; o >>= 1) {
+                    const uint32_t ok = __shfl_xor(bk, o, MJ_WAVE);
+                    const int oi = __shfl_xor(bi, o, MJ_WAVE);
+                    if (ok > bk || (ok == bk && oi < bi)) {
+                        bk = ok;
+                        bi = oi;
+                    }
+                }
+                if (lane == 0) {
+                    const int pi = s_i;
+                    const uint32_t pk = pi < a.V ? keys[pi] : 0u;
+                    if (pi >= a.V || bk > pk || (bk == pk && bi < pi)) s_i = bi;
+                }
+            }
+        }
+        __syncthreads();
+        tok = s_i < a.V ? s_i : 0;
+    }
+    if (t < 64) write_result(a, st.acc, tok);
 }
 
 static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 size_t nucleus_bytes(int V) {
-    return 4 * up256((size_t)V * 4) + up256(sort_tmp_bytes(V)) + up256(sizeof(NucState));
+    return up256((size_t)V * 4) + up256(4 * 256 * 4) + up256(4 * 256 * 8) +
+           up256((size_t)NUC_BLOCKS * 256 * 4) + up256(sizeof(NucState));
 }
 
 void nucleus_layout(void* base, int V, NucleusBuf& nb) {
     char* p = (char*)base;
-    const size_t row = up256((size_t)V * 4);
     nb.keys = (uint32_t*)p;
-    nb.ids = (int32_t*)(p + row);
-    nb.keys_s = (uint32_t*)(p + 2 * row);
-    nb.ids_s = (int32_t*)(p + 3 * row);
-    nb.tmp = p + 4 * row;
-    nb.tmp_bytes = sort_tmp_bytes(V);
-    nb.st = (NucState*)(p + 4 * row + up256(nb.tmp_bytes));
+    p += up256((size_t)V * 4);
+    nb.hcnt = (uint32_t*)p;
+    p += up256(4 * 256 * 4);
+    nb.hmass = (uint64_t*)p;
+    p += up256(4 * 256 * 8);
+    nb.hblk = (uint32_t*)p;
+    p += up256((size_t)NUC_BLOCKS * 256 * 4);
+    nb.st = (NucState*)p;
 }
 
 hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* draft,
@@ -700,7 +848,8 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
     a.o = o;
     if (nb) a.nb = *nb;
     a.head_max = head_max;
-    if (V > MAX_CHUNKS * CH || rows > MJ_ROWS) return hipErrorInvalidValue;
+    if (V > MAX_CHUNKS * CH || V > NUC_BLOCKS * NUC_PER_BLOCK || rows > MJ_ROWS)
+        return hipErrorInvalidValue;
     hipError_t e = hipSuccess;
     if (!head_max) {
         hipLaunchKernelGGL(k_penalize, dim3(rows), dim3(256), 0, st, a);
@@ -722,12 +871,11 @@ hipError_t launch_accept_sampled(float* logits, int rows, int V, const int32_t* 
     hipLaunchKernelGGL(k_resid_walk, dim3(1), dim3(256), 0, st, a);
     e = hipGetLastError();
     if (e != hipSuccess || !nb) return e;
-    hipLaunchKernelGGL(k_nucleus_keys, dim3((V + 255) / 256), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_nucleus_round<0>, dim3(NUC_BLOCKS), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_nucleus_round<1>, dim3(NUC_BLOCKS), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_nucleus_round<2>, dim3(NUC_BLOCKS), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_nucleus_round<3>, dim3(NUC_BLOCKS), dim3(256), 0, st, a);
     e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    size_t tb = nb->tmp_bytes;
-    e = hipcub::DeviceRadixSort::SortPairsDescending(nb->tmp, tb, nb->keys, nb->keys_s, nb->ids,
-                                                      nb->ids_s, V, 0, 32, st);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_nucleus_pick, dim3(1), dim3(1024), 0, st, a);
     return hipGetLastError();

@@ -849,12 +849,14 @@ void or_penalize_row(float* l, int V, const int32_t* hist_tok, const int32_t* hi
     }
 }
 
-/* LogitsProcessor.samplePrepared's nucleus + multinomial (LogitsProcessor.swift:137-164) in
- * the canonical order.  Tokens are ranked by e descending, the lower id first among equal e
- * (the reference's unstable sort leaves ties unordered); the kept set is the shortest ranked
- * prefix whose prefix sum, accumulated in or_canon_walk's blocked order over the ranked
- * values, reaches clamp(top_p, 0, 1) * Z; the sample is or_canon_walk over the kept e in id
- * order at u * (their or_canon_sum), or the top-ranked token when that sum is 0. */
+/* LogitsProcessor.samplePrepared's nucleus + multinomial (LogitsProcessor.swift:137-164).
+ * Tokens are ranked by e descending, the lower id first among equal e (the reference's unstable
+ * sort leaves ties unordered).  The kept set is the shortest ranked prefix (at least one token)
+ * whose mass reaches clamp(top_p, 0, 1) * Z, the masses summed exactly: each e as the integer
+ * trunc(e * 2^40), the target as trunc(fl(tp * Z) * 2^40) (an order-free sum, so the device may
+ * find the cut by a radix selection instead of a sort).  The sample is or_canon_walk over the
+ * kept e in id order at u * (their or_canon_sum), or the top-ranked token when that sum is 0;
+ * with the target above the whole mass every token is kept. */
 typedef struct {
     float e;
     int32_t id;
@@ -867,25 +869,33 @@ static int rank_cmp(const void* a, const void* b) {
     return x->id < y->id ? -1 : (x->id > y->id ? 1 : 0);
 }
 
+uint64_t or_nucleus_fixed(float e) { return (uint64_t)((double)e * 0x1p40); }
+
 int or_nucleus_sample(const float* e, int V, float Z, float top_p, float u) {
     rank_item* it = (rank_item*)malloc(sizeof(rank_item) * (size_t)V);
-    float* se = (float*)malloc(sizeof(float) * (size_t)V);
     float* kept = (float*)malloc(sizeof(float) * (size_t)V);
     for (int v = 0; v < V; ++v) {
         it[v].e = e[v];
         it[v].id = v;
     }
     qsort(it, (size_t)V, sizeof(rank_item), rank_cmp);
-    for (int i = 0; i < V; ++i) se[i] = it[i].e;
     const float tp = top_p < 0.0f ? 0.0f : (top_p > 1.0f ? 1.0f : top_p);
-    const int k = or_canon_walk(se, V, tp * Z);
+    const uint64_t F = or_nucleus_fixed(tp * Z);
+    int k = V - 1;
+    uint64_t acc = 0;
+    for (int i = 0; i < V; ++i) {
+        acc += or_nucleus_fixed(it[i].e);
+        if (acc >= F) {
+            k = i;
+            break;
+        }
+    }
     const float es = it[k].e;
     const int is = it[k].id;
     for (int v = 0; v < V; ++v) kept[v] = (e[v] > es || (e[v] == es && v <= is)) ? e[v] : 0.0f;
     const float S = or_canon_sum(kept, V);
     const int tok = S > 0.0f ? or_canon_walk(kept, V, u * S) : it[0].id;
     free(it);
-    free(se);
     free(kept);
     return tok;
 }

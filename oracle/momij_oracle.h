@@ -153,6 +153,8 @@ void or_penalize_row(float* l, int V, const int32_t* hist_tok, const int32_t* hi
                      float freq);
 /* Nucleus + multinomial in the canonical order (ranked by e descending, lower id first). */
 int or_nucleus_sample(const float* e, int V, float Z, float top_p, float u);
+/* the fixed-point mass of one e in the nucleus cut: trunc(e * 2^40) */
+uint64_t or_nucleus_fixed(float e);
 /* or_accept_sampled with penalties (history + accepted drafts) and top-p. */
 int or_accept_sampled_ex(const float* logits, int rows, int V, const int32_t* draft,
                          float temperature, float top_p, float rep, float pres, float freq,

@@ -256,9 +256,9 @@ def test_accept_sampled_bit_exact(ctx, head_case, orc, q_mode, temp):
 def test_accept_sampled_ex_bit_exact(ctx, head_case, orc, opts):
     """LogitsProcessor options over the full 151936-token head: penalties on every row (the
     history plus the drafts accepted before it) and samplePrepared's nucleus for the bonus and
-    for a residual without mass (a device radix sort ranks the row), bit for bit against the
-    oracle's canonical rule on the same logits and uniforms; the caller's logits stay as they
-    were."""
+    for a residual without mass (the cut found by a radix selection over the row), bit for bit
+    against the oracle's canonical rule on the same logits and uniforms; the caller's logits
+    stay as they were."""
     import torch
 
     am = head_case["am"]
@@ -330,6 +330,38 @@ def test_accept_sampled_point_q_bit_exact(ctx, head_case, orc, opts):
         seen[ref[0]] = seen.get(ref[0], 0) + 1
     print("accepted-count histogram (point q)", opts, seen, flush=True)
     assert len(seen) >= 2
+
+
+@pytest.mark.parametrize("levels,top_p", [(3, 0.5), (7, 0.9), (2, 0.02), (40, 0.6), (1, 0.37)])
+def test_nucleus_ties_bit_exact(ctx, orc, levels, top_p):
+    """Rows whose logits take only a few distinct values, so the nucleus cut falls inside a tie
+    group spread over the whole vocabulary: the cut key from the four digit rounds, then the
+    j-th tie in id order found across the selection's blocks.  Drafts of q = 1e-12 (below every
+    p here) and, with one level, a uniform q equal to every p are accepted with certainty, so
+    the bonus row goes through the nucleus.  Bit for bit against the oracle."""
+    import torch
+
+    rng = np.random.default_rng(levels)
+    Vs, rows = 151936, 3
+    lv = rng.integers(0, levels, (rows, Vs)).astype(np.float32) * 0.25
+    logits = dev(lv)
+    out = torch.empty(2, dtype=torch.int32, device="cuda")
+    draft = rng.integers(0, Vs, rows - 1).astype(np.int32)
+    dd = dev(draft)
+    qp = np.full(rows - 1, 1e-12, np.float32)
+    dq = dev(qp)
+    q_mode = 1 if levels == 1 else 0
+    for trial in range(4):
+        torch.cuda.synchronize()
+        ctx.accept_sampled_ex(logits, rows, Vs, dd, q_mode, 91, trial, out, 1.0,
+                              q_point=dq if q_mode == 0 else None, top_p=top_p)
+        ctx.sync()
+        got = tuple(int(v) for v in host(out))
+        u = orc.verify_uniforms(91, trial, rows)
+        ref = orc.accept_sampled_ex(lv, draft, 1.0, q_mode, u,
+                                    q_point=qp if q_mode == 0 else None, top_p=top_p)
+        assert got == ref, (levels, top_p, trial, got, ref)
+        assert ref[0] == rows - 1, ref  # the bonus, through the nucleus
 
 
 @pytest.mark.parametrize("Vs,off,opts", [

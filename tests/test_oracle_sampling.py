@@ -316,3 +316,22 @@ def test_point_q_extremes(orc):
         assert acc_lo == rows - 1
         assert orc.accept_sampled(logits, draft, 1.0, 0, u, q_point=np.ones(rows - 1, np.float32)) \
             == orc.accept_sampled(logits, draft, 1.0, 0, u)
+
+
+def test_nucleus_equal_values_cut_by_id(orc):
+    """V equal e (= 1): the ranked order is the id order and each token carries mass 1, so the
+    kept set is exactly the first ceil(t) ids, t = top_p * Z in fp32 (the fewest whose mass
+    reaches the target, at least one), and the sample is the kept id at u * |kept|.  A cut one
+    token short or long, or ties broken by the higher id, would miss."""
+    for V in (1, 7, 100, 4096):
+        e = np.ones(V, np.float32)
+        Z = orc.canon_sum(e)
+        assert Z == V
+        for top_p in (0.0, 0.3, 0.5, 0.999, 1.0):
+            t = float(np.float32(top_p) * np.float32(Z))
+            n_kept = min(V, max(1, int(np.ceil(t))))
+            for u in (0.0, 0.25, 0.5, 0.9999):
+                tok = orc.nucleus_sample(e, Z, top_p, u)
+                want = max(0, int(np.ceil(float(np.float32(u) * np.float32(n_kept)))) - 1)
+                assert tok == want, (V, top_p, u, tok, want, n_kept)
+
