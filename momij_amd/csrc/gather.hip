@@ -144,10 +144,13 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     // current item computes.  Expert mode: block u serves expert u, whose ecnt[u] (row, slot)
     // pairs are listed at eplist[u * MJ_ROWS ..]; count and list are loaded together, and an
     // expert nobody picked ends here.  Bucket mode: block u serves the u-th expert of a Buckets
-    // table.  Dense: rows 0 .. dense_rows-1.
+    // table.  Dense: rows 0 .. dense_rows-1 in groups of R, block u taking group u (the blocks
+    // of a group stream the same weights, concurrently with the other groups' blocks).
     const int* plist = nullptr;
     int lpair = 0;  // expert modes: pair j of the list in lane j
-    int e = 0, np = a.dense_rows;
+    const bool dense_mode = !PER && a.ecnt == nullptr && a.bk == nullptr;
+    const int rbase = dense_mode ? R * u : 0;  // dense: first row of the block's group
+    int e = 0, np = dense_mode ? min(R, a.dense_rows - rbase) : a.dense_rows;
     int item = blockIdx.x;
     int rec_n = 0;  // the next item's record (persistent mode)
     extern __shared__ __align__(16) char g5lds[];
@@ -319,7 +322,8 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         uint16_t* xs = xs_of(b);
         float2* xsl = xsl_of(b);
         const int myr = min(pb + (lane < R ? lane : 0), npp - 1);
-        const int prl = (PER || a.ecnt) ? __shfl(lp, myr, MJ_WAVE) : (plist ? plist[myr] : myr);
+        const int prl =
+            (PER || a.ecnt) ? __shfl(lp, myr, MJ_WAVE) : (plist ? plist[myr] : rbase + myr);
         if constexpr (RES_PF) {
             // (after the pair list: the wait for a list load would cover these too)
             if (first && res_pf) {
@@ -328,7 +332,7 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int i = npass <= 4 ? q : 4 * q + r;
-                    resv[r] = a.y[(size_t)min(i, npass - 1) * a.N + col];
+                    resv[r] = a.y[(size_t)(rbase + min(i, npass - 1)) * a.N + col];
                 }
             }
         }
@@ -748,7 +752,7 @@ bool gather3_supported(int epi, int K, int N, int gs) {
 hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets,
                           hipStream_t st) {
     if (!gather3_supported(epi, a.K, a.N, a.gs)) return hipErrorInvalidValue;
-    const int rows = max_rows_per_bucket;
+    int rows = max_rows_per_bucket;
     // expert products over routed-expert slot records (at most 64 experts): persistent
     const bool per = a.srec != nullptr;
     if (per && (n_buckets > 64 || (epi != EPI_SWIGLU && epi != EPI_STORE)))
@@ -785,8 +789,14 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
                       : launch_g5<KPL, 128, E, W, KS128>(a, rows, n_buckets, st);
     // dense projections (qkv, o-proj: a few MB at most) spread over many small blocks, four
     // waves of one 16-row tile (group 64) or two (group 128): the unpack work of a block is
-    // then short, and the launch fills the chip
+    // then short, and the launch fills the chip.  More than 16 rows: one set of blocks per
+    // 16-row group, running side by side (each re-reads the small weight matrix) instead of
+    // one block unpacking its tile again for every further 16 rows.
     const bool dense = a.srec == nullptr && a.ecnt == nullptr && a.bk == nullptr;
+    if (dense) {
+        n_buckets = (a.dense_rows + 15) / 16;
+        rows = rows < 16 ? rows : 16;
+    }
     switch (epi) {
         case EPI_SWIGLU: MJ_G5(8, EPI_SWIGLU, 8, 2, 2)
         case EPI_ADD: MJ_G5(8, EPI_ADD, 4, 4, 2)
