@@ -32,22 +32,28 @@ def sources():
 
 
 # Kernels whose waits count their own outstanding vector-memory requests (s_waitcnt vmcnt(N)
-# with N > 0): a register spill would add scratch requests to that count, so none may spill.
+# with N > 0): a register spill to scratch memory would add requests to that count, so none
+# may use scratch (SGPR spills into VGPR lanes, which issue no memory requests, are allowed).
 COUNTED_WAIT_KERNELS = ("k_gather5", "k_lm_head")
 
 
 def _spills(stderr: str) -> list:
-    """(kernel, VGPR spill count) of the counted-wait kernels that spill, from the resource
-    remarks of one compile."""
+    """(kernel, what) of the counted-wait kernels that spill VGPRs or use scratch memory, from
+    the resource remarks of one compile."""
     out, cur = [], None
     for line in stderr.splitlines():
         m = re.search(r"Function Name: (\S+)", line)
         if m:
             cur = m.group(1)
             continue
+        if not cur or not any(k in cur for k in COUNTED_WAIT_KERNELS):
+            continue
         m = re.search(r"VGPRs Spill: (\d+)", line)
-        if m and cur and int(m.group(1)) > 0 and any(k in cur for k in COUNTED_WAIT_KERNELS):
-            out.append((cur, int(m.group(1))))
+        if m and int(m.group(1)) > 0:
+            out.append((cur, f"{m.group(1)} VGPR spills"))
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            out.append((cur, f"{m.group(1)} scratch bytes a lane"))
     return out
 
 

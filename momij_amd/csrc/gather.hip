@@ -118,7 +118,8 @@ __device__ __forceinline__ void lds_only_barrier() {
 // static LDS of the fused routing's slot records (persistent up || gate kernels)
 constexpr size_t G5_FUSED_REC_BYTES = 64 * MJ_G5_FUSED_ROWS;
 
-template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false>
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false,
+          bool FUS = false>
 // four waves per SIMD: two 8-wave blocks (or one 16-wave block) per CU
 __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gather5(
     GatherArgs a, int RA, int multi) {
@@ -167,9 +168,11 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
         // 16-byte read)
         uint8_t rank[64][MJ_G5_FUSED_ROWS];
     };
-    constexpr bool FUSABLE = PER && EPI == EPI_SWIGLU;
+    // (an instantiation of its own, FUS: the routing code stays out of the other kernels)
+    constexpr bool FUSABLE = FUS;
+    static_assert(!FUS || (PER && EPI == EPI_SWIGLU), "fused routing: persistent up || gate");
     __shared__ __align__(16) std::conditional_t<FUSABLE, FusedRoute, char> s_fr;
-    const bool fused = FUSABLE && a.rlogits != nullptr;
+    constexpr bool fused = FUS;
     uint32_t em = 0;
     uint64_t er = 0;
     // record of slot sl in the global records' form: pair j in lane j, expert id and pair count
@@ -732,6 +735,13 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     const bool multi = want > RA;
     int grid = n_buckets * ncb;
     if (PER && grid > persistent_blocks()) grid = persistent_blocks();
+    if constexpr (PER && EPI == EPI_SWIGLU) {
+        if (a.rlogits != nullptr) {
+            launch_timed(k_gather5<KPL, GS, EPI, WPB, KS, PER, ROWA, true>, dim3(grid),
+                         dim3(WPB * 64), S::lds(RA, multi || PER), st, a, RA, (int)multi);
+            return hipGetLastError();
+        }
+    }
     launch_timed(k_gather5<KPL, GS, EPI, WPB, KS, PER, ROWA>, dim3(grid), dim3(WPB * 64),
                  S::lds(RA, multi || PER), st, a, RA, (int)multi);
     return hipGetLastError();
@@ -810,9 +820,10 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
     return hipErrorInvalidValue;
 }
 
-template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false>
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false,
+          bool FUS = false>
 static hipError_t g5_attr() {
-    return hipFuncSetAttribute((const void*)k_gather5<KPL, GS, EPI, WPB, KS, PER, ROWA>,
+    return hipFuncSetAttribute((const void*)k_gather5<KPL, GS, EPI, WPB, KS, PER, ROWA, FUS>,
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)std::min(G5Shape<KPL, GS, EPI, WPB, KS>::lds(16, true),
                                              G5_LDS_MAX));
@@ -834,6 +845,11 @@ hipError_t set_gather3_attributes() {
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, 8, KS64, false, true>();       \
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, 8, KS128, false, true>();
     MJ_AA(8, EPI_SWIGLU, 2, 2) MJ_AA(2, EPI_STORE, 1, 1) MJ_AA(4, EPI_STORE, 1, 1)
+    // the fused-routing up || gate kernels
+    if (e == hipSuccess) e = g5_attr<8, 64, EPI_SWIGLU, 8, 2, true, false, true>();
+    if (e == hipSuccess) e = g5_attr<8, 128, EPI_SWIGLU, 8, 2, true, false, true>();
+    if (e == hipSuccess) e = g5_attr<8, 64, EPI_SWIGLU, 8, 2, true, true, true>();
+    if (e == hipSuccess) e = g5_attr<8, 128, EPI_SWIGLU, 8, 2, true, true, true>();
     MJ_AA(8, EPI_STORE, 2, 2)
 #undef MJ_AA
     return e;
