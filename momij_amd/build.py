@@ -25,6 +25,9 @@ FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-result", "-Wno-unused-value",
     "-I", os.path.join(ROOT, "include"), "-I", CSRC,
 ]
+# Measurement variants: MJ_BUILD_DEFINES="NAME=VALUE ..." adds -DNAME=VALUE to every compile
+# (e.g. MJ_TILE_MIN_ROWS=2 builds the one-row MoE through the VALU GEMV path).
+FLAGS += ["-D" + d for d in os.environ.get("MJ_BUILD_DEFINES", "").split()]
 
 
 def sources():

@@ -419,6 +419,13 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
     return MJ_OK;
 }
 
+// Fewest rows that take the MFMA tile path (fewer: the VALU dot2 GEMV path, k_qmv2).  1: one
+// row takes the tile path too, so that a verify row equals the one-row step bit for bit; the
+// one-row A/B of the two paths is built with 2.
+#ifndef MJ_TILE_MIN_ROWS
+#define MJ_TILE_MIN_ROWS 1
+#endif
+
 mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint16_t* y, int M,
                   int flags, const MoeScratch& ms, int32_t* inds, float* scores, hipStream_t st,
                   Prof* prof, const NormOut* next) {
@@ -432,7 +439,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
     // tile path: the top-k launch also lists each expert's (row, slot) pairs for the gathers.
     // One row takes it too, so a row's result does not depend on how many rows share its pass
     // (a verify row equals the one-row decode step at its position, bit for bit).
-    const bool tile = fused && M >= 1 && M <= MJ_MAX_ROWS && up_tile && dn_tile;
+    const bool tile = fused && M >= MJ_TILE_MIN_ROWS && M <= MJ_MAX_ROWS && up_tile && dn_tile;
     // up to 16 rows over at most 64 experts: the up || gate product ranks the logits itself
     // (its blocks build the slot records in LDS), one launch fewer
     const bool topk_in_up = tile && E <= 64 && M <= MJ_G5_FUSED_ROWS;

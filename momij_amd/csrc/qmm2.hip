@@ -111,7 +111,6 @@ hipError_t launch_qx_prep(const uint16_t* x, uint16_t* xperm, float2* xsum, int 
 // ---------------------------------------------------------------------------------------
 template <int LPR, int U, int EPI>
 __global__ __launch_bounds__(256) void k_qmv2(QmvArgs a) {
-    if (aborted(a.abort)) return;
     constexpr int SUB = 64 / LPR;
     constexpr int OUT_PER_IT = (EPI == EPI_SWIGLU ? SUB / 2 : SUB) * U;
     const int lane = threadIdx.x & 63;
@@ -124,10 +123,16 @@ __global__ __launch_bounds__(256) void k_qmv2(QmvArgs a) {
     const int sub = lane / LPR, li = lane % LPR;
     const int kw = a.K >> 4, kg = a.K / a.gs;
     const int gidx = (64 * li) / a.gs;
-    // The weight stream is the long latency: the expert id and the activation block are
-    // fetched first, the first iteration's codes, scales and biases requested as soon as the
-    // id is in, and the activation block formed while they arrive.
+    // The weight stream is the long latency: the expert id, the abort word and the activation
+    // block are fetched together first, the first iteration's codes, scales and biases
+    // requested as soon as the id is in, and the activation block formed while they arrive.
+    // The abort word is tested before anything is written (an aborted call writes nothing).
     const int e = a.inds[p];
+    // (a relaxed atomic load, with no branch around it: a vector load, waited for where it is
+    // tested; a scalar load, or one inside a branch, is waited for before the next loads)
+    const int ab = __hip_atomic_load(a.abort != nullptr ? a.abort : &a.inds[p], __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) &
+                   (a.abort != nullptr ? ~0 : 0);
     const uint16_t* xr = a.x + (size_t)(a.lhs_per ? p : 0) * a.K + 64 * li;
     u4v xraw[8];
 #pragma unroll
@@ -171,6 +176,7 @@ __global__ __launch_bounds__(256) void k_qmv2(QmvArgs a) {
         Bx = dot2(xp[i], code_base2(i), Bx);
     }
 
+    if (ab != 0) return;
     for (int o0 = wb; o0 < wend; o0 += OUT_PER_IT) {
         if (o0 != wb) request(o0);
         float part[U];
