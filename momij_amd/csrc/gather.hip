@@ -116,7 +116,7 @@ __device__ __forceinline__ void lds_only_barrier() {
 }
 
 // static LDS of the fused routing's slot records (persistent up || gate kernels)
-constexpr size_t G5_FUSED_REC_BYTES = 64 * MJ_G5_FUSED_ROWS;
+constexpr size_t G5_FUSED_REC_BYTES = 64 * (4 + 8);
 
 template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false,
           bool FUS = false>
@@ -164,9 +164,10 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     // row.  The last block also writes inds / scores and the global records for the down
     // product.
     struct FusedRoute {
-        // rank of expert t in row r, 0xFF where r did not pick t (rows of one expert in one
-        // 16-byte read)
-        uint8_t rank[64][MJ_G5_FUSED_ROWS];
+        // per expert t, set by LDS atomics as the rows are ranked: the rows that picked t (bit
+        // r) and t's rank in each (3 bits at 3r)
+        uint32_t em[64];
+        uint64_t er[64];
     };
     // (an instantiation of its own, FUS: the routing code stays out of the other kernels)
     constexpr bool FUSABLE = FUS;
@@ -211,6 +212,18 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
             for (int sr = 0; sr < 2; ++sr)
                 v[sr] = a.rlogits[min(wv + WPB * sr, M - 1) * E + min(lane, E - 1)];
             if (aborted(a.abort)) return;
+            if (wv == 0) {
+                s_fr.em[lane] = 0u;
+                s_fr.er[lane] = 0ull;
+            }
+            __syncthreads();  // (LDS only: the logits stay in flight)
+            // expert t picked by row r at rank rk: its bits, ORed in from any wave
+            auto mark = [&](int t, int r, int rk) {
+                __hip_atomic_fetch_or(&s_fr.em[t], 1u << r, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_fetch_or(&s_fr.er[t], (uint64_t)rk << (3 * r), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_WORKGROUP);
+            };
             const bool wr = blockIdx.x == gridDim.x - 1;  // writes inds / scores / records
 #pragma unroll
             for (int sr = 0; sr < 2; ++sr) {
@@ -221,32 +234,23 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
                 if (wr) {  // the selection with its weights
                     int ind = 0;
                     float gate = 0.0f;
-                    s_fr.rank[lane][r] = 0xFF;
                     row_topk<1>(s_row, E, k, s_ind, s_gate, ind, gate);
-                    if (lane < k) {  // (in order after the 0xFF above: one wave's LDS writes)
-                        s_fr.rank[ind][r] = (uint8_t)lane;
+                    if (lane < k) {
+                        mark(ind, r, lane);
                         a.rinds[r * k + lane] = ind;
                         a.rscores[r * k + lane] = gate;
                     }
                 } else {  // the selection only: the ranks of row_topk, no weights
                     const int rank = row_rank64(s_row, E);
-                    s_fr.rank[lane][r] = lane < E && rank < k ? (uint8_t)rank : (uint8_t)0xFF;
+                    if (lane < E && rank < k) mark(lane, r, rank);
                 }
                 __builtin_amdgcn_wave_barrier();
             }
             __syncthreads();
-            // lane t: the rows that picked expert t, and its rank in each (bytes of rows >= M
-            // were never written)
-            static_assert(MJ_G5_FUSED_ROWS == 16, "one 16-byte read an expert");
-            const u4v rb = *(const u4v*)s_fr.rank[lane];
-#pragma unroll
-            for (int r = 0; r < MJ_G5_FUSED_ROWS; ++r) {
-                const uint32_t b = (rb[r >> 2] >> (8 * (r & 3))) & 0xFFu;
-                if (r < M && b != 0xFFu) {
-                    em |= 1u << r;
-                    er |= (uint64_t)(b & 7u) << (3 * r);
-                }
-            }
+            // lane t: the rows that picked expert t, and its rank in each
+            static_assert(MJ_G5_FUSED_ROWS <= 16, "3-bit ranks of 16 rows in 64 bits");
+            em = s_fr.em[lane];
+            er = s_fr.er[lane];
             if (wr && wv == 0) {
                 const uint64_t on = __ballot(em != 0u);
                 const int total = __popcll(on);
