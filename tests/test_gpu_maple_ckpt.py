@@ -19,9 +19,11 @@ from tests.teacher import capture_pass, check_head, check_layer
 
 pytestmark = pytest.mark.gpu
 
-# absolute bound of the free-running comparisons (8 fp16 ulps at magnitude 4); the
-# teacher-forced block checks keep the 1e-2 bar
-FREE_RUN_ABS = 3.2e-2
+# Drift check, not the parity bar: absolute bound of the free-running comparisons, where the
+# oracle replays every pass on its own caches so both sides' rounding accumulates over the
+# layers (8 fp16 ulps at magnitude 4).  Parity itself is the teacher-forced block checks
+# (check_layer / check_head), which keep the 1e-2 absolute and 2e-2 relative-to-norm bar.
+DRIFT_ABS = 3.2e-2
 
 
 @pytest.fixture(scope="module")
@@ -101,7 +103,7 @@ def test_maple_checkpoint_prefill_and_verify(maple, orc):
     om.prefill(prompt[:-1])
     xf = om.rows(prompt[-1:], [-1])
     om.L += 1
-    assert_close(cap["head_in"][35:36], xf, abs_tol=FREE_RUN_ABS,
+    assert_close(cap["head_in"][35:36], xf, abs_tol=DRIFT_ABS,
                  what="prefill head input (free-running)")
     L0 = eng.offset
     cont, t = [], y
@@ -126,7 +128,7 @@ def test_maple_checkpoint_prefill_and_verify(maple, orc):
     # the free-running replay accumulates both sides' rounding over 4 layers and 109 positions:
     # the relative bar holds, single elements of magnitude ~4 may drift by a few fp16 ulps
     xf = om.rows([y] + draft, parents)
-    assert_close(cap["head_in"][:9], xf, abs_tol=FREE_RUN_ABS, what="verify head input (free-running)")
+    assert_close(cap["head_in"][:9], xf, abs_tol=DRIFT_ABS, what="verify head input (free-running)")
 
 
 def test_full_attention_capacity_guard(maple):

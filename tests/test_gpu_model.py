@@ -23,10 +23,11 @@ from tests.teacher import capture_pass, check_head, check_layer
 
 pytestmark = pytest.mark.gpu
 
-# absolute bound of the free-running comparisons (the oracle replays every pass on its own
-# caches, so both sides' rounding accumulates: 8 fp16 ulps at magnitude 4); the teacher-forced
-# block checks keep the 1e-2 bar
-FREE_RUN_ABS = 3.2e-2
+# Drift check, not the parity bar: absolute bound of the free-running comparisons, where the
+# oracle replays every pass on its own caches so both sides' rounding accumulates over the
+# layers (8 fp16 ulps at magnitude 4).  Parity itself is the teacher-forced block checks
+# (check_layer / check_head), which keep the 1e-2 absolute and 2e-2 relative-to-norm bar.
+DRIFT_ABS = 3.2e-2
 
 # 16 draft nodes, depth 6: 3 at depth 1, 2 under each, 2 under the first depth-2 node, then
 # 1-chains (3+6+2+2+2+1); row 0 is the fed token.
@@ -137,7 +138,7 @@ def test_prefill_and_chain_verify_vs_oracle(model, orc):
     om.prefill(prompt[:-1])
     xf = om.rows(prompt[-1:], [-1])
     om.L += 1
-    assert_close(cap["head_in"][Mlast - 1:Mlast], xf, abs_tol=FREE_RUN_ABS,
+    assert_close(cap["head_in"][Mlast - 1:Mlast], xf, abs_tol=DRIFT_ABS,
                  what="prefill head input (free-running)")
     cont = greedy_continuation(eng, y, 8)
     draft = cont[:5] + [int(t) for t in rng.integers(0, cfg.vocab, 3)]
@@ -154,7 +155,7 @@ def test_prefill_and_chain_verify_vs_oracle(model, orc):
     assert oacc == acc and list(oemit) == toks
     # and the oracle's own pass on its own caches stays within tolerance of the device's
     xf = om.rows([y] + draft, list(range(-1, 8)))
-    assert_close(cap["head_in"][:9], xf, abs_tol=FREE_RUN_ABS,
+    assert_close(cap["head_in"][:9], xf, abs_tol=DRIFT_ABS,
                  what="verify head input (free-running)")
 
 
