@@ -619,19 +619,20 @@ __global__ __launch_bounds__(64) void k_head_final(const float* pval, const int*
 __device__ __forceinline__ void accept_greedy_wave(int tok, int par, int am, int n,
                                                    StepResult* res, int32_t* out_flat) {
     const int lane = threadIdx.x & 63;
+    // (cur and next are wave-uniform: the row values are read with readlane, no LDS permute)
     int cur = 0, acc = 0, my_path = 0, my_emit = 0;
     for (;;) {
-        const int amc = __shfl(am, cur);
+        const int amc = __builtin_amdgcn_readlane(am, cur);
         const uint64_t kids = __ballot(lane < n && par == cur && tok == amc);
         if (!kids) break;
         const int next = __ffsll((unsigned long long)kids) - 1;
-        const int tn = __shfl(tok, next);
+        const int tn = __builtin_amdgcn_readlane(tok, next);
         if (lane == acc) my_emit = tn;
         ++acc;
         if (lane == acc) my_path = next;
         cur = next;
     }
-    const int fin = __shfl(am, cur);
+    const int fin = __builtin_amdgcn_readlane(am, cur);
     if (lane == acc) my_emit = fin;
     if (res) {
         if (lane == 0) {
@@ -673,8 +674,12 @@ __global__ __launch_bounds__(512) void k_head_final_accept(const float* pval, co
                                                            int nblk, int M, int32_t* out_idx,
                                                            float* out_max, const int* abort,
                                                            GreedyAccept ga) {
-    if (aborted(abort)) return;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    // the abort word requested with the partials, tested before anything is written (a
+    // relaxed atomic load, no branch around it: waited for only where it is tested)
+    const int ab = __hip_atomic_load(abort != nullptr ? abort : ga.tokens, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) &
+                   (abort != nullptr ? ~0 : 0);
     const int g = t & 7;                 // row group: rows 4g .. 4g + 3
     const int ng = (M + 3) >> 2;         // row groups in use
     __shared__ float s_v[8][32];
@@ -716,7 +721,7 @@ __global__ __launch_bounds__(512) void k_head_final_accept(const float* pval, co
         }
     }
     __syncthreads();
-    if (wv != 0) return;
+    if (wv != 0 || ab != 0) return;
     float bm = -INFINITY;
     int im = 0x7fffffff;
     if (lane < M)
