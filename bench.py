@@ -34,7 +34,7 @@ HBM_PEAK_GBS = 8000.0
 TREE16 = [-1, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 10, 11, 12, 13, 14]
 METRIC = "verify-step tokens/s (K=8, 1 GPU) + 2-bit gather-qmm HBM GB/s vs peak"
 TIMER_HOLD_MS = 0.020  # length of the calibration hold the library brackets (MJ_KERNEL_TIMER)
-UP_KERNEL = "void k_gather5<8, 64, 2, 8, 2, true, false>"  # the up||gate tile gather + SwiGLU
+UP_KERNEL = "void k_gather5<8, 64, 2, 8, 2, true, false, true>"  # up||gate gather, fused routing
 
 
 def log(*a):
