@@ -118,11 +118,16 @@ __device__ __forceinline__ void lds_only_barrier() {
 // static LDS of the fused routing's slot records (persistent up || gate kernels)
 constexpr size_t G5_FUSED_REC_BYTES = 64 * (4 + 8);
 
-template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false,
-          bool FUS = false>
-// four waves per SIMD: two 8-wave blocks (or one 16-wave block) per CU
-__global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gather5(
-    GatherArgs a, int RA, int multi) {
+// How one call of the tile-gather body fits into a launch.  MODE 0: the whole launch (the
+// standalone kernels).  The fused MoE kernel calls the up || gate body (MODE 1) and then the down
+// body (MODE 2) in every block; io carries the routing words from the first to the second.
+struct FuseIO {
+    uint32_t em = 0;  // lane t: rows that picked expert t (bit r)
+    uint64_t er = 0;  // ... and expert t's rank in each of them (3 bits at 3r)
+};
+
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER, bool ROWA, bool FUS, int MODE>
+__device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO& io) {
     using S = G5Shape<KPL, GS, EPI, WPB, KS>;
     constexpr int R = S::R, K = S::K, KB = S::KB, KBW = S::KBW, TPB = S::TPB, XS = S::XS;
     constexpr int SCW = S::SCW;
@@ -703,6 +708,15 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     buf ^= 1;
     early = true;
   }
+}
+
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false,
+          bool FUS = false>
+// four waves per SIMD: two 8-wave blocks (or one 16-wave block) per CU
+__global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_gather5(
+    GatherArgs a, int RA, int multi) {
+    FuseIO io;
+    g5_body<KPL, GS, EPI, WPB, KS, PER, ROWA, FUS, 0>(a, RA, multi, io);
 }
 
 // dynamic LDS a tile-gather launch may take (the device has 160 KB per workgroup)
