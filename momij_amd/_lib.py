@@ -112,6 +112,7 @@ _SIGS = {
     "mj_set_stream": (i32, [vp, vp]),
     "mj_get_stream": (vp, [vp]),
     "mj_set_abort": (i32, [vp, i32]),
+    "mj_set_wait_limit": (i32, [vp, i32]),
     "mj_sync": (i32, [vp]),
     "mj_alloc": (i32, [vp, C.c_size_t, C.POINTER(vp)]),
     "mj_free": (i32, [vp, vp]),

@@ -37,7 +37,7 @@ def sources():
 # Kernels whose waits count their own outstanding vector-memory requests (s_waitcnt vmcnt(N)
 # with N > 0): a register spill to scratch memory would add requests to that count, so none
 # may use scratch (SGPR spills into VGPR lanes, which issue no memory requests, are allowed).
-COUNTED_WAIT_KERNELS = ("k_gather5", "k_lm_head")
+COUNTED_WAIT_KERNELS = ("k_gather5", "k_moe_fused", "k_lm_head")
 
 
 def _spills(stderr: str) -> list:

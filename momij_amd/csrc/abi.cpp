@@ -99,7 +99,16 @@ mj_status mj_abort_end(mj_ctx* ctx, unsigned gen) {
     const unsigned now = ctx->abort_gen.load();
     const bool ab = ctx->abort_host.load() || now != gen;
     ctx->synced_gen = now;
-    return ab ? mj_fail(ctx, MJ_ABORTED, "aborted by the abort word") : MJ_OK;
+    if (ab) return mj_fail(ctx, MJ_ABORTED, "aborted by the abort word");
+    // the kernels that set the fault word have completed: the caller has synchronised
+    if (ctx->fault && __atomic_load_n(ctx->fault, __ATOMIC_ACQUIRE) != 0) {
+        __atomic_store_n(ctx->fault, 0, __ATOMIC_RELEASE);
+        return mj_fail(ctx, MJ_HIP_ERROR,
+                       "fused MoE launch: a block's wait for the up product ran out its bound "
+                       "(blocks not co-resident: another stream's kernels on the device?); the "
+                       "results since the last synchronising call are invalid");
+    }
+    return MJ_OK;
 }
 
 extern "C" {
@@ -139,12 +148,16 @@ mj_status mj_init(int device, mj_ctx** out) {
         hipHostMalloc(&c->abort_src, 2 * sizeof(int), hipHostMallocDefault) != hipSuccess ||
         hipMalloc(&c->abort_dev, sizeof(int)) != hipSuccess ||
         hipMemset(c->abort_dev, 0, sizeof(int)) != hipSuccess ||
+        hipHostMalloc(&c->fault, sizeof(int), hipHostMallocMapped | hipHostMallocCoherent) !=
+            hipSuccess ||
+        hipHostGetDevicePointer((void**)&c->fault_dev, c->fault, 0) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         mj_destroy(c);
         return MJ_HIP_ERROR;
     }
     c->abort_src[0] = 0;
     c->abort_src[1] = 1;
+    *c->fault = 0;
     c->stream = c->own;
     *out = c;
     return MJ_OK;
@@ -158,6 +171,7 @@ mj_status mj_destroy(mj_ctx* ctx) {
     if (ctx->scratch) hipFree(ctx->scratch);
     if (ctx->abort_dev) hipFree(ctx->abort_dev);
     if (ctx->abort_src) hipHostFree(ctx->abort_src);
+    if (ctx->fault) hipHostFree(ctx->fault);
     if (ctx->own) hipStreamDestroy(ctx->own);
     if (ctx->ctl) hipStreamDestroy(ctx->ctl);
     delete ctx;
@@ -196,6 +210,12 @@ mj_status mj_set_abort(mj_ctx* ctx, int flag) {
     if (e == hipSuccess && !v) ctx->abort_host.store(0);
     if (prev >= 0) hipSetDevice(prev);
     return e == hipSuccess ? MJ_OK : MJ_HIP_ERROR;
+}
+
+mj_status mj_set_wait_limit(mj_ctx* ctx, int polls) {
+    if (!ctx || polls < 0) return MJ_INVALID_ARG;
+    ctx->wait_polls = polls;
+    return MJ_OK;
 }
 
 // Reports MJ_ABORTED when the word is set, or was set since the previous synchronising call:
@@ -407,6 +427,7 @@ void moe_scratch_layout(Arena& a, int H, int I, int E, int k, int M, MoeScratch&
     ms.ecnt = (int*)a.take((size_t)E * 4);
     ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
     ms.srec = (int*)a.take((size_t)64 * 64 * 4);
+    ms.fcnt = (int*)a.take((size_t)MJ_FCNT * MJ_FCNT_STRIDE * 4);
 }
 
 mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms) {
@@ -418,6 +439,12 @@ mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch
     moe_scratch_layout(real, H, I, E, k, M, ms);
     return MJ_OK;
 }
+
+// 1: passes that rank the routing inside the up product run both expert products as one
+// launch (moe_fused_supported shapes); 0: two launches (kept for measurement).
+#ifndef MJ_MOE_FUSED
+#define MJ_MOE_FUSED 1
+#endif
 
 // Fewest rows that take the MFMA tile path (fewer: the VALU dot2 GEMV path, k_qmv2).  1: one
 // row takes the tile path too, so that a verify row equals the one-row step bit for bit; the
@@ -443,6 +470,11 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
     // up to 16 rows over at most 64 experts: the up || gate product ranks the logits itself
     // (its blocks build the slot records in LDS), one launch fewer
     const bool topk_in_up = tile && E <= 64 && M <= MJ_G5_FUSED_ROWS;
+    // ... and then the down product in the same launch (the common expert shape)
+    const bool moe_fused =
+        MJ_MOE_FUSED && topk_in_up && ms.fcnt != nullptr &&
+        (w->up_gate_alpha == nullptr) == (w->down_alpha == nullptr) &&
+        moe_fused_supported(H, I, E, w->gs, M, w->up_gate_alpha != nullptr);
     if (fused) {
         RouteArgs ra{};
         ra.x = x;
@@ -463,6 +495,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.k = k;
         ra.eps = w->eps;
         ra.abort = ab;
+        ra.fcnt = moe_fused ? ms.fcnt : nullptr;
         s = mj_hip(ctx, launch_route_logits(ra, H, st), "route");
         if (s != MJ_OK) return s;
         if (!topk_in_up) {
@@ -564,10 +597,13 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
             up.rscores = scores;
             up.rsrec = ms.srec;
         }
-        if (prof) prof->begin(PROF_UP, st);
-        s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, tile ? E : nb, st), "up gather");
-        if (prof) prof->end(st);
-        if (s != MJ_OK) return s;
+        up.fcnt = moe_fused ? ms.fcnt : nullptr;
+        if (!moe_fused) {
+            if (prof) prof->begin(PROF_UP, st);
+            s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, tile ? E : nb, st), "up gather");
+            if (prof) prof->end(st);
+            if (s != MJ_OK) return s;
+        }
         // the tile kernel's SwiGLU epilogue writes act without block sums: the tile down
         // kernel forms them from its staged rows, any other down kernel gets them here
         if (up_tile && !dn_tile) {
@@ -587,10 +623,20 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         dn.K = I;
         dn.N = H;
         dn.x_div = 1;
-        if (prof) prof->begin(PROF_DOWN, st);
-        s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, tile ? E : nb, st), "down gather");
-        if (prof) prof->end(st);
-        if (s != MJ_OK) return s;
+        if (moe_fused) {
+            dn.rk = k;  // the down phase forms its records from the routing words too
+            dn.fpolls = ctx->wait_polls;
+            dn.ffault = ctx->fault_dev;
+            if (prof) prof->begin(PROF_MOE, st);
+            s = mj_hip(ctx, launch_moe_fused(up, dn, M, st), "fused MoE gathers");
+            if (prof) prof->end(st);
+            if (s != MJ_OK) return s;
+        } else {
+            if (prof) prof->begin(PROF_DOWN, st);
+            s = mj_hip(ctx, launch_gather(dn, EPI_STORE, M, tile ? E : nb, st), "down gather");
+            if (prof) prof->end(st);
+            if (s != MJ_OK) return s;
+        }
     }
     const uint16_t* resid = (flags & MJ_MOE_RESIDUAL) ? x : nullptr;
     if (next && H == 2048)

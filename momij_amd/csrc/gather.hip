@@ -29,6 +29,13 @@ __device__ __forceinline__ void load_lds16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
 }
 
+// the same with a cache policy (16: sc1, device-coherent: sees stores of other XCDs made with
+// sc1 once they have completed)
+template <int CPOL>
+__device__ __forceinline__ void load_lds16c(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, CPOL);
+}
+
 // 4 bytes per lane, landing at lds + 4 * lane
 __device__ __forceinline__ void load_lds4(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 4, 0, 0);
@@ -179,8 +186,13 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     static_assert(!FUS || (PER && EPI == EPI_SWIGLU), "fused routing: persistent up || gate");
     __shared__ __align__(16) std::conditional_t<FUSABLE, FusedRoute, char> s_fr;
     constexpr bool fused = FUS;
-    uint32_t em = 0;
-    uint64_t er = 0;
+    static_assert(MODE == 0 || (MODE == 1 && FUS) || (MODE == 2 && PER && EPI == EPI_STORE),
+                  "fused MoE phases: up || gate with routing, then down");
+    // slot records from the routing words in registers: the ranking kernel itself, or the down
+    // phase of the fused MoE launch (words handed over by its up phase)
+    constexpr bool RREC = FUS || MODE == 2;
+    uint32_t em = MODE == 2 ? io.em : 0u;
+    uint64_t er = MODE == 2 ? io.er : 0ull;
     // record of slot sl in the global records' form: pair j in lane j, expert id and pair count
     // in the high halves of lanes 0 and 1 (count 0 past the last routed expert)
     auto fused_rec = [&](int sl) -> int {
@@ -256,6 +268,8 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             static_assert(MJ_G5_FUSED_ROWS <= 16, "3-bit ranks of 16 rows in 64 bits");
             em = s_fr.em[lane];
             er = s_fr.er[lane];
+            io.em = em;
+            io.er = er;
             if (wr && wv == 0) {
                 const uint64_t on = __ballot(em != 0u);
                 const int total = __popcll(on);
@@ -284,8 +298,15 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     {
         const int ab = !fused && a.abort ? *a.abort : 0;  // fused: checked with the logits
         if constexpr (PER) {
-            const int rec = fused ? fused_rec(min(item / ncb, 63))
-                                  : a.srec[min(item / ncb, 63) * MJ_ROWS + lane];
+            if constexpr (MODE == 2) {
+                // blocks with one up item fewer come free first: they take the first down items
+                // (slots in increasing order, the order the up items complete in)
+                const int nS = __popcll(__ballot(em != 0u));
+                const int G = (int)gridDim.x, rem = (nS * a.fup_ncb) % G;
+                item = (int)blockIdx.x >= rem ? (int)blockIdx.x - rem : (int)blockIdx.x + (G - rem);
+            }
+            const int rec = RREC ? fused_rec(min(item / ncb, 63))
+                                 : a.srec[min(item / ncb, 63) * MJ_ROWS + lane];
             e = __builtin_amdgcn_readlane(rec, 0) >> 16;
             np = item / ncb < 64 ? __builtin_amdgcn_readlane(rec, 1) >> 16 : 0;
             lpair = rec & 0xFFFF;
@@ -357,7 +378,8 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
                 const char* src = (const char*)(a.xperm + (size_t)(pr / a.x_div) * K);
 #pragma unroll
                 for (int i = 0; i < PPR / 64; ++i)
-                    load_lds16(src + 1024 * i + 16 * lane, (char*)(xs + r * XS) + 1024 * i);
+                    load_lds16c<MODE == 2 ? 16 : 0>(src + 1024 * i + 16 * lane,
+                                                    (char*)(xs + r * XS) + 1024 * i);
                 if (!own_sums && lane < KB / 2)
                     load_lds16((const char*)(a.xsum + (size_t)(pr / a.x_div) * KB) + 16 * lane,
                                xsl + r * S::SS);
@@ -434,12 +456,53 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     // reduction and epilogue; the item's rows are staged after the block is done with the old
     // ones, so the item starts once everything it issued has landed
     bool early = false;
+    // fused MoE launch.  Up phase: an item's act rows are stored device-coherent (sc1); once
+    // every wave's stores of it have completed (the next barrier that waits for them) one
+    // thread counts it in fcnt[slot].  Down phase: a wave stages an item's rows only when the
+    // slot's count is complete (a bounded wait: the launch is sized so that every block is
+    // resident, two a CU, and then the counts complete; a wait that runs out its bound sets
+    // the fault word, which the host reports, and goes on, so the launch always ends)
+    int sig_slot = -1;
+    bool next_ready = true;  // down phase: the next item's slot count was complete
+    auto signal_done = [&]() {
+        if constexpr (MODE == 1) {
+            if (tid == 0 && sig_slot >= 0)
+                __hip_atomic_fetch_add(a.fcnt + sig_slot * MJ_FCNT_STRIDE, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            sig_slot = -1;
+        }
+    };
+    auto slot_ready = [&](int sl) -> bool {
+        return __hip_atomic_load(a.fcnt + sl * MJ_FCNT_STRIDE, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) >=
+               a.fup_ncb;
+    };
+    auto wait_slot = [&](int sl) {
+        bool ok = slot_ready(sl);
+        for (int it = 0; !ok && it < a.fpolls; ++it) {
+            if ((it & 63) == 63 && aborted(a.abort)) return;
+            __builtin_amdgcn_s_sleep(8);
+            ok = slot_ready(sl);
+        }
+        if (!ok && a.ffault != nullptr && lane == 0)
+            __hip_atomic_store(a.ffault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    };
 
   for (;;) {
     const int npass0 = min(RA, np);
     if (!early) {
-        stage_load(0, npass0, buf, lpair, np, true);  // ahead of the weights (loads return in order)
-        issue_weights(e, cb);
+        if constexpr (MODE == 2) {
+            // the weights do not depend on the up phase: requested first, the rows once the
+            // slot is complete (the count, requested before the weights, is waited for alone)
+            const bool ready = slot_ready(item / ncb);
+            issue_weights(e, cb);
+            if (!ready) wait_slot(item / ncb);
+            stage_load(0, npass0, buf, lpair, np, true);
+            early = true;  // everything issued lands before the first pass
+        } else {
+            stage_load(0, npass0, buf, lpair, np, true);  // ahead of the weights (loads return in order)
+            issue_weights(e, cb);
+        }
     }
     const UnpackK uk = unpack_consts();
     const int xrow = min(n, RA - 1);
@@ -461,6 +524,8 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             lds_barrier<G + NSB>();
         else
             lds_barrier<0>();
+        // (every wave's stores of the previous item have completed: the barrier waits for them)
+        if (pb == 0) signal_done();
         if (own_sums) {
             own_block_sums(npass);
             lds_barrier<G + NSB>();
@@ -472,9 +537,15 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         constexpr int PF = PER ? 1 : 0;
         if constexpr (PER) {
             if (pb == 0) {
-                const int* rp = fused ? (const int*)a.rlogits
-                                      : a.srec + min((item + (int)gridDim.x) / ncb, 63) * MJ_ROWS + lane;
-                rec_n = *rp;
+                if constexpr (MODE == 2) {
+                    // the next item's slot count (device-coherent), for its rows below
+                    rec_n = __hip_atomic_load(a.fcnt + min((item + (int)gridDim.x) / ncb, MJ_FCNT - 1) * MJ_FCNT_STRIDE,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    const int* rp = fused ? (const int*)a.rlogits
+                                          : a.srec + min((item + (int)gridDim.x) / ncb, 63) * MJ_ROWS + lane;
+                    rec_n = *rp;
+                }
             }
         }
         wait_vmcnt<G + PF>();      // scales and biases have landed
@@ -606,7 +677,12 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         int np_next = 0;
         if constexpr (PER) {
             const int nx = item + (int)gridDim.x;
-            if (fused) rec_n = fused_rec(min(nx / ncb, 63)) | (rec_n & (int)opaque(0u));
+            if constexpr (MODE == 2) {
+                // the first pass holds the count (a later pass of the item finds the record)
+                if (pb == 0) next_ready = __builtin_amdgcn_readfirstlane(rec_n) >= a.fup_ncb;
+                rec_n = fused_rec(min(nx / ncb, 63));
+            } else if (fused)
+                rec_n = fused_rec(min(nx / ncb, 63)) | (rec_n & (int)opaque(0u));
             np_next = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
             stage_next = pb + RA >= np && nx / ncb < 64 && np_next > 0;
             if (stage_next) issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16, nx % ncb);
@@ -637,6 +713,9 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             if (stage_next) {
                 // every wave has read its rows (the K-slice barrier, or this one)
                 if constexpr (KS == 1) lds_only_barrier();
+                if constexpr (MODE == 2) {
+                    if (!next_ready) wait_slot((item + (int)gridDim.x) / ncb);
+                }
                 stage_load(0, min(RA, np_next), buf ^ 1, rec_n & 0xFFFF, np_next);
             }
         }
@@ -653,7 +732,11 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
                 up = fminf(fmaxf(up, -7.0f), 7.0f);
                 const float act = hround(g / (1.0f + expf(-g)) * up);
                 const int j = (cb * TPB + tt) * 8 + (n & 7);
-                a.y[(size_t)s_pair[buf][i] * I + (j & ~15) + perm_pos(j & 15)] = f2h(act);
+                uint16_t* dst = a.y + (size_t)s_pair[buf][i] * I + (j & ~15) + perm_pos(j & 15);
+                if constexpr (MODE == 1)
+                    __hip_atomic_store(dst, f2h(act), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    *dst = f2h(act);
             };
             if constexpr (NR == 1) {
                 const float recv = __shfl_xor(acc[0], 8, MJ_WAVE);
@@ -698,6 +781,7 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         run_pass(std::integral_constant<int, 4>{}, pb, npass);
     }
     if constexpr (!PER) break;
+    if constexpr (MODE == 1) sig_slot = item / ncb;  // counted once its stores have completed
     item += gridDim.x;
     if (item / ncb >= 64) break;
     np = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
@@ -708,6 +792,10 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     buf ^= 1;
     early = true;
   }
+  if constexpr (MODE == 1) {
+      lds_barrier<0>();  // every wave's stores of the last item have completed
+      signal_done();
+  }
 }
 
 template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false,
@@ -717,6 +805,20 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
     GatherArgs a, int RA, int multi) {
     FuseIO io;
     g5_body<KPL, GS, EPI, WPB, KS, PER, ROWA, FUS, 0>(a, RA, multi, io);
+}
+
+// Fused MoE launch (H = 2048, I = 1024): the up || gate product with its routing, then the down
+// product, in the same persistent blocks.  A block that has finished its up items takes down
+// items (blocks with fewer up items first, slots in increasing order) and stages an item's act
+// rows once every up item of its slot has completed, so the up product's last round overlaps
+// the down product, which needs no launch or record read of its own.
+template <int GS, bool ROWA>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_fused(
+    GatherArgs up, GatherArgs dn, int ra_up, int ra_dn, int multi_up, int multi_dn) {
+    FuseIO io;
+    g5_body<8, GS, EPI_SWIGLU, 8, 2, true, ROWA, true, 1>(up, ra_up, multi_up, io);
+    __syncthreads();  // every wave is done with the up phase's LDS
+    g5_body<4, GS, EPI_STORE, 8, 1, true, ROWA, false, 2>(dn, ra_dn, multi_dn, io);
 }
 
 // dynamic LDS a tile-gather launch may take (the device has 160 KB per workgroup)
@@ -838,6 +940,72 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
     return hipErrorInvalidValue;
 }
 
+// static LDS of the fused MoE kernel: both phases' pair lists and the routing words
+constexpr size_t G5_FUSED_MOE_STAT = 256 + 256 + G5_FUSED_REC_BYTES;
+
+// rows staged a pass by the two phases, and the dynamic LDS of the launch
+template <int GS>
+static size_t moe_fused_lds(int rows, int& ra_up, int& ra_dn) {
+    using SU = G5Shape<8, GS, EPI_SWIGLU, 8, 2>;
+    using SD = G5Shape<4, GS, EPI_STORE, 8, 1>;
+    const int want = rows < 1 ? 1 : rows;
+    const size_t limit = 80 * 1024 - G5_FUSED_MOE_STAT;  // two blocks a CU
+    ra_up = want < 16 ? want : 16;
+    ra_dn = ra_up;
+    while (ra_up > 1 && SU::lds(ra_up, true) > limit) --ra_up;
+    while (ra_dn > 1 && SD::lds(ra_dn, true) > limit) --ra_dn;
+    return std::max(SU::lds(ra_up, true), SD::lds(ra_dn, true));
+}
+
+// every block of the launch resident at once: two a CU at the largest footprint (16 rows)
+template <int GS, bool ROWA>
+static bool moe_fused_resident() {
+    static int ok = -1;
+    if (ok < 0) {
+        int ra_up = 0, ra_dn = 0, n = 0;
+        const size_t lds = moe_fused_lds<GS>(MJ_G5_FUSED_ROWS, ra_up, ra_dn);
+        ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_moe_fused<GS, ROWA>, 512, lds) ==
+                     hipSuccess &&
+             n >= 2;
+    }
+    return ok == 1;
+}
+
+template <int GS, bool ROWA>
+static hipError_t launch_moe_fused_t(GatherArgs up, GatherArgs dn, int rows, hipStream_t st) {
+    using SU = G5Shape<8, GS, EPI_SWIGLU, 8, 2>;
+    const int want = rows < 1 ? 1 : rows;
+    int ra_up = 0, ra_dn = 0;
+    const size_t lds = moe_fused_lds<GS>(rows, ra_up, ra_dn);
+    up.fup_ncb = up.N / (16 * SU::TPB);
+    dn.fup_ncb = up.fup_ncb;
+    dn.fcnt = up.fcnt;
+    launch_timed(k_moe_fused<GS, ROWA>, dim3(persistent_blocks()), dim3(512), lds, st, up, dn,
+                 ra_up, ra_dn, (int)(want > ra_up), (int)(want > ra_dn));
+    return hipGetLastError();
+}
+
+bool moe_fused_supported(int H, int I, int E, int gs, int M, bool rowa) {
+    if (!(H == 2048 && I == 1024 && E <= 64 && (gs == 64 || gs == 128) && M >= 1 &&
+          M <= MJ_G5_FUSED_ROWS))
+        return false;
+    if (gs == 64) return rowa ? moe_fused_resident<64, true>() : moe_fused_resident<64, false>();
+    return rowa ? moe_fused_resident<128, true>() : moe_fused_resident<128, false>();
+}
+
+hipError_t launch_moe_fused(const GatherArgs& up, const GatherArgs& dn, int rows, hipStream_t st) {
+    const bool rowa = up.alpha != nullptr;
+    if (!moe_fused_supported(up.K, dn.K, up.rE, up.gs, up.rM, rowa) || up.N != 2 * dn.K ||
+        dn.N != up.K || up.rlogits == nullptr || up.fcnt == nullptr || up.srec == nullptr ||
+        dn.srec == nullptr)
+        return hipErrorInvalidValue;
+    if (up.gs == 64)
+        return rowa ? launch_moe_fused_t<64, true>(up, dn, rows, st)
+                    : launch_moe_fused_t<64, false>(up, dn, rows, st);
+    return rowa ? launch_moe_fused_t<128, true>(up, dn, rows, st)
+                : launch_moe_fused_t<128, false>(up, dn, rows, st);
+}
+
 template <int KPL, int GS, int EPI, int WPB, int KS, bool PER = false, bool ROWA = false,
           bool FUS = false>
 static hipError_t g5_attr() {
@@ -863,6 +1031,17 @@ hipError_t set_gather3_attributes() {
     if (e == hipSuccess) e = g5_attr<KPL, 64, E, 8, KS64, false, true>();       \
     if (e == hipSuccess) e = g5_attr<KPL, 128, E, 8, KS128, false, true>();
     MJ_AA(8, EPI_SWIGLU, 2, 2) MJ_AA(2, EPI_STORE, 1, 1) MJ_AA(4, EPI_STORE, 1, 1)
+    // the fused MoE kernels
+    {
+        int ra_up = 0, ra_dn = 0;
+        const int lds = (int)std::min(std::max(moe_fused_lds<64>(MJ_G5_FUSED_ROWS, ra_up, ra_dn),
+                                               moe_fused_lds<128>(MJ_G5_FUSED_ROWS, ra_up, ra_dn)),
+                                      G5_LDS_MAX);
+        const void* ks[] = {(const void*)k_moe_fused<64, false>, (const void*)k_moe_fused<64, true>,
+                            (const void*)k_moe_fused<128, false>, (const void*)k_moe_fused<128, true>};
+        for (const void* k : ks)
+            if (e == hipSuccess) e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    }
     // the fused-routing up || gate kernels
     if (e == hipSuccess) e = g5_attr<8, 64, EPI_SWIGLU, 8, 2, true, false, true>();
     if (e == hipSuccess) e = g5_attr<8, 128, EPI_SWIGLU, 8, 2, true, false, true>();

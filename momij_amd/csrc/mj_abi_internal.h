@@ -27,6 +27,12 @@ struct mj_ctx {
     std::atomic<unsigned> abort_gen{0};
     unsigned synced_gen = 0;       // abort_gen the owning thread's last synchronising call saw
     std::mutex abort_mu;           // one set or clear at a time
+    // Fault word of the fused MoE launch (pinned, mapped: device writes land in host memory):
+    // a block whose wait for the up product's items ran out its bound of polls sets it, and the
+    // next synchronising call reports MJ_HIP_ERROR and clears it.
+    int* fault = nullptr;
+    int* fault_dev = nullptr;
+    int wait_polls = 1 << 17;      // that bound (mj_set_wait_limit)
     void* scratch = nullptr;       // op-level scratch arena
     size_t scratch_bytes = 0;
     std::string err;
@@ -53,6 +59,7 @@ struct MoeScratch {
     int* ecnt;           // pairs per expert [E]
     int* eplist;         // pair lists per expert [E][MJ_ROWS]
     int* srec;           // routed-expert slot records [64][64] (E <= 64)
+    int* fcnt;           // slot counters of the fused MoE launch [MJ_FCNT][MJ_FCNT_STRIDE]
     bool want_plain = false;  // also write the normed rows plain into xn (debug capture)
 };
 
@@ -60,7 +67,8 @@ struct MoeScratch {
 enum {
     PROF_UP = 0, PROF_DOWN = 1, PROF_HEAD = 2, PROF_ATTN = 3, PROF_DENSE = 4,
     PROF_TIMER = 5,  // brackets around a hold of PROF_TIMER_US: bracket - hold = timer cost
-    PROF_CLASSES = 6
+    PROF_MOE = 6,    // up || gate then down in one launch (the fused MoE kernel)
+    PROF_CLASSES = 7
 };
 constexpr unsigned PROF_TIMER_US = 20;
 struct Prof {

@@ -118,8 +118,18 @@ struct GatherArgs {
     int32_t* rinds;
     float* rscores;
     int* rsrec;
+    // fused MoE launch (up || gate then down in one kernel): fcnt[s] counts the finished up
+    // items of routed-expert slot s (zeroed by the router-logits launch before it); a down item
+    // of slot s starts once fcnt[s] reaches fup_ncb, the up product's column blocks
+    int* fcnt;
+    int fup_ncb;
+    int fpolls;   // bound of a down item's wait, in polls of its slot's count
+    int* ffault;  // set (system scope) by a wait that ran out its bound (nullable)
 };
 #define MJ_G5_FUSED_ROWS 16
+#define MJ_FCNT 64  // slot counters of the fused MoE launch
+#define MJ_FCNT_STRIDE 32  // ints between two counters: one 128-byte line each (the atomics of
+                           // different slots do not queue on one line)
 
 struct QmvArgs {
     const uint16_t* x;      // plain fp16 [rows_x][K]
@@ -144,6 +154,10 @@ hipError_t launch_selftest_mfma(const uint16_t* A, const uint16_t* B, float* D, 
 
 // gather.hip: the tile gather (one 16-row weight tile over the whole K per wave)
 bool gather3_supported(int epi, int K, int N, int gs);
+// the fused MoE launch: up || gate with its routing, then down, in one persistent kernel
+// (the shapes, and two blocks of the launch resident a CU: its waits assume every block runs)
+bool moe_fused_supported(int H, int I, int E, int gs, int M, bool rowa);
+hipError_t launch_moe_fused(const GatherArgs& up, const GatherArgs& dn, int rows, hipStream_t st);
 hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket, int n_buckets,
                           hipStream_t st);
 
@@ -295,6 +309,8 @@ struct RouteArgs {
     int M, E, k;
     float eps;
     const int* abort;
+    int* fcnt;               // slot counters of the fused MoE launch that follows (nullable):
+                             // zeroed here, before that launch reads them
 };
 bool route_supported(int H, int E, int k);
 hipError_t launch_route_logits(const RouteArgs& a, int H, hipStream_t st);

@@ -422,6 +422,7 @@ __global__ __launch_bounds__(256) void k_route_logits(RouteArgs a) {
         }
     }
     *(u4v*)(xn + 8 * tid) = xv;
+    if (a.fcnt && blockIdx.x == 0 && tid < MJ_FCNT) a.fcnt[tid * MJ_FCNT_STRIDE] = 0;
     if (grp == 0) {
         if (a.xn) *(u4v*)(a.xn + (size_t)r * RT_H + 8 * tid) = xv;
         if (a.xperm)

@@ -170,7 +170,8 @@ class VerifyEngine:
     def last_pass_ms(self) -> float:
         return float(self.lib.mj_model_last_pass_ms(self.h))
 
-    KERNEL_CLASSES = ("expert_up", "expert_down", "lm_head", "attention", "dense", "timer")
+    KERNEL_CLASSES = ("expert_up", "expert_down", "lm_head", "attention", "dense", "timer",
+                      "expert_moe")
 
     def profile(self, enable: bool):
         self.ctx.check(self.lib.mj_model_profile(self.h, int(enable)))

@@ -56,6 +56,10 @@ class Context:
     def set_abort(self, flag: bool):
         self.check(self.lib.mj_set_abort(self.h, int(flag)))
 
+    def set_wait_limit(self, polls: int):
+        """Bound of the fused MoE launch's waits for its up product, in polls."""
+        self.check(self.lib.mj_set_wait_limit(self.h, int(polls)))
+
     # ---------------------------------------------------------------- ops
     def gather_qmm2(self, x, w, scales, biases, inds, y, M, ktop, K, N, gs, lhs_per_expert=False,
                     epilogue=_lib.MJ_EPI_STORE):

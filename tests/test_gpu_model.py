@@ -420,6 +420,43 @@ def test_graph_replays_equal_eager(model):
     assert all(r == results[0] for r in results), results
 
 
+def test_fused_moe_wait_bound_reported(model):
+    """The fused MoE launch's waits for its up product: one that runs out its bound is reported
+    by the synchronising call (MJ_HIP_ERROR) and the report is cleared.  With no polls allowed,
+    a pass either finds every slot complete at its first check, and then equals the normal pass,
+    or fails with that report; the normal pass after it is unaffected."""
+    from momij_amd._lib import MomijError
+
+    eng, cfg, ctx = model["eng"], model["cfg"], model["ctx"]
+    print("case: 9-row chain verify, fused MoE waits bounded to 0 polls", flush=True)
+    rng = np.random.default_rng(8)
+    eng.rewind(0)
+    y = eng.prefill(rng.integers(0, cfg.vocab, 40).tolist())
+    L0 = eng.offset
+    draft = [int(t) for t in rng.integers(0, cfg.vocab, 8)]
+    eng.set_graphs(False)
+    faults = 0
+    try:
+        eng.rewind(L0)
+        want = eng.verify_greedy(y, draft)
+        ctx.set_wait_limit(0)
+        for _ in range(4):
+            eng.rewind(L0)
+            try:
+                got = eng.verify_greedy(y, draft)
+            except MomijError as e:
+                assert e.status == 6 and "fused MoE" in str(e), e
+                faults += 1
+            else:
+                assert got == want
+    finally:
+        ctx.set_wait_limit(1 << 17)
+        eng.set_graphs(True)
+    eng.rewind(L0)
+    assert eng.verify_greedy(y, draft) == want
+    print("passes with a reported wait", faults, "of 4", flush=True)
+
+
 def test_teacher_forced_layers(model, orc):
     """Each layer of a tree verify pass re-run by the oracle from the device's own block inputs
     and KV cache (a random draft: acceptance mostly 0, so every row is exercised)."""
