@@ -35,7 +35,7 @@ TREE16 = [-1, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 10, 11, 12, 13, 14]
 METRIC = "verify-step tokens/s (K=8, 1 GPU) + 2-bit gather-qmm HBM GB/s vs peak"
 TIMER_HOLD_MS = 0.020  # length of the calibration hold the library brackets (MJ_KERNEL_TIMER)
 UP_KERNEL = "void k_gather5<8, 64, 2, 8, 2, true, false, true>"  # up||gate gather, fused routing
-MOE_KERNEL = "void k_moe_fused<64, false>"  # up||gate then down in one launch
+MOE_KERNEL = "void k_moe_fused<64, false, 16>"  # up||gate then down in one launch (<= 16 rows)
 
 
 def log(*a):

@@ -65,7 +65,7 @@ void* mj_get_stream(const mj_ctx* ctx);
  * flag = 0; the next call runs normally. */
 mj_status mj_set_abort(mj_ctx* ctx, int flag);
 /* Bound of the fused MoE launch's waits (no counterpart in the reference: it has no fused
- * launch).  Passes of at most 16 rows run the up||gate and down products as one launch whose
+ * launch).  Passes of at most 32 rows run the up||gate and down products as one launch whose
  * blocks all stay resident; a block takes a down item once every up item of its expert slot has
  * completed, polling the slot's count at most `polls` times (default 131072, about 30 ms).  A
  * wait that runs out its bound -- the launch's blocks were not all resident, e.g. kernels of
@@ -388,7 +388,7 @@ float mj_model_last_pass_ms(const mj_model* model);
 #define MJ_KERNEL_DENSE 4       /* qkv and o projections */
 #define MJ_KERNEL_TIMER 5       /* the same bracket around a 20 us wall-clock hold */
 #define MJ_KERNEL_EXPERT_MOE 6  /* up||gate + SwiGLU then down, one launch (passes of at most
-                                   16 rows over at most 64 experts, H 2048, intermediate 1024) */
+                                   32 rows over at most 64 experts, H 2048, intermediate 1024) */
 mj_status mj_model_profile(mj_model* model, int enable);
 float mj_model_kernel_ms(const mj_model* model, int kernel_class, int64_t* launches);
 

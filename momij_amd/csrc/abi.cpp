@@ -467,14 +467,15 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
     // One row takes it too, so a row's result does not depend on how many rows share its pass
     // (a verify row equals the one-row decode step at its position, bit for bit).
     const bool tile = fused && M >= MJ_TILE_MIN_ROWS && M <= MJ_MAX_ROWS && up_tile && dn_tile;
-    // up to 16 rows over at most 64 experts: the up || gate product ranks the logits itself
-    // (its blocks build the slot records in LDS), one launch fewer
-    const bool topk_in_up = tile && E <= 64 && M <= MJ_G5_FUSED_ROWS;
-    // ... and then the down product in the same launch (the common expert shape)
+    // the common expert shape, up to 32 rows over at most 64 experts: one launch ranks the
+    // logits (its blocks build the slot records in LDS) and runs both products
     const bool moe_fused =
-        MJ_MOE_FUSED && topk_in_up && ms.fcnt != nullptr &&
+        MJ_MOE_FUSED && tile && E <= 64 && ms.fcnt != nullptr &&
         (w->up_gate_alpha == nullptr) == (w->down_alpha == nullptr) &&
         moe_fused_supported(H, I, E, w->gs, M, w->up_gate_alpha != nullptr);
+    // otherwise, up to 16 rows: the up || gate product still ranks the logits itself (one
+    // launch fewer than a separate top-k)
+    const bool topk_in_up = moe_fused || (tile && E <= 64 && M <= MJ_G5_FUSED_ROWS);
     if (fused) {
         RouteArgs ra{};
         ra.x = x;

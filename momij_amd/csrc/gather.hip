@@ -123,18 +123,24 @@ __device__ __forceinline__ void lds_only_barrier() {
 }
 
 // static LDS of the fused routing's slot records (persistent up || gate kernels)
-constexpr size_t G5_FUSED_REC_BYTES = 64 * (4 + 8);
+// static LDS of the routing words of a launch that ranks up to FR rows itself
+constexpr size_t g5_fused_rec_bytes(int FR) { return 64 * (4 + 8 + (FR > 16 ? 8 : 0)); }
 
 // How one call of the tile-gather body fits into a launch.  MODE 0: the whole launch (the
 // standalone kernels).  The fused MoE kernel calls the up || gate body (MODE 1) and then the down
 // body (MODE 2) in every block; io carries the routing words from the first to the second.
 struct FuseIO {
-    uint32_t em = 0;  // lane t: rows that picked expert t (bit r)
-    uint64_t er = 0;  // ... and expert t's rank in each of them (3 bits at 3r)
+    uint32_t em = 0;   // lane t: rows that picked expert t (bit r)
+    uint64_t er = 0;   // ... and expert t's rank in rows 0 .. 15 (3 bits at 3r)
+    uint64_t er1 = 0;  // ... and in rows 16 .. 31 (3 bits at 3 (r - 16))
 };
 
-template <int KPL, int GS, int EPI, int WPB, int KS, bool PER, bool ROWA, bool FUS, int MODE>
+// FR: rows the fused routing ranks at most (16: two a wave, ranks in er; 32: four a wave, rows
+// 16 .. 31's ranks in er1)
+template <int KPL, int GS, int EPI, int WPB, int KS, bool PER, bool ROWA, bool FUS, int MODE,
+          int FR = MJ_G5_FUSED_ROWS>
 __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO& io) {
+    static_assert(FR == 16 || FR == 32, "fused routing rows");
     using S = G5Shape<KPL, GS, EPI, WPB, KS>;
     constexpr int R = S::R, K = S::K, KB = S::KB, KBW = S::KBW, TPB = S::TPB, XS = S::XS;
     constexpr int SCW = S::SCW;
@@ -177,9 +183,10 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     // product.
     struct FusedRoute {
         // per expert t, set by LDS atomics as the rows are ranked: the rows that picked t (bit
-        // r) and t's rank in each (3 bits at 3r)
+        // r) and t's rank in each (3 bits at 3r for rows 0 .. 15, at 3 (r - 16) in er1 beyond)
         uint32_t em[64];
         uint64_t er[64];
+        uint64_t er1[FR > 16 ? 64 : 0];
     };
     // (an instantiation of its own, FUS: the routing code stays out of the other kernels)
     constexpr bool FUSABLE = FUS;
@@ -193,6 +200,7 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     constexpr bool RREC = FUS || MODE == 2;
     uint32_t em = MODE == 2 ? io.em : 0u;
     uint64_t er = MODE == 2 ? io.er : 0ull;
+    uint64_t er1 = MODE == 2 ? io.er1 : 0ull;
     // record of slot sl in the global records' form: pair j in lane j, expert id and pair count
     // in the high halves of lanes 0 and 1 (count 0 past the last routed expert)
     auto fused_rec = [&](int sl) -> int {
@@ -202,48 +210,55 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         if (hit == 0) return 0;
         const int ex = __builtin_ctzll(hit);
         const uint32_t rm = __builtin_amdgcn_readlane(em, ex);
-        const uint64_t rx = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(er >> 32), ex) << 32) |
-                            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)er, ex);
-        // lane r < 16 (row r) sends its pair to lane "rows of ex before r"; the lanes that
-        // send nothing send to lane 63, which no record entry uses (at most 16 pairs)
-        const int r16 = lane & 15;
-        const bool mine = lane < 16 && ((rm >> r16) & 1u);
-        const int pos = __popc(rm & ((1u << r16) - 1u));
-        const int pr = r16 * a.rk + (int)((rx >> (3 * r16)) & 7u);
+        auto rl64 = [&](uint64_t w) {
+            return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(w >> 32), ex) << 32) |
+                   (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)w, ex);
+        };
+        const uint64_t rx0 = rl64(er), rx1 = FR > 16 ? rl64(er1) : 0ull;
+        // lane r < FR (row r) sends its pair to lane "rows of ex before r"; the lanes that
+        // send nothing send to lane 63, which no record entry uses (at most FR pairs)
+        const int rr = lane & (FR - 1);
+        const bool mine = lane < FR && ((rm >> rr) & 1u);
+        const int pos = __popc(rm & ((1u << rr) - 1u));
+        const int pr = rr * a.rk + (int)(((rr < 16 ? rx0 : rx1) >> (3 * (rr & 15))) & 7u);
         const int got = __builtin_amdgcn_ds_permute((mine ? pos : 63) * 4, pr);
         return got | (lane == 0 ? ex << 16 : lane == 1 ? __popc(rm) << 16 : 0);
     };
     if constexpr (FUSABLE) {
-        static_assert(sizeof(FusedRoute) == G5_FUSED_REC_BYTES, "record bytes");
-        static_assert(MJ_G5_FUSED_ROWS <= 2 * WPB && MJ_G5_FUSED_ROWS <= 16, "two rows a wave");
+        static_assert(sizeof(FusedRoute) == g5_fused_rec_bytes(FR), "record bytes");
+        static_assert(FR <= 4 * WPB, "at most four rows a wave");
+        constexpr int RPW = (FR + WPB - 1) / WPB;  // rows a wave ranks
         if (fused) {
             const int M = a.rM, E = a.rE, k = a.rk;
             // row scratch in the weight tile area, free until the first item's loads
             float* s_row = (float*)g5lds + 64 * wv;                  // [WPB][64]
             float* s_gate = (float*)(g5lds + 256 * WPB) + 8 * wv;    // [WPB][8]
             int* s_ind = (int*)(g5lds + 288 * WPB) + 8 * wv;         // [WPB][8]
-            // both rows' logits (clamped row and expert: no branch waits) and the abort flag
-            // requested together
-            float v[2];
+            // the wave's rows' logits (clamped row and expert: no branch waits) and the abort
+            // flag requested together
+            float v[RPW];
 #pragma unroll
-            for (int sr = 0; sr < 2; ++sr)
+            for (int sr = 0; sr < RPW; ++sr)
                 v[sr] = a.rlogits[min(wv + WPB * sr, M - 1) * E + min(lane, E - 1)];
             if (aborted(a.abort)) return;
             if (wv == 0) {
                 s_fr.em[lane] = 0u;
                 s_fr.er[lane] = 0ull;
+                if constexpr (FR > 16) s_fr.er1[lane] = 0ull;
             }
             __syncthreads();  // (LDS only: the logits stay in flight)
             // expert t picked by row r at rank rk: its bits, ORed in from any wave
             auto mark = [&](int t, int r, int rk) {
                 __hip_atomic_fetch_or(&s_fr.em[t], 1u << r, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_fetch_or(&s_fr.er[t], (uint64_t)rk << (3 * r), __ATOMIC_RELAXED,
+                uint64_t* w = &s_fr.er[t];
+                if constexpr (FR > 16) w = r < 16 ? w : &s_fr.er1[t];
+                __hip_atomic_fetch_or(w, (uint64_t)rk << (3 * (r & 15)), __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_WORKGROUP);
             };
             const bool wr = blockIdx.x == gridDim.x - 1;  // writes inds / scores / records
 #pragma unroll
-            for (int sr = 0; sr < 2; ++sr) {
+            for (int sr = 0; sr < RPW; ++sr) {
                 const int r = wv + WPB * sr;
                 if (r >= M) break;
                 s_row[lane] = lane < E ? v[sr] + 0.0f : -INFINITY;
@@ -265,11 +280,12 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             }
             __syncthreads();
             // lane t: the rows that picked expert t, and its rank in each
-            static_assert(MJ_G5_FUSED_ROWS <= 16, "3-bit ranks of 16 rows in 64 bits");
             em = s_fr.em[lane];
             er = s_fr.er[lane];
+            if constexpr (FR > 16) er1 = s_fr.er1[lane];
             io.em = em;
             io.er = er;
+            io.er1 = er1;
             if (wr && wv == 0) {
                 const uint64_t on = __ballot(em != 0u);
                 const int total = __popcll(on);
@@ -278,9 +294,9 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
                     const int cnt = __popc(em);
                     int c = 0;
 #pragma unroll
-                    for (int r = 0; r < MJ_G5_FUSED_ROWS; ++r) {
+                    for (int r = 0; r < FR; ++r) {
                         if ((em >> r) & 1u) {
-                            gr[c] = (r * k + (int)((er >> (3 * r)) & 7u)) |
+                            gr[c] = (r * k + (int)(((r < 16 ? er : er1) >> (3 * (r & 15))) & 7u)) |
                                     (c == 0 ? lane << 16 : c == 1 ? cnt << 16 : 0);
                             ++c;
                         }
@@ -812,13 +828,15 @@ __global__ __launch_bounds__(WPB * 64) __attribute__((amdgpu_waves_per_eu(4))) v
 // items (blocks with fewer up items first, slots in increasing order) and stages an item's act
 // rows once every up item of its slot has completed, so the up product's last round overlaps
 // the down product, which needs no launch or record read of its own.
-template <int GS, bool ROWA>
+// FR: rows the launch ranks at most, 16 or 32 (the 32-row form ranks four rows a wave and
+// carries a second rank word, which costs a 9-row pass about 1 us).
+template <int GS, bool ROWA, int FR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_fused(
     GatherArgs up, GatherArgs dn, int ra_up, int ra_dn, int multi_up, int multi_dn) {
     FuseIO io;
-    g5_body<8, GS, EPI_SWIGLU, 8, 2, true, ROWA, true, 1>(up, ra_up, multi_up, io);
+    g5_body<8, GS, EPI_SWIGLU, 8, 2, true, ROWA, true, 1, FR>(up, ra_up, multi_up, io);
     __syncthreads();  // every wave is done with the up phase's LDS
-    g5_body<4, GS, EPI_STORE, 8, 1, true, ROWA, false, 2>(dn, ra_dn, multi_dn, io);
+    g5_body<4, GS, EPI_STORE, 8, 1, true, ROWA, false, 2, FR>(dn, ra_dn, multi_dn, io);
 }
 
 // dynamic LDS a tile-gather launch may take (the device has 160 KB per workgroup)
@@ -848,7 +866,7 @@ static hipError_t launch_g5(const GatherArgs& a, int rows, int n_buckets, hipStr
     const bool expert = a.ecnt != nullptr || a.srec != nullptr;
     // two blocks a CU for the expert products; static LDS: the pair lists (128 bytes) and, in
     // the persistent up || gate kernels, the fused routing's records
-    const size_t stat = 256 + (PER && EPI == EPI_SWIGLU ? G5_FUSED_REC_BYTES : 0);
+    const size_t stat = 256 + (PER && EPI == EPI_SWIGLU ? g5_fused_rec_bytes(MJ_G5_FUSED_ROWS) : 0);
     const size_t limit =
         (EPI == EPI_SWIGLU || EPI == EPI_STORE) && expert ? 80 * 1024 - stat : G5_LDS_MAX;
     while (RA > 1 && S::lds(RA, want > RA || PER) > limit) --RA;
@@ -941,15 +959,15 @@ hipError_t launch_gather3(const GatherArgs& a, int epi, int max_rows_per_bucket,
 }
 
 // static LDS of the fused MoE kernel: both phases' pair lists and the routing words
-constexpr size_t G5_FUSED_MOE_STAT = 256 + 256 + G5_FUSED_REC_BYTES;
+constexpr size_t g5_fused_moe_stat(int FR) { return 256 + 256 + g5_fused_rec_bytes(FR); }
 
-// rows staged a pass by the two phases, and the dynamic LDS of the launch
+// rows staged a pass by the two phases, and the dynamic LDS of the launch (the form for `rows`)
 template <int GS>
 static size_t moe_fused_lds(int rows, int& ra_up, int& ra_dn) {
     using SU = G5Shape<8, GS, EPI_SWIGLU, 8, 2>;
     using SD = G5Shape<4, GS, EPI_STORE, 8, 1>;
     const int want = rows < 1 ? 1 : rows;
-    const size_t limit = 80 * 1024 - G5_FUSED_MOE_STAT;  // two blocks a CU
+    const size_t limit = 80 * 1024 - g5_fused_moe_stat(want <= 16 ? 16 : 32);  // two blocks a CU
     ra_up = want < 16 ? want : 16;
     ra_dn = ra_up;
     while (ra_up > 1 && SU::lds(ra_up, true) > limit) --ra_up;
@@ -957,16 +975,20 @@ static size_t moe_fused_lds(int rows, int& ra_up, int& ra_dn) {
     return std::max(SU::lds(ra_up, true), SD::lds(ra_dn, true));
 }
 
-// every block of the launch resident at once: two a CU at the largest footprint (16 rows)
+// every block of the launch resident at once: two a CU at the largest footprint (32 rows),
+// for both forms
 template <int GS, bool ROWA>
 static bool moe_fused_resident() {
     static int ok = -1;
     if (ok < 0) {
-        int ra_up = 0, ra_dn = 0, n = 0;
-        const size_t lds = moe_fused_lds<GS>(MJ_G5_FUSED_ROWS, ra_up, ra_dn);
-        ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_moe_fused<GS, ROWA>, 512, lds) ==
-                     hipSuccess &&
-             n >= 2;
+        int ra_up = 0, ra_dn = 0, n16 = 0, n32 = 0;
+        const size_t lds16 = moe_fused_lds<GS>(16, ra_up, ra_dn);
+        const size_t lds32 = moe_fused_lds<GS>(MJ_MOE_FUSED_ROWS, ra_up, ra_dn);
+        ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n16, k_moe_fused<GS, ROWA, 16>, 512,
+                                                          lds16) == hipSuccess &&
+             hipOccupancyMaxActiveBlocksPerMultiprocessor(&n32, k_moe_fused<GS, ROWA, 32>, 512,
+                                                          lds32) == hipSuccess &&
+             n16 >= 2 && n32 >= 2;
     }
     return ok == 1;
 }
@@ -980,14 +1002,18 @@ static hipError_t launch_moe_fused_t(GatherArgs up, GatherArgs dn, int rows, hip
     up.fup_ncb = up.N / (16 * SU::TPB);
     dn.fup_ncb = up.fup_ncb;
     dn.fcnt = up.fcnt;
-    launch_timed(k_moe_fused<GS, ROWA>, dim3(persistent_blocks()), dim3(512), lds, st, up, dn,
-                 ra_up, ra_dn, (int)(want > ra_up), (int)(want > ra_dn));
+    if (want <= 16)
+        launch_timed(k_moe_fused<GS, ROWA, 16>, dim3(persistent_blocks()), dim3(512), lds, st, up,
+                     dn, ra_up, ra_dn, (int)(want > ra_up), (int)(want > ra_dn));
+    else
+        launch_timed(k_moe_fused<GS, ROWA, 32>, dim3(persistent_blocks()), dim3(512), lds, st, up,
+                     dn, ra_up, ra_dn, (int)(want > ra_up), (int)(want > ra_dn));
     return hipGetLastError();
 }
 
 bool moe_fused_supported(int H, int I, int E, int gs, int M, bool rowa) {
     if (!(H == 2048 && I == 1024 && E <= 64 && (gs == 64 || gs == 128) && M >= 1 &&
-          M <= MJ_G5_FUSED_ROWS))
+          M <= MJ_MOE_FUSED_ROWS))
         return false;
     if (gs == 64) return rowa ? moe_fused_resident<64, true>() : moe_fused_resident<64, false>();
     return rowa ? moe_fused_resident<128, true>() : moe_fused_resident<128, false>();
@@ -1034,11 +1060,15 @@ hipError_t set_gather3_attributes() {
     // the fused MoE kernels
     {
         int ra_up = 0, ra_dn = 0;
-        const int lds = (int)std::min(std::max(moe_fused_lds<64>(MJ_G5_FUSED_ROWS, ra_up, ra_dn),
-                                               moe_fused_lds<128>(MJ_G5_FUSED_ROWS, ra_up, ra_dn)),
-                                      G5_LDS_MAX);
-        const void* ks[] = {(const void*)k_moe_fused<64, false>, (const void*)k_moe_fused<64, true>,
-                            (const void*)k_moe_fused<128, false>, (const void*)k_moe_fused<128, true>};
+        size_t most = 0;
+        for (int rows : {16, MJ_MOE_FUSED_ROWS})
+            most = std::max({most, moe_fused_lds<64>(rows, ra_up, ra_dn),
+                             moe_fused_lds<128>(rows, ra_up, ra_dn)});
+        const int lds = (int)std::min(most, G5_LDS_MAX);
+        const void* ks[] = {(const void*)k_moe_fused<64, false, 16>, (const void*)k_moe_fused<64, true, 16>,
+                            (const void*)k_moe_fused<128, false, 16>, (const void*)k_moe_fused<128, true, 16>,
+                            (const void*)k_moe_fused<64, false, 32>, (const void*)k_moe_fused<64, true, 32>,
+                            (const void*)k_moe_fused<128, false, 32>, (const void*)k_moe_fused<128, true, 32>};
         for (const void* k : ks)
             if (e == hipSuccess) e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     }

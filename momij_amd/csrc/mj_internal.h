@@ -126,7 +126,8 @@ struct GatherArgs {
     int fpolls;   // bound of a down item's wait, in polls of its slot's count
     int* ffault;  // set (system scope) by a wait that ran out its bound (nullable)
 };
-#define MJ_G5_FUSED_ROWS 16
+#define MJ_G5_FUSED_ROWS 16  // rows the standalone up || gate gather ranks itself
+#define MJ_MOE_FUSED_ROWS 32  // rows the fused MoE launch ranks itself
 #define MJ_FCNT 64  // slot counters of the fused MoE launch
 #define MJ_FCNT_STRIDE 32  // ints between two counters: one 128-byte line each (the atomics of
                            // different slots do not queue on one line)

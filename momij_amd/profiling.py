@@ -170,7 +170,7 @@ def main():
     ap.add_argument("kind", choices=["trace", "counters", "traffic", "multi"])
     ap.add_argument("csv")
     ap.add_argument("csv2", nargs="?")
-    ap.add_argument("--kernel", default="void k_moe_fused<64, false>")
+    ap.add_argument("--kernel", default="void k_moe_fused<64, false, 16>")
     ap.add_argument("--copy-mb", type=int, default=512)
     ap.add_argument("--out", default=None)
     ap.add_argument("--rows", type=int, default=9)

@@ -110,7 +110,8 @@ def _moe_dev(mw):
     return d
 
 
-@pytest.mark.parametrize("M,flags", [(1, 0), (8, 0), (8, 3), (1, 3), (9, 3), (16, 3), (17, 3)])
+@pytest.mark.parametrize("M,flags", [(1, 0), (8, 0), (8, 3), (1, 3), (9, 3), (16, 3), (17, 3),
+                                     (32, 3), (33, 3)])
 def test_moe_block(ctx, orc, M, flags):
     """Config 1 (M=1) and the K=8 verify rows of config 2 (M=8), and the pre-norm+residual form
     used inside a layer: routing bit-exact, outputs within tolerance.  Up to 16 rows the up ||
@@ -137,20 +138,21 @@ def test_moe_block(ctx, orc, M, flags):
     assert rel < 5e-3
 
 
-@pytest.mark.parametrize("M", [1, 9, 16])
+@pytest.mark.parametrize("M", [1, 9, 16, 17, 32])
 def test_moe_fused_routing_equals_separate_topk(ctx, M):
-    """Passes of at most 16 rows rank the router logits in the up gather's prologue (every block
-    builds the slot records in LDS); 17 rows take the separate top-k launch.  A row's routing
-    and output do not depend on the other rows of its pass, so an M-row pass equals the first M
-    rows of a 17-row pass bit for bit: expert ids, weights and outputs."""
+    """Passes of at most 32 rows rank the router logits in the fused MoE launch's prologue
+    (every block builds the slot records in LDS; four rows a wave past 16) and run both expert
+    products in that one launch; 33 rows take the separate top-k, up and down launches.  A
+    row's routing and output do not depend on the other rows of its pass, so an M-row pass
+    equals the first M rows of a 33-row pass bit for bit: expert ids, weights and outputs."""
     import torch
 
-    print(f"case: moe fused routing M={M} vs 17 rows", flush=True)
+    print(f"case: moe fused routing M={M} vs 33 rows", flush=True)
     rng = np.random.default_rng(500 + M)
     E, H, I, gs, k = 64, 2048, 1024, 64, 8
     mw = _moe_data(rng, E, H, I, gs)
     dmw = _moe_dev(mw)
-    x = synth.normal_f16(rng, (17, H))
+    x = synth.normal_f16(rng, (33, H))
 
     def run(rows):
         dx = dev(np.ascontiguousarray(x[:rows]))
@@ -160,11 +162,11 @@ def test_moe_fused_routing_equals_separate_topk(ctx, M):
         _run(ctx, lambda: ctx.moe_block(dmw, dx, y, rows, 3, inds, scores))
         return host(y), host(inds), host(scores)
 
-    y17, i17, s17 = run(17)
+    y33, i33, s33 = run(33)
     ym, im, sm = run(M)
-    assert (im == i17[:M]).all()
-    assert (sm.view(np.uint32) == s17[:M].view(np.uint32)).all()
-    diff = ym.view(np.uint16) != y17[:M].view(np.uint16)
+    assert (im == i33[:M]).all()
+    assert (sm.view(np.uint32) == s33[:M].view(np.uint32)).all()
+    diff = ym.view(np.uint16) != y33[:M].view(np.uint16)
     assert not diff.any(), f"rows differing: {np.nonzero(diff.any(axis=1))[0].tolist()}"
 
 
@@ -279,7 +281,8 @@ def test_moe_block_all_rows_on_each_expert(ctx, orc, M):
     assert rel < 5e-3
 
 
-@pytest.mark.parametrize("E,I,M", [(64, 1024, 9), (64, 1024, 64), (128, 1024, 17), (40, 1024, 5)])
+@pytest.mark.parametrize("E,I,M", [(64, 1024, 9), (64, 1024, 64), (128, 1024, 17), (40, 1024, 5),
+                                   (64, 1024, 27)])
 def test_moe_routing_ties(ctx, orc, E, I, M):
     """Router rows repeated in pairs, so every logit is tied with another expert's: the lower
     index has to rank first, exactly as in the oracle (ties reach the exact comparison rule of
