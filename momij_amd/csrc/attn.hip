@@ -158,7 +158,10 @@ __device__ __forceinline__ int rope_f0(int d0) {
 __host__ __device__ inline int tab_floats2(int M, int half) {
     return ((M * half / 2 + 63) / 64) * 64 * 2;
 }
-template <int HALF>  // rope_dim / 2 (0: no RoPE)
+// HALF: rope_dim / 2 (0: no RoPE).  JR: finishing jobs (8 a vector) a thread requests before the
+// first barrier; jobs past 256 JR go in further rounds, each a dependent load round trip, so
+// passes with more vectors (a 17-row tree: 680 jobs) take JR = 3 and one round.
+template <int HALF, int JR>
 __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int g = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
@@ -249,7 +252,6 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
                      : (M - (c - cg.n_abs) * AK < AK ? M - (c - cg.n_abs) * AK : AK);
     }
     const int njobs = 8 * (nqv + ko1 - ko0);
-    constexpr int JR = 2;  // jobs a thread loads before the first barrier (more: in a loop)
     u4v jxa[JR], jxb[JR];
     auto job_src = [&](int j, int& pa) -> const uint16_t* {
         const int vi = j >> 3, jb = j & 7;
@@ -572,11 +574,16 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
     const size_t lds = (size_t)(nqt * 16 * QSTR + AK * QSTR + HD * VSTR) * 2 +
                        (size_t)tab_floats2(a.M, a.rope_dim / 2) * 8 + AK * 4 + MJ_ROWS * (4 + 8) +
                        2 * HD * 2 + 16;
+    // finishing jobs of the block that also holds the pass's own keys
+    const bool jr3 = 8 * (a.M * gqa + (a.M < AK ? a.M : AK)) > 256 * 2;
+    auto go = [&](auto k2, auto k3) {
+        launch_timed(jr3 ? k3 : k2, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a);
+    };
     switch (a.rope_dim) {
-        case 0: launch_timed(k_attn_chunk<0>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
-        case 32: launch_timed(k_attn_chunk<16>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
-        case 64: launch_timed(k_attn_chunk<32>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
-        default: launch_timed(k_attn_chunk<64>, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a); break;
+        case 0: go(k_attn_chunk<0, 2>, k_attn_chunk<0, 3>); break;
+        case 32: go(k_attn_chunk<16, 2>, k_attn_chunk<16, 3>); break;
+        case 64: go(k_attn_chunk<32, 2>, k_attn_chunk<32, 3>); break;
+        default: go(k_attn_chunk<64, 2>, k_attn_chunk<64, 3>); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -586,8 +593,10 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
 
 hipError_t set_attn_attributes() {
     hipError_t e = hipSuccess;
-    const void* ks[] = {(const void*)k_attn_chunk<0>, (const void*)k_attn_chunk<16>,
-                        (const void*)k_attn_chunk<32>, (const void*)k_attn_chunk<64>};
+    const void* ks[] = {(const void*)k_attn_chunk<0, 2>,  (const void*)k_attn_chunk<16, 2>,
+                        (const void*)k_attn_chunk<32, 2>, (const void*)k_attn_chunk<64, 2>,
+                        (const void*)k_attn_chunk<0, 3>,  (const void*)k_attn_chunk<16, 3>,
+                        (const void*)k_attn_chunk<32, 3>, (const void*)k_attn_chunk<64, 3>};
     for (const void* k : ks)
         if (e == hipSuccess)
             e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
