@@ -161,9 +161,16 @@ __host__ __device__ inline int tab_floats2(int M, int half) {
 // HALF: rope_dim / 2 (0: no RoPE).  JR: finishing jobs (8 a vector) a thread requests before the
 // first barrier; jobs past 256 JR go in further rounds, each a dependent load round trip, so
 // passes with more vectors (a 17-row tree: 680 jobs) take JR = 3 and one round.
-template <int HALF, int JR>
-__global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
+// NT: threads of a block, 256 or 512.  The K / V staging takes threads 0 .. 255; a pass of more
+// than four query tiles (a 17-row tree: five) runs 512 threads, so that no wave takes two tiles
+// and the finishing jobs spread over twice the threads.
+template <int HALF, int JR, int NT>
+__global__ __launch_bounds__(NT) void k_attn_chunk(AttnArgs a) {
+    static_assert(NT == 256 || NT == 512, "block size");
+    constexpr int NW = NT / 64;  // waves
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const bool kvt = NT == 256 || t < 256;  // stages K / V (wave-uniform)
+    const int tk = t & 255;
     const int g = blockIdx.x / a.max_chunks, c = blockIdx.x % a.max_chunks;
     const StepDesc* sd = a.sd;
     const int64_t L = sd->L;
@@ -211,15 +218,15 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     uint16_t* knw_s = qnw_s + HD;                  // [HD] k norm weights
     int* s_abort = (int*)(knw_s + HD);
 
-    // ---- K: key kk = t / 4, dims 32 dq ..
-    const int kk = t >> 2, dq = t & 3;
+    // ---- K: key kk = tk / 4, dims 32 dq ..
+    const int kk = tk >> 2, dq = tk & 3;
     int64_t kp;
     const int kcls = key_of(kk, kp);
     const bool kvalid = kcls != -2;
     const bool kown = kcls >= 0;
     const int ar = kown ? kcls : 0;  // pass row of an own key
     u4v kv[4];
-    {
+    if (kvt) {
         const int64_t slot = kvalid && !kown ? slot_of(kp) : 0;
         const uint16_t* ks = kown ? a.qkv + (size_t)ar * qkvN + (a.nQ + g) * HD + 32 * dq
                                   : a.kc + ((size_t)g * a.C + slot) * HD + 32 * dq;
@@ -227,7 +234,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
         for (int q = 0; q < 4; ++q) kv[q] = *(const u4v*)(ks + 8 * q);
     }
     // ---- V: keys 4 vg .. 4 vg + 3, dims 8 vd ..
-    const int vg = t & 15, vd = t >> 4;
+    const int vg = tk & 15, vd = tk >> 4;
     u4v vv[4];
     int vcls[4];
 #pragma unroll
@@ -238,7 +245,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
         const uint16_t* vs =
             vcls[j] >= 0 ? a.qkv + (size_t)vcls[j] * qkvN + (a.nQ + a.nKV + g) * HD + 8 * vd
                          : a.vc + ((size_t)g * a.C + slot) * HD + 8 * vd;
-        vv[j] = *(const u4v*)vs;
+        if (kvt) vv[j] = *(const u4v*)vs;
     }
     // ---- vectors to finish (RMSNorm + RoPE): the block's queries (vector qv = r * gqa + j is
     // head g * gqa + j of row r) and the pass's own keys in this chunk (lanes ko0 .. ko1 - 1).
@@ -264,7 +271,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     };
 #pragma unroll
     for (int jj = 0; jj < JR; ++jj) {
-        const int j = t + 256 * jj;
+        const int j = t + NT * jj;
         int pa;
         const uint16_t* src = job_src(j < njobs ? j : njobs - 1, pa);
         jxa[jj] = *(const u4v*)(src + 8 * pa);
@@ -281,7 +288,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     // the table goes straight into LDS (16 bytes a lane): pairs 2e, 2e + 1 of the [M][half]
     // angles, wave w taking pairs 64 w + lane, 64 (w + 4) + lane, ...
     const int ntab4 = M * half / 2, hd = half > 0 ? half : 1;
-    for (int e0 = 64 * wv; e0 < ntab4; e0 += 256) {
+    for (int e0 = 64 * wv; e0 < ntab4; e0 += NT) {
         const int e = e0 + lane;
         if (e < ntab4)
             __builtin_amdgcn_global_load_lds(a.rope_cs + (2 * e / hd) * MJ_ROPE_F + 2 * e % hd,
@@ -296,12 +303,12 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
 
     // ---- LDS: K rows (own keys raw for now), V^T, the table, metadata; the padding query
     // rows of the last tile (read by the MFMAs, masked after) are cleared
-    for (int i = nqv * 16 + t; i < nqt * 16 * 16; i += 256)
+    for (int i = nqv * 16 + t; i < nqt * 16 * 16; i += NT)
         *(u4v*)(Qs + (i >> 4) * QSTR + 8 * (i & 15)) = (u4v){0u, 0u, 0u, 0u};
+    if (kvt) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        *(u4v*)(Ks + kk * QSTR + 32 * dq + 8 * q) = kvalid ? kv[q] : (u4v){0u, 0u, 0u, 0u};
-    {
+        for (int q = 0; q < 4; ++q)
+            *(u4v*)(Ks + kk * QSTR + 32 * dq + 8 * q) = kvalid ? kv[q] : (u4v){0u, 0u, 0u, 0u};
         u4v w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) w[j] = vcls[j] != -2 ? vv[j] : (u4v){0u, 0u, 0u, 0u};
@@ -331,10 +338,10 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
     // d + half (maple_qk_norm_rope); queries into Qs, own keys into Ks and appended at slot
     // (L + r) % C with their V rows (maple_write_kv_pair).  No other block of this launch
     // reads those slots (the committed window never reaches them).
-    for (int j0 = 0; j0 < njobs; j0 += 256 * JR) {
+    for (int j0 = 0; j0 < njobs; j0 += NT * JR) {
 #pragma unroll
         for (int jj = 0; jj < JR; ++jj) {
-            const int j = j0 + t + 256 * jj;
+            const int j = j0 + t + NT * jj;
             if (j0 > 0) {
                 int pa;
                 const uint16_t* src = job_src(j < njobs ? j : njobs - 1, pa);
@@ -394,7 +401,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
             }
         }
     }
-    if (own_chunk) {
+    if (own_chunk && kvt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if (vcls[j] >= 0)
@@ -407,9 +414,9 @@ __global__ __launch_bounds__(256) void k_attn_chunk(AttnArgs a) {
 
     const float sc2 = a.scale * LOG2E;
     const int ln = lane & 15, lq = lane >> 4;
-    const int iters = (nqt + 3) / 4;
+    const int iters = (nqt + NW - 1) / NW;
     for (int it = 0; it < iters; ++it) {
-        const int qt = wv + 4 * it;
+        const int qt = wv + NW * it;
         if (qt >= nqt) break;  // wave-uniform; no block barrier follows
         // S^T tiles: keys 16 kt + 4 lq + r against query vector 16 qt + ln
         u4v qb[4];
@@ -574,16 +581,23 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
     const size_t lds = (size_t)(nqt * 16 * QSTR + AK * QSTR + HD * VSTR) * 2 +
                        (size_t)tab_floats2(a.M, a.rope_dim / 2) * 8 + AK * 4 + MJ_ROWS * (4 + 8) +
                        2 * HD * 2 + 16;
-    // finishing jobs of the block that also holds the pass's own keys
-    const bool jr3 = 8 * (a.M * gqa + (a.M < AK ? a.M : AK)) > 256 * 2;
-    auto go = [&](auto k2, auto k3) {
-        launch_timed(jr3 ? k3 : k2, dim3(a.nKV * a.max_chunks), dim3(256), lds, st, a);
+    // finishing jobs of the block that also holds the pass's own keys; more than four query
+    // tiles take 512-thread blocks (two jobs a thread then cover up to 1024)
+    const int jobs = 8 * (a.M * gqa + (a.M < AK ? a.M : AK));
+    const bool wide = nqt > 4;
+    const bool jr3 = jobs > 256 * 2;
+    auto go = [&](auto k2, auto k3, auto w2) {
+        const dim3 grid(a.nKV * a.max_chunks);
+        if (wide)
+            launch_timed(w2, grid, dim3(512), lds, st, a);
+        else
+            launch_timed(jr3 ? k3 : k2, grid, dim3(256), lds, st, a);
     };
     switch (a.rope_dim) {
-        case 0: go(k_attn_chunk<0, 2>, k_attn_chunk<0, 3>); break;
-        case 32: go(k_attn_chunk<16, 2>, k_attn_chunk<16, 3>); break;
-        case 64: go(k_attn_chunk<32, 2>, k_attn_chunk<32, 3>); break;
-        default: go(k_attn_chunk<64, 2>, k_attn_chunk<64, 3>); break;
+        case 0: go(k_attn_chunk<0, 2, 256>, k_attn_chunk<0, 3, 256>, k_attn_chunk<0, 2, 512>); break;
+        case 32: go(k_attn_chunk<16, 2, 256>, k_attn_chunk<16, 3, 256>, k_attn_chunk<16, 2, 512>); break;
+        case 64: go(k_attn_chunk<32, 2, 256>, k_attn_chunk<32, 3, 256>, k_attn_chunk<32, 2, 512>); break;
+        default: go(k_attn_chunk<64, 2, 256>, k_attn_chunk<64, 3, 256>, k_attn_chunk<64, 2, 512>); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -593,10 +607,12 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t st) {
 
 hipError_t set_attn_attributes() {
     hipError_t e = hipSuccess;
-    const void* ks[] = {(const void*)k_attn_chunk<0, 2>,  (const void*)k_attn_chunk<16, 2>,
-                        (const void*)k_attn_chunk<32, 2>, (const void*)k_attn_chunk<64, 2>,
-                        (const void*)k_attn_chunk<0, 3>,  (const void*)k_attn_chunk<16, 3>,
-                        (const void*)k_attn_chunk<32, 3>, (const void*)k_attn_chunk<64, 3>};
+    const void* ks[] = {(const void*)k_attn_chunk<0, 2, 256>,  (const void*)k_attn_chunk<16, 2, 256>,
+                        (const void*)k_attn_chunk<32, 2, 256>, (const void*)k_attn_chunk<64, 2, 256>,
+                        (const void*)k_attn_chunk<0, 3, 256>,  (const void*)k_attn_chunk<16, 3, 256>,
+                        (const void*)k_attn_chunk<32, 3, 256>, (const void*)k_attn_chunk<64, 3, 256>,
+                        (const void*)k_attn_chunk<0, 2, 512>,  (const void*)k_attn_chunk<16, 2, 512>,
+                        (const void*)k_attn_chunk<32, 2, 512>, (const void*)k_attn_chunk<64, 2, 512>};
     for (const void* k : ks)
         if (e == hipSuccess)
             e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);

@@ -22,7 +22,7 @@ TREE16 = [-1, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 10, 11, 12, 13, 14]  # 16 nodes, 
 
 
 @pytest.mark.parametrize("case", ["cfg2_chain", "ring_wrap", "tree16", "rope128", "full_attn",
-                                  "early_window"])
+                                  "early_window", "ring_shared_chunk", "ring_tree16"])
 def test_attn_block(ctx, orc, case):
     import torch
 
@@ -34,6 +34,12 @@ def test_attn_block(ctx, orc, case):
     L, parents = 4096, list(range(-1, 8))  # K=8 chain -> 9 rows ([y] + 8 drafts)
     if case == "ring_wrap":
         cfg["C"], L = 1024 + 64, 5000
+    elif case == "ring_shared_chunk":
+        # the window's first keys and the pass's last rows sit in one 64-slot chunk of the ring
+        # (the 56 unused slots between them: (L + 8) % C = 194 = 3 * 64 + 2)
+        cfg["C"], L = 1024 + 64, 4538
+    elif case == "ring_tree16":
+        cfg["C"], L, parents = 1024 + 64, 4538, TREE16
     elif case == "tree16":
         parents = TREE16
     elif case == "rope128":
