@@ -66,13 +66,14 @@ void* mj_get_stream(const mj_ctx* ctx);
 mj_status mj_set_abort(mj_ctx* ctx, int flag);
 /* Bound of the fused MoE launch's waits (no counterpart in the reference: it has no fused
  * launch).  Passes of at most 32 rows run the up||gate and down products as one launch whose
- * blocks all stay resident; a block takes a down item once every up item of its expert slot has
- * completed, polling the slot's count at most `polls` times (default 131072, about 30 ms).  A
- * wait that runs out its bound -- the launch's blocks were not all resident, e.g. kernels of
- * another stream held CUs -- sets the context's fault word, and the next synchronising call
- * reports MJ_HIP_ERROR (the results since the previous one are invalid) and clears it.
- * polls = 0 forces that report whenever a slot is not complete at its first check.  A pass
- * replayed from a graph keeps the bound it was captured with. */
+ * blocks all stay resident; a down item computes once the act rows it stages hold no value the
+ * up product has yet to write, staging them again at most `polls` times (default 131072, each
+ * after a short sleep: well under a second).  A wait that runs out its bound -- the launch's
+ * blocks were not all resident, e.g. kernels of another stream held CUs -- sets the context's
+ * fault word, and the next synchronising call reports MJ_HIP_ERROR (the results since the
+ * previous one are invalid) and clears it.  polls = 0 forces that report whenever a down item's
+ * rows are not complete at its first check.  A pass replayed from a graph keeps the bound it
+ * was captured with. */
 mj_status mj_set_wait_limit(mj_ctx* ctx, int polls);
 /* One wait for everything queued (cb.commit + waitUntilCompleted,
  * SeedlessDecodeEngine.swift:324-325).  Reports MJ_ABORTED if the abort word is set or was set

@@ -427,7 +427,6 @@ void moe_scratch_layout(Arena& a, int H, int I, int E, int k, int M, MoeScratch&
     ms.ecnt = (int*)a.take((size_t)E * 4);
     ms.eplist = (int*)a.take((size_t)E * MJ_MAX_ROWS * 4);
     ms.srec = (int*)a.take((size_t)64 * 64 * 4);
-    ms.fcnt = (int*)a.take((size_t)MJ_FCNT * MJ_FCNT_STRIDE * 4);
 }
 
 mj_status moe_scratch(mj_ctx* ctx, int H, int I, int E, int k, int M, MoeScratch& ms) {
@@ -470,7 +469,7 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
     // the common expert shape, up to 32 rows over at most 64 experts: one launch ranks the
     // logits (its blocks build the slot records in LDS) and runs both products
     const bool moe_fused =
-        MJ_MOE_FUSED && tile && E <= 64 && ms.fcnt != nullptr &&
+        MJ_MOE_FUSED && tile && E <= 64 &&
         (w->up_gate_alpha == nullptr) == (w->down_alpha == nullptr) &&
         moe_fused_supported(H, I, E, w->gs, M, w->up_gate_alpha != nullptr);
     // otherwise, up to 16 rows: the up || gate product still ranks the logits itself (one
@@ -496,7 +495,8 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
         ra.k = k;
         ra.eps = w->eps;
         ra.abort = ab;
-        ra.fcnt = moe_fused ? ms.fcnt : nullptr;
+        ra.act_mark = moe_fused ? ms.act : nullptr;
+        ra.act_n16 = moe_fused ? M * k * I / 8 : 0;
         s = mj_hip(ctx, launch_route_logits(ra, H, st), "route");
         if (s != MJ_OK) return s;
         if (!topk_in_up) {
@@ -598,7 +598,6 @@ mj_status run_moe(mj_ctx* ctx, const mj_moe_weights* w, const uint16_t* x, uint1
             up.rscores = scores;
             up.rsrec = ms.srec;
         }
-        up.fcnt = moe_fused ? ms.fcnt : nullptr;
         if (!moe_fused) {
             if (prof) prof->begin(PROF_UP, st);
             s = mj_hip(ctx, launch_gather(up, EPI_SWIGLU, M, tile ? E : nb, st), "up gather");

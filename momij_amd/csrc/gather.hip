@@ -472,47 +472,41 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     // reduction and epilogue; the item's rows are staged after the block is done with the old
     // ones, so the item starts once everything it issued has landed
     bool early = false;
-    // fused MoE launch.  Up phase: an item's act rows are stored device-coherent (sc1); once
-    // every wave's stores of it have completed (the next barrier that waits for them) one
-    // thread counts it in fcnt[slot].  Down phase: a wave stages an item's rows only when the
-    // slot's count is complete (a bounded wait: the launch is sized so that every block is
-    // resident, two a CU, and then the counts complete; a wait that runs out its bound sets
-    // the fault word, which the host reports, and goes on, so the launch always ends)
-    int sig_slot = -1;
-    bool next_ready = true;  // down phase: the next item's slot count was complete
-    auto signal_done = [&]() {
-        if constexpr (MODE == 1) {
-            if (tid == 0 && sig_slot >= 0)
-                __hip_atomic_fetch_add(a.fcnt + sig_slot * MJ_FCNT_STRIDE, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            sig_slot = -1;
+    // Fused MoE launch.  Up phase: an item's act values are stored device-coherent (sc1) into
+    // act rows that the router launch filled with the marker 0xFFFF (a NaN, which the clamped
+    // SwiGLU never produces: both its inputs are clamped to [-7, 7] first).  Down phase: an
+    // item stages its rows at once and, once they have landed, checks them for the marker; rows
+    // still marked are staged again.  The wait is bounded: the launch is sized so that every
+    // block is resident, two a CU, and then every up item completes; a wait that runs out its
+    // bound sets the fault word, which the host reports, and goes on, so the launch always ends.
+    __shared__ int s_mark[WPB];
+    // a half of the pass's staged rows still holds the marker (the same answer in every thread)
+    auto rows_marked = [&](int npass) -> bool {
+        const uint16_t* xs = xs_of(buf);
+        bool bad = false;
+        for (int idx = tid; idx < npass * (K / 8); idx += NT) {
+            const int r = idx / (K / 8), c = idx - r * (K / 8);
+            const u4v v = *(const u4v*)(xs + r * XS + 8 * c);
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                bad |= (v[w] & 0xFFFFu) == 0xFFFFu || (v[w] >> 16) == 0xFFFFu;
         }
-    };
-    auto slot_ready = [&](int sl) -> bool {
-        return __hip_atomic_load(a.fcnt + sl * MJ_FCNT_STRIDE, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) >=
-               a.fup_ncb;
-    };
-    auto wait_slot = [&](int sl) {
-        bool ok = slot_ready(sl);
-        for (int it = 0; !ok && it < a.fpolls; ++it) {
-            if ((it & 63) == 63 && aborted(a.abort)) return;
-            __builtin_amdgcn_s_sleep(8);
-            ok = slot_ready(sl);
-        }
-        if (!ok && a.ffault != nullptr && lane == 0)
-            __hip_atomic_store(a.ffault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const bool wbad = __ballot(bad) != 0ull;
+        if (lane == 0) s_mark[wv] = wbad ? 1 : 0;
+        lds_only_barrier();
+        int any = 0;
+#pragma unroll
+        for (int w = 0; w < WPB; ++w) any |= s_mark[w];
+        return any != 0;
     };
 
   for (;;) {
     const int npass0 = min(RA, np);
     if (!early) {
         if constexpr (MODE == 2) {
-            // the weights do not depend on the up phase: requested first, the rows once the
-            // slot is complete (the count, requested before the weights, is waited for alone)
-            const bool ready = slot_ready(item / ncb);
+            // the weights do not depend on the up phase: requested first, then the rows, checked
+            // for the marker once they have landed
             issue_weights(e, cb);
-            if (!ready) wait_slot(item / ncb);
             stage_load(0, npass0, buf, lpair, np, true);
             early = true;  // everything issued lands before the first pass
         } else {
@@ -540,8 +534,21 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             lds_barrier<G + NSB>();
         else
             lds_barrier<0>();
-        // (every wave's stores of the previous item have completed: the barrier waits for them)
-        if (pb == 0) signal_done();
+        if constexpr (MODE == 2) {
+            // act rows an up item has not finished yet: staged again until they have
+            for (int it = 0; rows_marked(npass); ++it) {
+                if (it >= a.fpolls) {
+                    if (a.ffault != nullptr && tid == 0)
+                        __hip_atomic_store(a.ffault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    break;
+                }
+                if ((it & 63) == 63 && aborted(a.abort)) break;
+                lds_only_barrier();  // every wave has read the marks before they are rewritten
+                __builtin_amdgcn_s_sleep(8);
+                stage_load(pb, npass, buf, lpair, np);
+                lds_barrier<0>();
+            }
+        }
         if (own_sums) {
             own_block_sums(npass);
             lds_barrier<G + NSB>();
@@ -550,18 +557,13 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         // vector load younger than them: PF).  With fused routing the record is formed from
         // registers once the weights have landed; the load is then a stand-in that keeps the
         // queue's count, and its value is consumed (times zero) so that it stays
-        constexpr int PF = PER ? 1 : 0;
-        if constexpr (PER) {
+        // (the down phase of the fused launch forms every record from registers: no load)
+        constexpr int PF = PER && MODE != 2 ? 1 : 0;
+        if constexpr (PER && MODE != 2) {
             if (pb == 0) {
-                if constexpr (MODE == 2) {
-                    // the next item's slot count (device-coherent), for its rows below
-                    rec_n = __hip_atomic_load(a.fcnt + min((item + (int)gridDim.x) / ncb, MJ_FCNT - 1) * MJ_FCNT_STRIDE,
-                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else {
-                    const int* rp = fused ? (const int*)a.rlogits
-                                          : a.srec + min((item + (int)gridDim.x) / ncb, 63) * MJ_ROWS + lane;
-                    rec_n = *rp;
-                }
+                const int* rp = fused ? (const int*)a.rlogits
+                                      : a.srec + min((item + (int)gridDim.x) / ncb, 63) * MJ_ROWS + lane;
+                rec_n = *rp;
             }
         }
         wait_vmcnt<G + PF>();      // scales and biases have landed
@@ -694,8 +696,6 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         if constexpr (PER) {
             const int nx = item + (int)gridDim.x;
             if constexpr (MODE == 2) {
-                // the first pass holds the count (a later pass of the item finds the record)
-                if (pb == 0) next_ready = __builtin_amdgcn_readfirstlane(rec_n) >= a.fup_ncb;
                 rec_n = fused_rec(min(nx / ncb, 63));
             } else if (fused)
                 rec_n = fused_rec(min(nx / ncb, 63)) | (rec_n & (int)opaque(0u));
@@ -729,9 +729,6 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             if (stage_next) {
                 // every wave has read its rows (the K-slice barrier, or this one)
                 if constexpr (KS == 1) lds_only_barrier();
-                if constexpr (MODE == 2) {
-                    if (!next_ready) wait_slot((item + (int)gridDim.x) / ncb);
-                }
                 stage_load(0, min(RA, np_next), buf ^ 1, rec_n & 0xFFFF, np_next);
             }
         }
@@ -797,7 +794,6 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         run_pass(std::integral_constant<int, 4>{}, pb, npass);
     }
     if constexpr (!PER) break;
-    if constexpr (MODE == 1) sig_slot = item / ncb;  // counted once its stores have completed
     item += gridDim.x;
     if (item / ncb >= 64) break;
     np = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
@@ -807,10 +803,6 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
     lpair = rec_n & 0xFFFF;
     buf ^= 1;
     early = true;
-  }
-  if constexpr (MODE == 1) {
-      lds_barrier<0>();  // every wave's stores of the last item have completed
-      signal_done();
   }
 }
 
@@ -1001,7 +993,6 @@ static hipError_t launch_moe_fused_t(GatherArgs up, GatherArgs dn, int rows, hip
     const size_t lds = moe_fused_lds<GS>(rows, ra_up, ra_dn);
     up.fup_ncb = up.N / (16 * SU::TPB);
     dn.fup_ncb = up.fup_ncb;
-    dn.fcnt = up.fcnt;
     if (want <= 16)
         launch_timed(k_moe_fused<GS, ROWA, 16>, dim3(persistent_blocks()), dim3(512), lds, st, up,
                      dn, ra_up, ra_dn, (int)(want > ra_up), (int)(want > ra_dn));
@@ -1022,7 +1013,7 @@ bool moe_fused_supported(int H, int I, int E, int gs, int M, bool rowa) {
 hipError_t launch_moe_fused(const GatherArgs& up, const GatherArgs& dn, int rows, hipStream_t st) {
     const bool rowa = up.alpha != nullptr;
     if (!moe_fused_supported(up.K, dn.K, up.rE, up.gs, up.rM, rowa) || up.N != 2 * dn.K ||
-        dn.N != up.K || up.rlogits == nullptr || up.fcnt == nullptr || up.srec == nullptr ||
+        dn.N != up.K || up.rlogits == nullptr || up.srec == nullptr ||
         dn.srec == nullptr)
         return hipErrorInvalidValue;
     if (up.gs == 64)

@@ -59,7 +59,6 @@ struct MoeScratch {
     int* ecnt;           // pairs per expert [E]
     int* eplist;         // pair lists per expert [E][MJ_ROWS]
     int* srec;           // routed-expert slot records [64][64] (E <= 64)
-    int* fcnt;           // slot counters of the fused MoE launch [MJ_FCNT][MJ_FCNT_STRIDE]
     bool want_plain = false;  // also write the normed rows plain into xn (debug capture)
 };
 

@@ -118,19 +118,15 @@ struct GatherArgs {
     int32_t* rinds;
     float* rscores;
     int* rsrec;
-    // fused MoE launch (up || gate then down in one kernel): fcnt[s] counts the finished up
-    // items of routed-expert slot s (zeroed by the router-logits launch before it); a down item
-    // of slot s starts once fcnt[s] reaches fup_ncb, the up product's column blocks
-    int* fcnt;
+    // fused MoE launch (up || gate then down in one kernel): the up product's column blocks,
+    // and the bound of a down item's wait for act rows still holding the router launch's
+    // marker, in re-stagings of its rows
     int fup_ncb;
-    int fpolls;   // bound of a down item's wait, in polls of its slot's count
+    int fpolls;
     int* ffault;  // set (system scope) by a wait that ran out its bound (nullable)
 };
 #define MJ_G5_FUSED_ROWS 16  // rows the standalone up || gate gather ranks itself
 #define MJ_MOE_FUSED_ROWS 32  // rows the fused MoE launch ranks itself
-#define MJ_FCNT 64  // slot counters of the fused MoE launch
-#define MJ_FCNT_STRIDE 32  // ints between two counters: one 128-byte line each (the atomics of
-                           // different slots do not queue on one line)
 
 struct QmvArgs {
     const uint16_t* x;      // plain fp16 [rows_x][K]
@@ -310,8 +306,8 @@ struct RouteArgs {
     int M, E, k;
     float eps;
     const int* abort;
-    int* fcnt;               // slot counters of the fused MoE launch that follows (nullable):
-                             // zeroed here, before that launch reads them
+    uint16_t* act_mark;      // act rows of the fused MoE launch that follows (nullable): every
+    int act_n16;             // 16-byte chunk of them set to the marker 0xFFFF here, before it
 };
 bool route_supported(int H, int E, int k);
 hipError_t launch_route_logits(const RouteArgs& a, int H, hipStream_t st);

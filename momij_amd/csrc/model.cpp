@@ -516,7 +516,6 @@ mj_status mj_model_create(mj_ctx* ctx, const mj_model_config* cfg, const mj_laye
         ms.ecnt = (int*)a.take((size_t)c.E * 4);
         ms.eplist = (int*)a.take((size_t)c.E * MJ_MAX_ROWS * 4);
         ms.srec = (int*)a.take((size_t)64 * 64 * 4);
-        ms.fcnt = (int*)a.take((size_t)MJ_FCNT * MJ_FCNT_STRIDE * 4);
     };
     Arena count;
     layout(count);

@@ -422,7 +422,9 @@ __global__ __launch_bounds__(256) void k_route_logits(RouteArgs a) {
         }
     }
     *(u4v*)(xn + 8 * tid) = xv;
-    if (a.fcnt && blockIdx.x == 0 && tid < MJ_FCNT) a.fcnt[tid * MJ_FCNT_STRIDE] = 0;
+    // the fused MoE launch's act rows: the "not yet written" marker, before that launch starts
+    for (int i = blockIdx.x * 256 + tid; i < a.act_n16; i += gridDim.x * 256)
+        ((u4v*)a.act_mark)[i] = (u4v){~0u, ~0u, ~0u, ~0u};
     if (grp == 0) {
         if (a.xn) *(u4v*)(a.xn + (size_t)r * RT_H + 8 * tid) = xv;
         if (a.xperm)

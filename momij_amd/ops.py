@@ -57,7 +57,8 @@ class Context:
         self.check(self.lib.mj_set_abort(self.h, int(flag)))
 
     def set_wait_limit(self, polls: int):
-        """Bound of the fused MoE launch's waits for its up product, in polls."""
+        """Bound of the fused MoE launch's waits for its up product, in re-stagings of a
+        down item's act rows."""
         self.check(self.lib.mj_set_wait_limit(self.h, int(polls)))
 
     # ---------------------------------------------------------------- ops

@@ -422,9 +422,10 @@ def test_graph_replays_equal_eager(model):
 
 def test_fused_moe_wait_bound_reported(model):
     """The fused MoE launch's waits for its up product: one that runs out its bound is reported
-    by the synchronising call (MJ_HIP_ERROR) and the report is cleared.  With no polls allowed,
-    a pass either finds every slot complete at its first check, and then equals the normal pass,
-    or fails with that report; the normal pass after it is unaffected."""
+    by the synchronising call (MJ_HIP_ERROR) and the report is cleared.  With no re-staging
+    allowed, a pass either finds every down item's act rows complete at its first check, and
+    then equals the normal pass, or fails with that report; the normal pass after it is
+    unaffected."""
     from momij_amd._lib import MomijError
 
     eng, cfg, ctx = model["eng"], model["cfg"], model["ctx"]
