@@ -428,7 +428,8 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
 
     // ---- a wave's weight tile, coalesced into LDS: scales and biases, then the code groups
     const int I = a.N / 2;
-    auto issue_weights = [&](int ee, int cbb) {
+    // scales (when `scales`) and code column groups j0 .. j1-1 of the tile
+    auto issue_weights = [&](int ee, int cbb, bool scales = true, int j0 = 0, int j1 = S::KBW / 4) {
         auto tile_row = [&](int r) -> size_t {  // global row of tile row r
             if constexpr (EPI == EPI_SWIGLU) {
                 const int j0 = (cbb * TPB + tt) * 8;
@@ -438,7 +439,8 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             }
         };
         __builtin_amdgcn_sched_barrier(0);  // loads issued before stay ahead in the vmcnt queue
-        if constexpr (ROWA) {
+        if (!scales) {
+        } else if constexpr (ROWA) {
             // row-alpha weights: one alpha per row (scale alpha, bias -alpha in every group);
             // tile rows 0..7 and 8..15 are each 8 consecutive rows, 16 bytes
             if (lane < 2) load_lds16((const char*)a.alpha + tile_row(8 * lane) * 2, wsc);
@@ -463,6 +465,7 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         const int r = lane >> 2, B4 = (lane & 3) ^ (r >> 2);
 #pragma unroll
         for (int j = 0; j < KBW / 4; ++j)  // column group j: blocks kh*KBW + 4j .. +3
+            if (j >= j0 && j < j1)
             load_lds16(wg + tile_row(r) * (K / 4) + 16 * (kh * KBW + 4 * j + B4),
                        wcode + 1024 * j);
         __builtin_amdgcn_sched_barrier(0);
@@ -629,10 +632,30 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         // row-alpha weights: every block has scale alpha, so the MFMA sums chain over the whole
         // slice and alpha scales them once
         f4 dacc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};  // even / odd blocks
+        // persistent mode, last pass of the item: the next item (its record, and whether there
+        // is one) and its weights.  In the fused launch (records formed from registers) the
+        // scales and first half of the code groups are requested once this item's first half
+        // is done (its scales are in registers, its first half's codes read), the rest after
+        // its MFMAs; the item waits for its own groups first, so later waits count nothing new
+        constexpr bool SPLIT = PER && (MODE == 1 || MODE == 2) && G >= 2;
+        bool stage_next = false;
+        int np_next = 0;
+        auto next_item = [&]() {
+            if constexpr (PER) {
+                const int nx = item + (int)gridDim.x;
+                if constexpr (MODE == 2) {
+                    rec_n = fused_rec(min(nx / ncb, 63));
+                } else if (fused)
+                    rec_n = fused_rec(min(nx / ncb, 63)) | (rec_n & (int)opaque(0u));
+                np_next = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
+                stage_next = pb + RA >= np && nx / ncb < 64 && np_next > 0;
+            }
+        };
         // sum_B s_B * (sum q x)_B: per 64-block f16 MFMA sums, scaled in fp32, one column group
         // at a time as its codes arrive
 #pragma unroll
         for (int j = 0; j < G; ++j) {
+          if (!(SPLIT && j >= G / 2 && stage_next)) {
             if (j == 0) wait_vmcnt<G - 1 + PF>();
             if (j == 1) wait_vmcnt<(G >= 2 ? G - 2 : 0) + PF>();
             if (j == 2) wait_vmcnt<(G >= 3 ? G - 3 : 0) + PF>();
@@ -641,6 +664,7 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             if (j == 5) wait_vmcnt<(G >= 6 ? G - 6 : 0) + PF>();
             if (j == 6) wait_vmcnt<(G >= 7 ? G - 7 : 0) + PF>();
             if (j == 7) wait_vmcnt<PF>();
+          }
             __builtin_amdgcn_sched_barrier(0);
             // LDS operands two blocks at a time (2 code words, 4 activation fragments), both
             // blocks' requested before the first is used
@@ -684,24 +708,29 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
             }
 #pragma unroll
             for (int r = 0; r < NR; ++r) pin(acc[r]);
+            if constexpr (SPLIT) {
+                if (j == G / 2 - 1) {
+                    next_item();
+                    if (stage_next) {
+                        wait_vmcnt<0>();  // this item's remaining groups have landed
+                        issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16,
+                                      (item + (int)gridDim.x) % ncb, true, 0, G / 2);
+                    }
+                }
+            }
         }
         if constexpr (ROWA) {
 #pragma unroll
             for (int r = 0; r < NR; ++r) acc[r] += alpha_n * (dacc[0][r] + dacc[1][r]);
         }
         // persistent mode, last pass of the item: this wave's tile is free, start the next
-        // item's weights; its rows follow once every wave is done with the current ones
-        bool stage_next = false;
-        int np_next = 0;
+        // item's weights (the rest of them, split); its rows follow once every wave is done
+        // with the current ones
         if constexpr (PER) {
-            const int nx = item + (int)gridDim.x;
-            if constexpr (MODE == 2) {
-                rec_n = fused_rec(min(nx / ncb, 63));
-            } else if (fused)
-                rec_n = fused_rec(min(nx / ncb, 63)) | (rec_n & (int)opaque(0u));
-            np_next = __builtin_amdgcn_readlane(rec_n, 1) >> 16;
-            stage_next = pb + RA >= np && nx / ncb < 64 && np_next > 0;
-            if (stage_next) issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16, nx % ncb);
+            if constexpr (!SPLIT) next_item();
+            if (stage_next)
+                issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16,
+                              (item + (int)gridDim.x) % ncb, !SPLIT, SPLIT ? G / 2 : 0, G);
         }
         if constexpr (KS > 1) {
             // K-slices of a tile meet in LDS (a slice's partial goes into its own wave's tile
