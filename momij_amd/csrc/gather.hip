@@ -638,6 +638,7 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         // is done (its scales are in registers, its first half's codes read), the rest after
         // its MFMAs; the item waits for its own groups first, so later waits count nothing new
         constexpr bool SPLIT = PER && (MODE == 1 || MODE == 2) && G >= 2;
+        constexpr int GP = G / 2;  // code groups a part (four parts measured slower)
         bool stage_next = false;
         int np_next = 0;
         auto next_item = [&]() {
@@ -655,7 +656,7 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         // at a time as its codes arrive
 #pragma unroll
         for (int j = 0; j < G; ++j) {
-          if (!(SPLIT && j >= G / 2 && stage_next)) {
+          if (!(SPLIT && j >= GP && stage_next)) {
             if (j == 0) wait_vmcnt<G - 1 + PF>();
             if (j == 1) wait_vmcnt<(G >= 2 ? G - 2 : 0) + PF>();
             if (j == 2) wait_vmcnt<(G >= 3 ? G - 3 : 0) + PF>();
@@ -709,13 +710,14 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
 #pragma unroll
             for (int r = 0; r < NR; ++r) pin(acc[r]);
             if constexpr (SPLIT) {
-                if (j == G / 2 - 1) {
-                    next_item();
-                    if (stage_next) {
-                        wait_vmcnt<0>();  // this item's remaining groups have landed
-                        issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16,
-                                      (item + (int)gridDim.x) % ncb, true, 0, G / 2);
+                if ((j + 1) % GP == 0) {
+                    if (j + 1 == GP) {
+                        next_item();
+                        if (stage_next) wait_vmcnt<0>();  // this item's remaining groups have landed
                     }
+                    if (stage_next)
+                        issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16,
+                                      (item + (int)gridDim.x) % ncb, j + 1 == GP, j + 1 - GP, j + 1);
                 }
             }
         }
@@ -727,10 +729,11 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         // item's weights (the rest of them, split); its rows follow once every wave is done
         // with the current ones
         if constexpr (PER) {
-            if constexpr (!SPLIT) next_item();
-            if (stage_next)
-                issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16,
-                              (item + (int)gridDim.x) % ncb, !SPLIT, SPLIT ? G / 2 : 0, G);
+            if constexpr (!SPLIT) {
+                next_item();
+                if (stage_next)
+                    issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16, (item + (int)gridDim.x) % ncb);
+            }
         }
         if constexpr (KS > 1) {
             // K-slices of a tile meet in LDS (a slice's partial goes into its own wave's tile
