@@ -654,6 +654,11 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         };
         // sum_B s_B * (sum q x)_B: per 64-block f16 MFMA sums, scaled in fp32, one column group
         // at a time as its codes arrive
+        // fused launch: the wave computes at raised priority (s_setprio, the issue arbiter's
+        // order among the CU's ready waves), so a wave whose tile has landed gets through its
+        // groups, and to its next item's requests, ahead of waves still on the unpack of
+        // theirs (launch 31.2 -> 30.1 us; through the epilogue as well: 30.4 us)
+        if constexpr (SPLIT) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < G; ++j) {
           if (!(SPLIT && j >= GP && stage_next)) {
@@ -718,6 +723,7 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
                     if (stage_next)
                         issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16,
                                       (item + (int)gridDim.x) % ncb, j + 1 == GP, j + 1 - GP, j + 1);
+                    if (j + 1 == G) __builtin_amdgcn_s_setprio(0);
                 }
             }
         }
