@@ -657,7 +657,8 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
         // fused launch: the wave computes at raised priority (s_setprio, the issue arbiter's
         // order among the CU's ready waves), so a wave whose tile has landed gets through its
         // groups, and to its next item's requests, ahead of waves still on the unpack of
-        // theirs (launch 31.2 -> 30.1 us; through the epilogue as well: 30.4 us)
+        // theirs (launch 31.2 -> 30.1 us; through the epilogue as well: 30.4 us; a second
+        // level for the second half: step 1.552 -> 1.548 ms)
         if constexpr (SPLIT) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < G; ++j) {
@@ -723,7 +724,12 @@ __device__ __forceinline__ void g5_body(GatherArgs a, int RA, int multi, FuseIO&
                     if (stage_next)
                         issue_weights(__builtin_amdgcn_readlane(rec_n, 0) >> 16,
                                       (item + (int)gridDim.x) % ncb, j + 1 == GP, j + 1 - GP, j + 1);
-                    if (j + 1 == G) __builtin_amdgcn_s_setprio(0);
+                    // priority 2 once the next item's first part is out (those waves are
+                    // nearest their last requests), 0 after the last group
+                    if (j + 1 == G)
+                        __builtin_amdgcn_s_setprio(0);
+                    else
+                        __builtin_amdgcn_s_setprio(2);
                 }
             }
         }
